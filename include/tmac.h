@@ -1,0 +1,196 @@
+/*
+ * tmac.h — C ABI of the TitanMAC sparse hot path for MI355X (gfx950).
+ *
+ * Two operations live behind this boundary:
+ *   - the Block-ELL block-sparse GEMM (forward Y = X·W, dX = dY·Wᵀ, and the
+ *     dW SDDMM restricted to W's non-zero blocks), which replaces the dense
+ *     nn.Linear calls of the TitanMAC MLP;
+ *   - windowed + persistent-token attention computed tile-sparsely, which
+ *     replaces the masked F.scaled_dot_product_attention call of
+ *     WindowedAttention.
+ *
+ * The reference (bigwolfeman/TitanMAC-Standalone) is pure Python and has no
+ * FFI of its own; each entry point below cites the reference call it stands in
+ * for. Paths are relative to the reference checkout.
+ *
+ * Conventions
+ *   - Every pointer named d_* is a device pointer owned by the caller. The
+ *     library never allocates, frees or synchronises the device.
+ *   - Every pointer named h_* is a host pointer.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *   - Return value: 0 on success, a negative tmac_status on an argument error
+ *     (nothing was launched), a positive hipError_t if a launch failed.
+ *   - Strides and leading dimensions are in elements, not bytes.
+ *   - Block-ELL layout (block size bs = 64):
+ *       W has logical shape [K, N]; n_brow = K/64 block-rows, n_bcol = N/64
+ *       block-columns. Each block-row r keeps `width` non-zero blocks whose
+ *       block-column indices col_idx[r*width + s] are strictly increasing.
+ *       vals[(r*width + s)*4096 + kk*64 + nn] = W[64*r + kk][64*col_idx[r][s] + nn]
+ *       (each block row-major in W's own orientation).
+ */
+#ifndef TMAC_H
+#define TMAC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMAC_ABI_VERSION 1
+#define TMAC_BLOCK 64
+
+typedef enum {
+  TMAC_OK = 0,
+  TMAC_ERR_NULL = -1,      /* a required pointer is NULL */
+  TMAC_ERR_SHAPE = -2,     /* a size is non-positive, not a multiple of 64, or inconsistent */
+  TMAC_ERR_INDEX = -3,     /* a Block-ELL index is out of range, duplicated or unsorted */
+  TMAC_ERR_DTYPE = -4,     /* unsupported dtype code */
+  TMAC_ERR_ALIGN = -5,     /* a pointer or stride breaks the 16-byte vector-load alignment */
+  TMAC_ERR_WORKSPACE = -6, /* workspace missing or smaller than required */
+  TMAC_ERR_CAPACITY = -7,  /* an output array is too small */
+  TMAC_ERR_VALUE = -8      /* an argument value is outside its domain (reference raises ValueError) */
+} tmac_status;
+
+typedef enum { TMAC_F32 = 0, TMAC_BF16 = 1, TMAC_F16 = 2 } tmac_dtype;
+
+/* Epilogue of the forward GEMM (fused into the store). */
+typedef enum { TMAC_EPI_NONE = 0, TMAC_EPI_GELU = 1 } tmac_epilogue;
+
+/* Attention masking pattern. */
+typedef enum {
+  TMAC_PATTERN_BAND = 0,    /* build_band_mask: attn/windowed_attention.py:97-152 */
+  TMAC_PATTERN_BLOCKWIN = 1 /* BlockSparseAttention: attn/block_sparse_attention.py:277-334 */
+} tmac_pattern;
+
+/* Human-readable text for a return code (negative tmac_status or positive hipError_t). */
+const char* tmac_status_string(int code);
+
+/* ABI version compiled into the library (TMAC_ABI_VERSION). */
+int tmac_abi_version(void);
+
+/* ------------------------------------------------------------------------- */
+/* Block-ELL index construction (host).                                       */
+/* The reference has no Block-ELL code; its MLP is dense nn.Linear             */
+/* (blocks/mlp.py:36,39). These build the sparsity pattern that replaces it.   */
+/* ------------------------------------------------------------------------- */
+
+/* Seeded sampler: for each block-row, in order, draw `width` distinct
+ * block-columns by a partial Fisher-Yates shuffle driven by one splitmix64
+ * stream started at `seed` (unbiased bounded draws by rejection), then sort the
+ * row ascending. h_col_idx has n_brow*width entries. */
+int tmac_bell_sample_col_idx(uint64_t seed, int n_brow, int n_bcol, int width,
+                             int32_t* h_col_idx);
+
+/* Check every index is in [0, n_bcol) and each row is strictly increasing. */
+int tmac_bell_validate(const int32_t* h_col_idx, int n_brow, int n_bcol, int width);
+
+/* Transposed (block-column-major) index used by the forward gather:
+ * for block-column c, entries e in [t_ptr[c], t_ptr[c+1]) list the block-rows
+ * t_row[e] (ascending) holding a non-zero block in column c, and
+ * t_vblk[e] = t_row[e]*width + slot, the block's index into vals.
+ * h_order receives the block-columns sorted by entry count, descending, ties by
+ * column ascending (the forward kernel's longest-first schedule).
+ * Sizes: t_ptr n_bcol+1, t_row and t_vblk n_brow*width, order n_bcol. */
+int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int width,
+                        int32_t* h_t_ptr, int32_t* h_t_row, int32_t* h_t_vblk,
+                        int32_t* h_order);
+
+/* ------------------------------------------------------------------------- */
+/* Block-ELL kernels (device).                                                */
+/* ------------------------------------------------------------------------- */
+
+/* Forward: Y[M, N] = epilogue(X[M, K] · W + bias), fp32 accumulation.
+ * Replaces the dense `self.fc1(x)` / `self.fc2(hidden)` calls of
+ * MLPBlock.forward (blocks/mlp.py:58,64; bias from nn.Linear, :36,39) and, with
+ * epi = TMAC_EPI_GELU, also the erf GELU between them (blocks/mlp.py:42,61).
+ * X, Y row-major with leading dimensions ldx, ldy; bias (nullable) has N
+ * entries of the same dtype. dtype: TMAC_BF16 or TMAC_F16.
+ * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary.
+ * t_ptr/t_row/t_vblk/order: device copies of tmac_bell_transpose's output. */
+int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
+                  const int32_t* d_t_ptr, const int32_t* d_t_row,
+                  const int32_t* d_t_vblk, const int32_t* d_order,
+                  const void* d_bias, void* d_Y, int64_t ldy,
+                  int M, int n_brow, int n_bcol, int width,
+                  int dtype, int epi, void* stream);
+
+/* Input gradient: dX[M, K] = dY[M, N] · Wᵀ, fp32 accumulation.
+ * Replaces autograd's grad_input of F.linear in the MLP backward
+ * (loss.backward() at train_titanmac_nested.py:462 through blocks/mlp.py:58,64).
+ * For block-row r: dX[:, 64r:64r+64] = Σ_s dY[:, 64·col_idx[r][s] + :] · W[r,s]ᵀ.
+ * d_col_idx: device copy of the row-major index. */
+int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
+                 const int32_t* d_col_idx, void* d_dX, int64_t lddx,
+                 int M, int n_brow, int n_bcol, int width, int dtype, void* stream);
+
+/* Bytes of device workspace tmac_bell_sddmm needs for these sizes. */
+int tmac_bell_sddmm_workspace(int M, int n_brow, int n_bcol, int width,
+                              size_t* ws_bytes);
+
+/* Weight gradient on the non-zero blocks only (SDDMM):
+ * dvals[r][s][kk][nn] = Σ_m X[m][64r+kk] · dY[m][64·col_idx[r][s]+nn].
+ * Replaces autograd's grad_weight = dYᵀ·X of F.linear (blocks/mlp.py:58,64),
+ * restricted to the Block-ELL pattern. The M reduction is split across
+ * workgroups and summed in a fixed order, so results are deterministic.
+ * dvals_dtype: TMAC_F32, TMAC_BF16 or TMAC_F16 (inputs: TMAC_BF16 or TMAC_F16). */
+int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, int64_t lddy,
+                    const int32_t* d_col_idx, void* d_dvals, int dvals_dtype,
+                    void* d_ws, size_t ws_bytes,
+                    int M, int n_brow, int n_bcol, int width, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Windowed attention (host tile maps + device kernel).                       */
+/* ------------------------------------------------------------------------- */
+
+/* Per-tile classification of the attention mask: kind[qt*n_kt + kt] is
+ * 0 (no allowed pair), 1 (every pair allowed) or 2 (some allowed) for the
+ * tq × tk tile (qt, kt); positions at or beyond S count as masked.
+ * The mask is build_band_mask (attn/windowed_attention.py:97-152) for
+ * TMAC_PATTERN_BAND and the effective mask of BlockSparseAttention
+ * (attn/block_sparse_attention.py:277-334, block size `block_size`) for
+ * TMAC_PATTERN_BLOCKWIN. Raises TMAC_ERR_VALUE where build_band_mask raises
+ * ValueError (n_persistent >= S, window < 0). */
+int tmac_wattn_tile_kinds(int S, int window, int n_persistent, int causal,
+                          int pattern, int block_size, int tq, int tk,
+                          uint8_t* h_kind);
+
+/* Work list of the attention kernel: for query block qb (q_block rows),
+ * entries e in [row_ptr[qb], row_ptr[qb+1]) name every 64-wide key tile with at
+ * least one allowed pair for the block, ascending. entries[e] & 0xffff is the
+ * key-tile index; bits 16+2j..17+2j hold the kind (0/1/2 as above) of the
+ * j-th `sub_rows`-row slice of the block against that tile.
+ * q_block must be a multiple of sub_rows and q_block/sub_rows <= 8.
+ * With h_entries == NULL only *n_entries is computed. */
+int tmac_wattn_schedule(int S, int window, int n_persistent, int causal,
+                        int pattern, int block_size, int q_block, int sub_rows,
+                        int32_t* h_row_ptr, int32_t* h_entries, int capacity,
+                        int* n_entries);
+
+/* Attention forward: O = softmax(Q·Kᵀ·scale + mask)·V over the allowed pairs
+ * only, fp32 accumulation and online softmax. Replaces
+ * F.scaled_dot_product_attention(q, k, v, attn_mask=additive band mask,
+ * is_causal=False) in WindowedAttention.forward
+ * (attn/windowed_attention.py:306-323), including the per-call mask
+ * conversion (:311-315).
+ * Q, K, V, O: [B, H, S, dh] addressed by strides (batch, head, seq) in
+ * elements, last dimension contiguous, so the chunked views of the fused qkv
+ * projection (:295-304) are taken without a copy. dh must be 64.
+ * lse (nullable): fp32 [B, H, S], natural-log log-sum-exp of each row.
+ * row_ptr/entries: device copies of tmac_wattn_schedule's output built with
+ * q_block = 128, sub_rows = 32.
+ * dtype: TMAC_BF16 / TMAC_F16 (MFMA path) or TMAC_F32 (fp32 FMA path). */
+int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
+                   const void* d_K, const int64_t k_strides[3],
+                   const void* d_V, const int64_t v_strides[3],
+                   void* d_O, const int64_t o_strides[3], float* d_lse,
+                   int B, int H, int S, int dh, int window, int n_persistent,
+                   int causal, int pattern, int block_size, float scale,
+                   const int32_t* d_row_ptr, const int32_t* d_entries,
+                   int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TMAC_H */

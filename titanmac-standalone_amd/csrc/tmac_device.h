@@ -1,0 +1,125 @@
+// Device-side building blocks shared by the gfx950 kernels: vector types, the
+// 32x32x16 MFMA wrappers, LDS transpose reads and conversions.
+//
+// Lane layouts of v_mfma_f32_32x32x16_{bf16,f16} (wave64, h = lane / 32):
+//   A operand (32 x 16):  lane holds A[lane % 32][8h + t], t = 0..7
+//   B operand (16 x 32):  lane holds B[8h + t][lane % 32], t = 0..7
+//   C/D (32 x 32, fp32):  lane holds C[8(j/4) + 4h + j%4][lane % 32], j = 0..15
+//
+// ds_read_b64_tr_b16 (gfx950): inside each group of 16 lanes, lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes 4j + i/4, j = 0..3.
+// Pointing lane i' of the group at row (r0 + i'/4), column (c0 + 4*(i'%4)) of a
+// row-major 16-bit tile therefore hands lane i the column (c0 + i) entries of
+// rows r0..r0+3: a 4x16 tile read transposed.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tmac.h"
+
+namespace tmac {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// Row pitch of every 64-wide 16-bit tile staged in LDS: 64 elements plus 8 of
+// padding (144 bytes), so eight consecutive rows start in eight different
+// 16-byte bank groups and both the row reads (16 B per lane over 32 rows) and
+// the transpose reads (8 rows x 64 B) proceed without bank conflicts.
+constexpr int kPitch = 72;
+constexpr int kTileElems = 64 * kPitch;  // one 64x64 tile, in 16-bit elements
+
+template <int DT>
+struct Mfma;
+
+template <>
+struct Mfma<TMAC_BF16> {
+  static __device__ __forceinline__ f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<__bf16>(x));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+};
+
+template <>
+struct Mfma<TMAC_F16> {
+  static __device__ __forceinline__ f32x16 run(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, static_cast<_Float16>(x));
+  }
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+};
+
+// Eight 16-bit values of column (c0 + lane%16 of the 16-lane group) from rows
+// r0..r0+7 of a row-major LDS tile with pitch kPitch, as one MFMA operand:
+// two transpose reads, rows r0..r0+3 then r0+4..r0+7. The caller passes the
+// tile base offset by the lane's own group (r0 row, c0 column already chosen).
+__device__ __forceinline__ u32x4 lds_read_tr8(const uint16_t* tile, int r0, int c0, int lane) {
+  const int i = lane & 15;
+  const uint16_t* p = tile + (r0 + (i >> 2)) * kPitch + c0 + 4 * (i & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p + 4 * kPitch));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
+}
+
+// Same as lds_read_tr8 but the two 4-row groups are independent
+// (rows r0..r0+3 and r1..r1+3).
+__device__ __forceinline__ u32x4 lds_read_tr4x2(const uint16_t* tile, int r0, int r1, int c0,
+                                                int lane) {
+  const int i = lane & 15;
+  const uint16_t* p0 = tile + (r0 + (i >> 2)) * kPitch + c0 + 4 * (i & 3);
+  const uint16_t* p1 = tile + (r1 + (i >> 2)) * kPitch + c0 + 4 * (i & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
+}
+
+__device__ __forceinline__ u32x4 ldg16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void stg16(uint16_t* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+__device__ __forceinline__ u32x4 lds16(const uint16_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void sts16(uint16_t* p, u32x4 v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// Workgroup id remapped so that consecutive logical ids run on the same XCD:
+// the hardware hands workgroup b to XCD b % 8, so logical = (b % 8) * per_xcd +
+// b / 8 keeps each XCD on one contiguous slice of the logical work order (and
+// its L2 on one slice of the data). Grids are padded to 8 * per_xcd.
+__device__ __forceinline__ int xcd_logical_id(int per_xcd) {
+  const int b = blockIdx.x;
+  return (b & 7) * per_xcd + (b >> 3);
+}
+
+__device__ __forceinline__ float gelu_erf(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+}  // namespace tmac

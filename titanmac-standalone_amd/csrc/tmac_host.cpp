@@ -1,0 +1,261 @@
+// Host-side index construction for the TitanMAC sparse hot path: Block-ELL
+// sampling / validation / transposition and the attention tile maps.
+// Everything here is plain integer work on host memory; the results are copied
+// to the device once per pattern by the caller and cached.
+
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "../../include/tmac.h"
+
+extern "C" int tmac_abi_version(void) { return TMAC_ABI_VERSION; }
+
+extern "C" const char* tmac_status_string(int code) {
+  switch (code) {
+    case TMAC_OK: return "ok";
+    case TMAC_ERR_NULL: return "a required pointer is NULL";
+    case TMAC_ERR_SHAPE: return "invalid or inconsistent shape";
+    case TMAC_ERR_INDEX: return "Block-ELL index out of range, duplicated or unsorted";
+    case TMAC_ERR_DTYPE: return "unsupported dtype";
+    case TMAC_ERR_ALIGN: return "pointer or stride not 16-byte aligned for vector loads";
+    case TMAC_ERR_WORKSPACE: return "workspace missing or too small";
+    case TMAC_ERR_CAPACITY: return "output array too small";
+    case TMAC_ERR_VALUE: return "argument value outside its domain";
+    default: break;
+  }
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown tmac status";
+}
+
+// ---------------------------------------------------------------------------
+// Block-ELL index
+// ---------------------------------------------------------------------------
+
+namespace {
+
+// splitmix64 (Steele, Lea, Flood 2014; public-domain reference by S. Vigna).
+struct SplitMix64 {
+  uint64_t s;
+  uint64_t next() {
+    s += 0x9E3779B97F4A7C15ull;
+    uint64_t z = s;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+  }
+  // Uniform integer in [0, n), n >= 1: reject draws below 2^64 mod n so every
+  // residue class has the same number of accepted values.
+  uint64_t bounded(uint64_t n) {
+    const uint64_t threshold = (0ull - n) % n;
+    for (;;) {
+      const uint64_t x = next();
+      if (x >= threshold) return x % n;
+    }
+  }
+};
+
+}  // namespace
+
+extern "C" int tmac_bell_sample_col_idx(uint64_t seed, int n_brow, int n_bcol, int width,
+                                        int32_t* h_col_idx) {
+  if (!h_col_idx) return TMAC_ERR_NULL;
+  if (n_brow <= 0 || n_bcol <= 0 || width <= 0 || width > n_bcol) return TMAC_ERR_SHAPE;
+  SplitMix64 rng{seed};
+  std::vector<int32_t> perm(n_bcol);
+  for (int r = 0; r < n_brow; ++r) {
+    for (int c = 0; c < n_bcol; ++c) perm[c] = c;
+    for (int i = 0; i < width; ++i) {
+      const int j = i + static_cast<int>(rng.bounded(static_cast<uint64_t>(n_bcol - i)));
+      std::swap(perm[i], perm[j]);
+    }
+    int32_t* row = h_col_idx + static_cast<size_t>(r) * width;
+    std::copy(perm.begin(), perm.begin() + width, row);
+    std::sort(row, row + width);
+  }
+  return TMAC_OK;
+}
+
+extern "C" int tmac_bell_validate(const int32_t* h_col_idx, int n_brow, int n_bcol, int width) {
+  if (!h_col_idx) return TMAC_ERR_NULL;
+  if (n_brow <= 0 || n_bcol <= 0 || width <= 0 || width > n_bcol) return TMAC_ERR_SHAPE;
+  for (int r = 0; r < n_brow; ++r) {
+    const int32_t* row = h_col_idx + static_cast<size_t>(r) * width;
+    for (int s = 0; s < width; ++s) {
+      if (row[s] < 0 || row[s] >= n_bcol) return TMAC_ERR_INDEX;
+      if (s > 0 && row[s] <= row[s - 1]) return TMAC_ERR_INDEX;
+    }
+  }
+  return TMAC_OK;
+}
+
+extern "C" int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int width,
+                                   int32_t* h_t_ptr, int32_t* h_t_row, int32_t* h_t_vblk,
+                                   int32_t* h_order) {
+  if (!h_t_ptr || !h_t_row || !h_t_vblk || !h_order) return TMAC_ERR_NULL;
+  const int st = tmac_bell_validate(h_col_idx, n_brow, n_bcol, width);
+  if (st != TMAC_OK) return st;
+  std::vector<int32_t> count(n_bcol, 0);
+  for (int e = 0; e < n_brow * width; ++e) ++count[h_col_idx[e]];
+  h_t_ptr[0] = 0;
+  for (int c = 0; c < n_bcol; ++c) h_t_ptr[c + 1] = h_t_ptr[c] + count[c];
+  std::vector<int32_t> fill(h_t_ptr, h_t_ptr + n_bcol);
+  // Rows ascending, so every column's list comes out ordered by block-row.
+  for (int r = 0; r < n_brow; ++r) {
+    for (int s = 0; s < width; ++s) {
+      const int c = h_col_idx[r * width + s];
+      const int e = fill[c]++;
+      h_t_row[e] = r;
+      h_t_vblk[e] = r * width + s;
+    }
+  }
+  for (int c = 0; c < n_bcol; ++c) h_order[c] = c;
+  std::stable_sort(h_order, h_order + n_bcol,
+                   [&](int32_t a, int32_t b) { return count[a] > count[b]; });
+  return TMAC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Attention tile maps
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct RowSpan {
+  // Allowed key columns of one query row: [0, a_end) ∪ [b_lo, b_hi).
+  int a_end;
+  int b_lo, b_hi;
+};
+
+// Allowed key set of row i, written as at most two half-open intervals.
+// Band (attn/windowed_attention.py:97-152):
+//   persistent rows (i < Np) see the persistent columns only (:115-132);
+//   sequence rows see the persistent columns (:118) and, among sequence
+//   columns, |i - j| <= w (:136-141) intersected with j <= i when causal (:144-150).
+// Blockwin (attn/block_sparse_attention.py:277-334), r = i - Np, b0 = bs*floor(r/bs):
+//   persistent rows see every key (:277-285);
+//   sequence rows see the persistent keys (:305) and sequence keys c = j - Np in
+//   [max(0, b0 - w), r] when causal (:299-301, :156-161), or
+//   [max(0, b0 - w), min(b0 + bs, S - Np)) when not (:299-300, causal_mask=None).
+RowSpan row_span(int i, int S, int w, int Np, bool causal, int pattern, int bs) {
+  RowSpan sp{Np, 0, 0};
+  if (i < Np) {
+    if (pattern == TMAC_PATTERN_BLOCKWIN) sp.a_end = S;
+    return sp;
+  }
+  if (pattern == TMAC_PATTERN_BAND) {
+    const long lo = std::max<long>(Np, static_cast<long>(i) - w);
+    const long hi = causal ? static_cast<long>(i) + 1
+                           : std::min<long>(S, static_cast<long>(i) + w + 1);
+    sp.b_lo = static_cast<int>(lo);
+    sp.b_hi = static_cast<int>(hi);
+  } else {
+    const int r = i - Np;
+    const int b0 = (r / bs) * bs;
+    const int c_lo = std::max(0, b0 - w);
+    const int c_hi = causal ? r + 1 : std::min(b0 + bs, S - Np);
+    sp.b_lo = Np + c_lo;
+    sp.b_hi = Np + c_hi;
+  }
+  return sp;
+}
+
+// Number of allowed keys of a row inside [k0, k1).
+inline int span_count(const RowSpan& sp, int k0, int k1) {
+  int n = 0;
+  const int a1 = std::min(sp.a_end, k1);
+  if (a1 > k0) n += a1 - k0;
+  const int b0 = std::max(sp.b_lo, k0), b1 = std::min(sp.b_hi, k1);
+  if (b1 > b0) {
+    // Remove any overlap with the first interval so nothing is counted twice.
+    const int ov0 = std::max(b0, k0), ov1 = std::min(b1, std::min(sp.a_end, k1));
+    n += (b1 - b0) - std::max(0, ov1 - ov0);
+  }
+  return n;
+}
+
+int check_mask_args(int S, int window, int n_persistent, int pattern, int block_size) {
+  if (S <= 0) return TMAC_ERR_SHAPE;
+  if (n_persistent < 0) return TMAC_ERR_VALUE;
+  if (n_persistent >= S) return TMAC_ERR_VALUE;  // windowed_attention.py:97-100
+  if (window < 0) return TMAC_ERR_VALUE;         // windowed_attention.py:102-103
+  if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
+  if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
+  return TMAC_OK;
+}
+
+// Kind of the tile rows [q0, q1) x keys [k0, k1) (both clipped to S by the
+// caller's padding rule: padded positions count as masked).
+uint8_t tile_kind(const std::vector<RowSpan>& spans, int S, int q0, int q1, int k0, int k1) {
+  const int tile_rows = q1 - q0, tile_cols = k1 - k0;
+  const int qe = std::min(q1, S), ke = std::min(k1, S);
+  long allowed = 0;
+  if (qe > q0 && ke > k0)
+    for (int i = q0; i < qe; ++i) allowed += span_count(spans[i], k0, ke);
+  if (allowed == 0) return 0;
+  if (allowed == static_cast<long>(tile_rows) * tile_cols) return 1;
+  return 2;
+}
+
+}  // namespace
+
+extern "C" int tmac_wattn_tile_kinds(int S, int window, int n_persistent, int causal,
+                                     int pattern, int block_size, int tq, int tk,
+                                     uint8_t* h_kind) {
+  if (!h_kind) return TMAC_ERR_NULL;
+  int st = check_mask_args(S, window, n_persistent, pattern, block_size);
+  if (st != TMAC_OK) return st;
+  if (tq <= 0 || tk <= 0) return TMAC_ERR_SHAPE;
+  std::vector<RowSpan> spans(S);
+  for (int i = 0; i < S; ++i)
+    spans[i] = row_span(i, S, window, n_persistent, causal != 0, pattern, block_size);
+  const int n_qt = (S + tq - 1) / tq, n_kt = (S + tk - 1) / tk;
+  for (int qt = 0; qt < n_qt; ++qt)
+    for (int kt = 0; kt < n_kt; ++kt)
+      h_kind[static_cast<size_t>(qt) * n_kt + kt] =
+          tile_kind(spans, S, qt * tq, qt * tq + tq, kt * tk, kt * tk + tk);
+  return TMAC_OK;
+}
+
+extern "C" int tmac_wattn_schedule(int S, int window, int n_persistent, int causal,
+                                   int pattern, int block_size, int q_block, int sub_rows,
+                                   int32_t* h_row_ptr, int32_t* h_entries, int capacity,
+                                   int* n_entries) {
+  if (!h_row_ptr || !n_entries) return TMAC_ERR_NULL;
+  int st = check_mask_args(S, window, n_persistent, pattern, block_size);
+  if (st != TMAC_OK) return st;
+  if (q_block <= 0 || sub_rows <= 0 || q_block % sub_rows != 0 || q_block / sub_rows > 8)
+    return TMAC_ERR_SHAPE;
+  const int n_sub = q_block / sub_rows;
+  const int n_qb = (S + q_block - 1) / q_block;
+  const int n_kt = (S + TMAC_BLOCK - 1) / TMAC_BLOCK;
+  if (n_kt > 0xffff) return TMAC_ERR_SHAPE;
+  std::vector<RowSpan> spans(S);
+  for (int i = 0; i < S; ++i)
+    spans[i] = row_span(i, S, window, n_persistent, causal != 0, pattern, block_size);
+  int count = 0;
+  h_row_ptr[0] = 0;
+  for (int qb = 0; qb < n_qb; ++qb) {
+    for (int kt = 0; kt < n_kt; ++kt) {
+      uint32_t kinds = 0;
+      for (int j = 0; j < n_sub; ++j) {
+        const int q0 = qb * q_block + j * sub_rows;
+        const uint8_t k = tile_kind(spans, S, q0, q0 + sub_rows, kt * TMAC_BLOCK,
+                                    kt * TMAC_BLOCK + TMAC_BLOCK);
+        kinds |= static_cast<uint32_t>(k) << (2 * j);
+      }
+      if (kinds == 0) continue;
+      if (h_entries) {
+        if (count >= capacity) return TMAC_ERR_CAPACITY;
+        h_entries[count] = static_cast<int32_t>(static_cast<uint32_t>(kt) | (kinds << 16));
+      }
+      ++count;
+    }
+    h_row_ptr[qb + 1] = count;
+  }
+  *n_entries = count;
+  return TMAC_OK;
+}

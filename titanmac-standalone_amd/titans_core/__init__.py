@@ -1,0 +1,18 @@
+"""TitanMAC sparse hot path for AMD MI355X (gfx950).
+
+Drop-in Python API of the reference's hot path over hand-written HIP kernels:
+``WindowedAttention`` / ``WindowConfig`` / ``build_band_mask`` (attention),
+``MLPBlock`` with Block-ELL linears (``BlockELLLinear``, ``block_ell_mm``) and
+``TitanMACConfig``. Importing the package does not load the GPU library; the
+first kernel call does, and raises if libtmac.so is missing.
+"""
+from .attn import WindowConfig, WindowedAttention, build_band_mask
+from .blocks import MLPBlock
+from .config import TITANS_VARIANTS, TitanMACConfig
+from .kernels import BlockELLLinear, BlockELLPattern, block_ell_mm, windowed_attention
+
+__version__ = "0.1.0"
+
+__all__ = ["TitanMACConfig", "TITANS_VARIANTS", "WindowedAttention", "WindowConfig",
+           "build_band_mask", "MLPBlock", "BlockELLLinear", "BlockELLPattern", "block_ell_mm",
+           "windowed_attention"]

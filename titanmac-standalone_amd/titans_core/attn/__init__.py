@@ -1,0 +1,6 @@
+"""Attention modules (reference: attn/__init__.py:10-18)."""
+from .windowed_attention import (WindowConfig, WindowedAttention, build_band_mask,
+                                 convert_mask_to_sdpa_format, enable_sdpa_backends)
+
+__all__ = ["WindowedAttention", "WindowConfig", "build_band_mask", "convert_mask_to_sdpa_format",
+           "enable_sdpa_backends"]

@@ -1,0 +1,119 @@
+"""Loader and ctypes signatures of libtmac.so (the C ABI declared in include/tmac.h).
+
+The library is hand-written HIP for gfx950. It is loaded lazily on first use;
+a missing or mismatched library raises ImportError at that point, and there is
+no fallback implementation: every hot-path op either runs the HIP kernel or
+raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
+
+ABI_VERSION = 1
+
+F32, BF16, F16 = 0, 1, 2
+EPI_NONE, EPI_GELU = 0, 1
+PATTERN_BAND, PATTERN_BLOCKWIN = 0, 1
+
+_DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
+
+_PKG_ROOT = Path(__file__).resolve().parents[2]  # titanmac-standalone_amd/
+DEFAULT_LIB_PATH = _PKG_ROOT / "lib" / "libtmac.so"
+
+_lock = threading.Lock()
+_lib = None
+
+_i, _i64, _u64, _vp, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t
+_i64p = ctypes.POINTER(ctypes.c_int64)
+
+# name -> argtypes (every function returns int except tmac_status_string)
+SIGNATURES = {
+    "tmac_abi_version": [],
+    "tmac_bell_sample_col_idx": [_u64, _i, _i, _i, _vp],
+    "tmac_bell_validate": [_vp, _i, _i, _i],
+    "tmac_bell_transpose": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
+    "tmac_bell_fwd": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _i, _vp],
+    "tmac_bell_dx": [_vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
+    "tmac_bell_sddmm_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
+    "tmac_bell_sddmm": [_vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _sz, _i, _i, _i, _i, _i, _vp],
+    "tmac_wattn_tile_kinds": [_i, _i, _i, _i, _i, _i, _i, _i, _vp],
+    "tmac_wattn_schedule": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
+    "tmac_wattn_fwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp],
+}
+
+
+def lib_path() -> Path:
+    return Path(os.environ.get("TMAC_LIB", DEFAULT_LIB_PATH))
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (loaded once per process)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            path = lib_path()
+            if not path.exists():
+                raise ImportError(
+                    f"libtmac.so not found at {path}; build it with "
+                    f"`python titanmac-standalone_amd/build.py` (hipcc, gfx950)")
+            L = ctypes.CDLL(str(path))
+            for name, args in SIGNATURES.items():
+                fn = getattr(L, name)
+                fn.argtypes = args
+                fn.restype = _i
+            L.tmac_status_string.argtypes = [_i]
+            L.tmac_status_string.restype = ctypes.c_char_p
+            got = L.tmac_abi_version()
+            if got != ABI_VERSION:
+                raise ImportError(f"libtmac.so ABI {got} != expected {ABI_VERSION}; rebuild it")
+            _lib = L
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise for a non-zero return code: ValueError for argument errors (the
+    reference's convention for invalid configurations and masks), RuntimeError
+    for HIP launch errors."""
+    if rc == 0:
+        return
+    msg = lib().tmac_status_string(rc).decode()
+    if rc < 0:
+        raise ValueError(f"{what}: {msg} (tmac status {rc})")
+    raise RuntimeError(f"{what}: HIP error {rc}: {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODE[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def stream_ptr(device: torch.device) -> ctypes.c_void_p:
+    """The raw hipStream_t of torch's current stream on `device`."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def require_device(*tensors: torch.Tensor, what: str) -> torch.device:
+    """All tensors on the same ROCm device; returns it. No CPU path exists."""
+    dev = tensors[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            f"{what}: the TitanMAC hot path runs only on the GPU (HIP kernels for gfx950); "
+            f"got a tensor on {dev}")
+    for t in tensors[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"{what}: tensors on different devices ({dev} and {t.device})")
+    return dev

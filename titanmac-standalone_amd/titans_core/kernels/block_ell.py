@@ -1,0 +1,419 @@
+"""Block-ELL block-sparse linear op and module (HIP kernels for gfx950).
+
+The reference MLP is dense: MLPBlock.fc1 / fc2 are nn.Linear with bias and the
+activation is erf GELU (blocks/mlp.py:36-42, forward :58-64). This module is the
+block-sparse replacement of those Linear layers:
+
+    y = x · W + b,   W [in, out] stored as Block-ELL with 64x64 blocks
+
+- ``BlockELLPattern``: the sparsity pattern (col_idx) and its derived indices,
+  built and validated by the library's host code (bit-exact, deterministic).
+- ``block_ell_mm``: the functional op, registered as ``titanmac::bell_fwd``
+  with autograd; its backward is ``titanmac::bell_dx`` (dX = dY·Wᵀ) and
+  ``titanmac::bell_sddmm`` (dW on the stored blocks only).
+- ``BlockELLLinear``: an nn.Module with nn.Linear's constructor arguments and
+  init bounds, plus dense <-> Block-ELL conversion for nn.Linear checkpoints.
+
+Layout: W has n_brow = in/64 block-rows and n_bcol = out/64 block-columns;
+``values[r, s]`` is W[64r:64r+64, 64c:64c+64] (c = col_idx[r, s]) row-major, i.e.
+the transpose of the matching nn.Linear weight block.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import numpy as np
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+BLOCK = 64
+
+
+class BlockELLPattern:
+    """Sparsity pattern of a Block-ELL matrix with `n_bcol` block-columns.
+
+    col_idx: int32 [n_brow, width], each row strictly increasing.
+    Derived (host, via libtmac): the transposed index (t_ptr, t_row, t_vblk)
+    and the longest-first column order used by the forward kernel.
+    Device copies are cached per device.
+    """
+
+    def __init__(self, col_idx, n_bcol: int):
+        ci = np.ascontiguousarray(np.asarray(col_idx, dtype=np.int32))
+        if ci.ndim != 2:
+            raise ValueError(f"col_idx must be 2-D [n_brow, width], got shape {ci.shape}")
+        self.n_brow, self.width = (int(s) for s in ci.shape)
+        self.n_bcol = int(n_bcol)
+        L = _lib.lib()
+        _lib.check(L.tmac_bell_validate(ci.ctypes.data, self.n_brow, self.n_bcol, self.width),
+                   "Block-ELL col_idx")
+        self.col_idx = ci
+        self.t_ptr = np.empty(self.n_bcol + 1, dtype=np.int32)
+        self.t_row = np.empty(self.n_brow * self.width, dtype=np.int32)
+        self.t_vblk = np.empty(self.n_brow * self.width, dtype=np.int32)
+        self.order = np.empty(self.n_bcol, dtype=np.int32)
+        _lib.check(L.tmac_bell_transpose(ci.ctypes.data, self.n_brow, self.n_bcol, self.width,
+                                         self.t_ptr.ctypes.data, self.t_row.ctypes.data,
+                                         self.t_vblk.ctypes.data, self.order.ctypes.data),
+                   "Block-ELL transpose")
+        self._dev = {}
+
+    @classmethod
+    def sample(cls, seed: int, n_brow: int, n_bcol: int, width: int) -> "BlockELLPattern":
+        """`width` distinct block-columns per block-row from a splitmix64 stream."""
+        ci = np.empty((n_brow, width), dtype=np.int32)
+        _lib.check(_lib.lib().tmac_bell_sample_col_idx(int(seed) & (2**64 - 1), n_brow, n_bcol,
+                                                       width, ci.ctypes.data),
+                   "Block-ELL sampler")
+        return cls(ci, n_bcol)
+
+    @property
+    def in_features(self) -> int:
+        return BLOCK * self.n_brow
+
+    @property
+    def out_features(self) -> int:
+        return BLOCK * self.n_bcol
+
+    @property
+    def nnz_blocks(self) -> int:
+        return self.n_brow * self.width
+
+    def block_mask(self) -> np.ndarray:
+        m = np.zeros((self.n_brow, self.n_bcol), dtype=bool)
+        m[np.arange(self.n_brow)[:, None], self.col_idx] = True
+        return m
+
+    def device_index(self, device: torch.device) -> dict:
+        device = torch.device(device)
+        key = str(device)
+        if key not in self._dev:
+            mk = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)  # noqa: E731
+            self._dev[key] = {
+                "col_idx": mk(self.col_idx.reshape(-1)), "t_ptr": mk(self.t_ptr),
+                "t_row": mk(self.t_row), "t_vblk": mk(self.t_vblk), "order": mk(self.order),
+            }
+        return self._dev[key]
+
+    def __repr__(self) -> str:
+        return (f"BlockELLPattern(n_brow={self.n_brow}, n_bcol={self.n_bcol}, width={self.width}, "
+                f"density={self.width / self.n_bcol:.3f})")
+
+
+# ---------------------------------------------------------------------------
+# torch.library ops
+# ---------------------------------------------------------------------------
+
+def _check_values(values: torch.Tensor, what: str) -> None:
+    if values.dim() != 4 or values.shape[2:] != (BLOCK, BLOCK):
+        raise ValueError(f"{what}: values must be [n_brow, width, 64, 64], got {tuple(values.shape)}")
+    if values.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"{what}: the MFMA kernels take bfloat16 or float16, got {values.dtype}")
+
+
+@torch.library.custom_op("titanmac::bell_fwd", mutates_args=())
+def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
+             t_row: torch.Tensor, t_vblk: torch.Tensor, order: torch.Tensor,
+             bias: Optional[torch.Tensor], gelu: bool) -> torch.Tensor:
+    """y = (gelu)(x · W + bias) with W in Block-ELL; x [..., 64*n_brow] -> y [..., 64*n_bcol]."""
+    _check_values(values, "bell_fwd")
+    n_brow, width = int(values.shape[0]), int(values.shape[1])
+    n_bcol = int(t_ptr.numel()) - 1
+    K, N = BLOCK * n_brow, BLOCK * n_bcol
+    if x.shape[-1] != K:
+        raise ValueError(f"bell_fwd: x has {x.shape[-1]} features, W has {K} rows")
+    if x.dtype != values.dtype:
+        raise TypeError(f"bell_fwd: x dtype {x.dtype} != values dtype {values.dtype}")
+    dev = _lib.require_device(x, values, t_ptr, what="bell_fwd")
+    x2 = x.reshape(-1, K)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    if M > 0:
+        if bias is not None:
+            if bias.shape != (N,) or bias.dtype != x.dtype:
+                raise ValueError(f"bell_fwd: bias must be [{N}] of {x.dtype}")
+            bias = bias.contiguous()
+        with torch.cuda.device(dev):
+            rc = _lib.lib().tmac_bell_fwd(
+                _lib.ptr(x2), K, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
+                _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, M, n_brow,
+                n_bcol, width, _lib.dtype_code(x.dtype), _lib.EPI_GELU if gelu else _lib.EPI_NONE,
+                _lib.stream_ptr(dev))
+        _lib.check(rc, "tmac_bell_fwd")
+    return y.reshape(*x.shape[:-1], N)
+
+
+@bell_fwd.register_fake
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu):
+    n_bcol = t_ptr.shape[0] - 1
+    return x.new_empty((*x.shape[:-1], BLOCK * n_bcol))
+
+
+@torch.library.custom_op("titanmac::bell_dx", mutates_args=())
+def bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bcol: int) -> torch.Tensor:
+    """dX = dY · Wᵀ; dy [..., 64*n_bcol] -> dx [..., 64*n_brow]."""
+    _check_values(values, "bell_dx")
+    n_brow, width = int(values.shape[0]), int(values.shape[1])
+    K, N = BLOCK * n_brow, BLOCK * n_bcol
+    if dy.shape[-1] != N:
+        raise ValueError(f"bell_dx: dy has {dy.shape[-1]} features, W has {N} columns")
+    dev = _lib.require_device(dy, values, col_idx, what="bell_dx")
+    dy2 = dy.reshape(-1, N)
+    if not dy2.is_contiguous():
+        dy2 = dy2.contiguous()
+    if dy2.dtype != values.dtype:
+        dy2 = dy2.to(values.dtype)
+    M = dy2.shape[0]
+    dx = torch.empty((M, K), dtype=values.dtype, device=dev)
+    if M > 0:
+        with torch.cuda.device(dev):
+            rc = _lib.lib().tmac_bell_dx(
+                _lib.ptr(dy2), N, _lib.ptr(values.contiguous()), _lib.ptr(col_idx), _lib.ptr(dx), K,
+                M, n_brow, n_bcol, width, _lib.dtype_code(values.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc, "tmac_bell_dx")
+    return dx.reshape(*dy.shape[:-1], K)
+
+
+@bell_dx.register_fake
+def _(dy, values, col_idx, n_bcol):
+    return dy.new_empty((*dy.shape[:-1], BLOCK * values.shape[0]), dtype=values.dtype)
+
+
+@torch.library.custom_op("titanmac::bell_sddmm", mutates_args=())
+def bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow: int, width: int,
+               out_dtype: torch.dtype) -> torch.Tensor:
+    """dvalues [n_brow, width, 64, 64] = (xᵀ·dy) on the pattern's blocks (deterministic)."""
+    K = BLOCK * n_brow
+    if x.shape[-1] != K:
+        raise ValueError(f"bell_sddmm: x has {x.shape[-1]} features, W has {K} rows")
+    dev = _lib.require_device(x, dy, col_idx, what="bell_sddmm")
+    N = dy.shape[-1]
+    if N % BLOCK:
+        raise ValueError(f"bell_sddmm: dy features {N} not a multiple of 64")
+    n_bcol = N // BLOCK
+    x2 = x.reshape(-1, K).contiguous()
+    dy2 = dy.reshape(-1, N).contiguous()
+    if dy2.dtype != x2.dtype:
+        dy2 = dy2.to(x2.dtype)
+    if x2.shape[0] != dy2.shape[0]:
+        raise ValueError("bell_sddmm: x and dy have different row counts")
+    M = x2.shape[0]
+    out = torch.empty((n_brow, width, BLOCK, BLOCK), dtype=out_dtype, device=dev)
+    if M == 0:
+        return out.zero_()
+    L = _lib.lib()
+    ws_bytes = _sddmm_workspace_bytes(L, M, n_brow, n_bcol, width)
+    ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.tmac_bell_sddmm(_lib.ptr(x2), K, _lib.ptr(dy2), N, _lib.ptr(col_idx), _lib.ptr(out),
+                               _lib.dtype_code(out_dtype), _lib.ptr(ws), ws.numel() * 4, M, n_brow,
+                               n_bcol, width, _lib.dtype_code(x2.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_bell_sddmm")
+    return out
+
+
+@bell_sddmm.register_fake
+def _(x, dy, col_idx, n_brow, width, out_dtype):
+    return x.new_empty((n_brow, width, BLOCK, BLOCK), dtype=out_dtype)
+
+
+def _sddmm_workspace_bytes(L, M: int, n_brow: int, n_bcol: int, width: int) -> int:
+    import ctypes
+    out = ctypes.c_size_t(0)
+    _lib.check(L.tmac_bell_sddmm_workspace(M, n_brow, n_bcol, width, ctypes.byref(out)),
+               "tmac_bell_sddmm_workspace")
+    return int(out.value)
+
+
+def _fwd_setup_context(ctx, inputs, output):
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu = inputs
+    if gelu:
+        # The fused activation keeps no pre-activation for the backward; the
+        # module only fuses GELU when no gradient is needed.
+        ctx.gelu = True
+        return
+    ctx.gelu = False
+    ctx.save_for_backward(x, values, col_idx)
+    ctx.n_bcol = int(t_ptr.shape[0]) - 1
+    ctx.has_bias = bias is not None
+
+
+def _fwd_backward(ctx, gy):
+    if ctx.gelu:
+        raise RuntimeError("bell_fwd with the fused GELU epilogue has no backward; "
+                           "apply GELU outside the op when gradients are needed")
+    x, values, col_idx = ctx.saved_tensors
+    n_brow, width = int(values.shape[0]), int(values.shape[1])
+    gx = gv = gb = None
+    if ctx.needs_input_grad[0]:
+        gx = bell_dx(gy, values, col_idx, ctx.n_bcol).to(x.dtype)
+    if ctx.needs_input_grad[1]:
+        gv = bell_sddmm(x, gy.to(x.dtype), col_idx, n_brow, width, values.dtype)
+    if ctx.has_bias and ctx.needs_input_grad[7]:
+        gb = gy.reshape(-1, gy.shape[-1]).sum(0)
+    return gx, gv, None, None, None, None, None, gb, None
+
+
+bell_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
+
+
+def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern,
+                 bias: Optional[torch.Tensor] = None, activation: Optional[str] = None) -> torch.Tensor:
+    """y = activation(x · W + bias) with W = (pattern, values) in Block-ELL.
+
+    activation: None or "gelu" (erf form, as nn.GELU()). The GELU is fused into
+    the kernel's store when no gradient is required; otherwise it is applied as
+    a separate op so autograd can differentiate it.
+    """
+    if activation not in (None, "gelu"):
+        raise ValueError(f"unsupported activation {activation!r}")
+    idx = pattern.device_index(values.device)
+    fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
+        x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
+    y = bell_fwd(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
+                 idx["order"], bias, fuse)
+    if activation == "gelu" and not fuse:
+        y = torch.nn.functional.gelu(y)
+    return y
+
+
+# ---------------------------------------------------------------------------
+# Module
+# ---------------------------------------------------------------------------
+
+def width_for_density(n_bcol: int, density: float) -> int:
+    if not 0.0 < density <= 1.0:
+        raise ValueError(f"density must be in (0, 1], got {density}")
+    return max(1, min(n_bcol, int(round(density * n_bcol))))
+
+
+class BlockELLLinear(nn.Module):
+    """Block-sparse drop-in for nn.Linear(in_features, out_features, bias).
+
+    Parameters: ``values`` [in/64, width, 64, 64] and ``bias`` [out]; buffer
+    ``col_idx`` int32 [in/64, width] (saved in the state_dict, so the pattern
+    round-trips with the weights). Initialisation draws the stored blocks from
+    nn.Linear's default bounds U(±1/sqrt(in_features)).
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True, *,
+                 density: float = 0.5, width: Optional[int] = None, seed: int = 0,
+                 col_idx=None, device=None, dtype=None):
+        super().__init__()
+        if in_features % BLOCK or out_features % BLOCK:
+            raise ValueError(f"Block-ELL needs features divisible by {BLOCK}, got "
+                             f"{in_features} -> {out_features}")
+        self.in_features, self.out_features = in_features, out_features
+        n_brow, n_bcol = in_features // BLOCK, out_features // BLOCK
+        if col_idx is not None:
+            pat = BlockELLPattern(col_idx, n_bcol)
+            if pat.n_brow != n_brow:
+                raise ValueError(f"col_idx has {pat.n_brow} block-rows, expected {n_brow}")
+        else:
+            w = width if width is not None else width_for_density(n_bcol, density)
+            pat = BlockELLPattern.sample(seed, n_brow, n_bcol, w)
+        self._pattern = pat
+        self.register_buffer("col_idx", torch.from_numpy(pat.col_idx.copy()).to(device))
+        fk = {"device": device, "dtype": dtype}
+        self.values = nn.Parameter(torch.empty(n_brow, pat.width, BLOCK, BLOCK, **fk))
+        self.bias = nn.Parameter(torch.empty(out_features, **fk)) if bias else None
+        self.reset_parameters()
+
+    @property
+    def pattern(self) -> BlockELLPattern:
+        if self._pattern is None:
+            self._pattern = BlockELLPattern(self.col_idx.cpu().numpy(), self.out_features // BLOCK)
+        return self._pattern
+
+    @property
+    def width(self) -> int:
+        return int(self.col_idx.shape[1])
+
+    @property
+    def density(self) -> float:
+        return self.width / (self.out_features // BLOCK)
+
+    def reset_parameters(self) -> None:
+        bound = 1.0 / math.sqrt(self.in_features)
+        nn.init.uniform_(self.values, -bound, bound)
+        if self.bias is not None:
+            nn.init.uniform_(self.bias, -bound, bound)
+
+    def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        key = prefix + "col_idx"
+        if key in state_dict:
+            ci = state_dict[key]
+            if tuple(ci.shape) != tuple(self.col_idx.shape):
+                # A checkpoint with another width: resize before the copy.
+                self.col_idx = torch.empty_like(ci, device=self.col_idx.device)
+                self.values = nn.Parameter(torch.empty(
+                    ci.shape[0], ci.shape[1], BLOCK, BLOCK,
+                    device=self.values.device, dtype=self.values.dtype))
+        self._pattern = None
+        super()._load_from_state_dict(state_dict, prefix, *args, **kwargs)
+
+    def forward(self, x: torch.Tensor, activation: Optional[str] = None) -> torch.Tensor:
+        return block_ell_mm(x, self.values, self.pattern, self.bias, activation)
+
+    # -- dense <-> Block-ELL ------------------------------------------------
+
+    @torch.no_grad()
+    def to_dense_weight(self) -> torch.Tensor:
+        """nn.Linear-layout weight [out, in] with the zero blocks materialised."""
+        pat = self.pattern
+        W = torch.zeros(self.in_features, self.out_features, dtype=self.values.dtype,
+                        device=self.values.device)
+        Wv = W.view(pat.n_brow, BLOCK, pat.n_bcol, BLOCK).permute(0, 2, 1, 3)
+        rows = torch.arange(pat.n_brow, device=W.device)[:, None].expand(-1, pat.width)
+        cols = self.col_idx.long().to(W.device)
+        Wv[rows, cols] = self.values
+        return W.t().contiguous()
+
+    @torch.no_grad()
+    def to_linear(self) -> nn.Linear:
+        lin = nn.Linear(self.in_features, self.out_features, bias=self.bias is not None,
+                        device=self.values.device, dtype=self.values.dtype)
+        lin.weight.copy_(self.to_dense_weight())
+        if self.bias is not None:
+            lin.bias.copy_(self.bias)
+        return lin
+
+    @classmethod
+    @torch.no_grad()
+    def from_linear(cls, linear: nn.Linear, *, density: float = 0.5, width: Optional[int] = None,
+                    seed: int = 0, col_idx=None, select: str = "sample") -> "BlockELLLinear":
+        """Prune a dense nn.Linear (weight [out, in]) to Block-ELL.
+
+        select="sample": the seeded splitmix64 pattern (weights ignored);
+        select="magnitude": per block-row, the `width` blocks of largest
+        Frobenius norm (ties by lower block-column), sorted ascending.
+        """
+        in_f, out_f = linear.in_features, linear.out_features
+        Wkn = linear.weight.detach().t()  # [in, out], W's own orientation
+        n_brow, n_bcol = in_f // BLOCK, out_f // BLOCK
+        if col_idx is None and select == "magnitude":
+            w = width if width is not None else width_for_density(n_bcol, density)
+            norms = Wkn.float().reshape(n_brow, BLOCK, n_bcol, BLOCK).pow(2).sum(dim=(1, 3))
+            order = torch.sort(-norms, dim=1, stable=True).indices[:, :w]
+            col_idx = torch.sort(order, dim=1).values.to(torch.int32).cpu().numpy()
+        elif col_idx is None and select != "sample":
+            raise ValueError(f"unknown select {select!r}")
+        mod = cls(in_f, out_f, linear.bias is not None, density=density, width=width, seed=seed,
+                  col_idx=col_idx, device=linear.weight.device, dtype=linear.weight.dtype)
+        pat = mod.pattern
+        blocks = Wkn.reshape(n_brow, BLOCK, n_bcol, BLOCK).permute(0, 2, 1, 3)
+        rows = torch.arange(n_brow, device=Wkn.device)[:, None].expand(-1, pat.width)
+        cols = mod.col_idx.long().to(Wkn.device)
+        mod.values.copy_(blocks[rows, cols])
+        if linear.bias is not None:
+            mod.bias.copy_(linear.bias)
+        return mod
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, width={self.width}, density={self.density:.3f}")
