@@ -1,0 +1,352 @@
+"""Benchmark of the TitanMAC sparse hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--mode MODE]
+
+A step is one pass of the hot path over one batch of synthetic input. The
+headline `value` is the Block-ELL SpMM forward of BASELINE config 2 (X [8192,
+2560] bf16 · W [2560, 10240] Block-ELL, 64x64 blocks, 40 of 160 block-columns
+per block-row), in effective TFLOP/s (multiply-adds on stored blocks only).
+The same run also times, as secondary figures:
+  - windowed attention forward of config 3 (B=8, H=10, S=4096, dh=64, w=512,
+    Np=16, bf16) in tokens/s, against the dense masked SDPA and the dense
+    bmm -> softmax -> bmm path on the same GPU (the faster one is the
+    denominator of `attn_speedup_vs_dense`);
+  - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40).
+Inputs are drawn on the CPU from fixed seeds and copied to HBM before timing.
+Kernel time is measured with HIP events on the launch stream (torch's current
+stream) around exactly K back-to-back launches after W warm-up launches.
+The CPU baseline runs the oracle's dense restatement of the reference path
+(X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only.
+
+Modes (for profiling runs): all (default), spmm, attn, dx, sddmm, copy (a
+plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "titanmac-standalone_amd"))
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+from titans_core.kernels import _lib  # noqa: E402
+from titans_core.kernels.block_ell import BlockELLPattern, _sddmm_workspace_bytes  # noqa: E402
+from titans_core.kernels.window_attn import _device_work_list  # noqa: E402
+
+METRIC = "Block-ELL SpMM effective TFLOP/s; windowed-attn fwd tokens/s at T=4096,w=512"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+BS = 64
+
+CFG2 = dict(M=8192, n_brow=40, n_bcol=160, width=40, seed=0)
+CFG3 = dict(B=8, H=10, S=4096, dh=64, window=512, n_persistent=16, seed=3)
+CFG4 = dict(M=32768, n_brow=10, n_bcol=40, width=20, seed=4)
+
+
+def band_pairs(S: int, w: int, Np: int) -> int:
+    """Allowed (query, key) pairs of the causal band mask with Np persistent tokens."""
+    T = S - Np
+    a = min(T, w + 1)
+    return Np * Np + T * Np + a * (a - 1) // 2 + (T - a) * w + T
+
+
+def timed(launch, steps: int, warmup: int, stream) -> float:
+    """Mean ms per launch over `steps` back-to-back launches on `stream`."""
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(steps):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def gen(shape, seed, scale=1.0, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# Workloads (each returns a zero-argument launch closure and its work figures)
+# ---------------------------------------------------------------------------
+
+def setup_spmm(dev):
+    c = CFG2
+    pat = BlockELLPattern.sample(c["seed"], c["n_brow"], c["n_bcol"], c["width"])
+    K, N = BS * c["n_brow"], BS * c["n_bcol"]
+    X_cpu = gen((c["M"], K), c["seed"] + 1)
+    V_cpu = gen((c["n_brow"], c["width"], BS, BS), c["seed"] + 2, 0.02)
+    X, V = X_cpu.to(dev), V_cpu.to(dev)
+    Y = torch.empty(c["M"], N, dtype=torch.bfloat16, device=dev)
+    idx = pat.device_index(dev)
+    L = _lib.lib()
+    stream = _lib.stream_ptr(dev)
+    args = (_lib.ptr(X), K, _lib.ptr(V), _lib.ptr(idx["t_ptr"]), _lib.ptr(idx["t_row"]),
+            _lib.ptr(idx["t_vblk"]), _lib.ptr(idx["order"]), _lib.ptr(None), _lib.ptr(Y), N,
+            c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
+
+    def launch():
+        rc = L.tmac_bell_fwd(*args)
+        if rc:
+            _lib.check(rc, "tmac_bell_fwd")
+
+    nnz = c["n_brow"] * c["width"]
+    flops = 2 * c["M"] * nnz * BS * BS
+    bytes_ = c["M"] * K * 2 + nnz * BS * BS * 2 + (c["n_bcol"] + 1 + 2 * nnz + c["n_bcol"]) * 4 + c["M"] * N * 2
+    return dict(launch=launch, flops=flops, bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu,
+                keep=(X, V, Y, idx))
+
+
+def setup_attn(dev):
+    c = CFG3
+    shape = (c["B"], c["S"], 3, c["H"], c["dh"])  # fused qkv projection output layout
+    qkv = gen(shape, c["seed"]).to(dev)
+    q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))  # [B, H, S, dh] views
+    out = torch.empty(c["B"], c["S"], c["H"], c["dh"], dtype=torch.bfloat16, device=dev)
+    o_view = out.permute(0, 2, 1, 3)
+    row_ptr, entries = _device_work_list(c["S"], c["window"], c["n_persistent"], True,
+                                         _lib.PATTERN_BAND, 64, dev)
+    import ctypes
+    st = lambda t: (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    L = _lib.lib()
+    stream = _lib.stream_ptr(dev)
+    args = (_lib.ptr(q), st(q), _lib.ptr(k), st(k), _lib.ptr(v), st(v), _lib.ptr(out), st(o_view),
+            None, c["B"], c["H"], c["S"], c["dh"], c["window"], c["n_persistent"], 1,
+            _lib.PATTERN_BAND, 64, float(1.0 / np.sqrt(c["dh"])), _lib.ptr(row_ptr),
+            _lib.ptr(entries), _lib.BF16, stream)
+
+    def launch():
+        rc = L.tmac_wattn_fwd(*args)
+        if rc:
+            _lib.check(rc, "tmac_wattn_fwd")
+
+    pairs = band_pairs(c["S"], c["window"], c["n_persistent"])
+    bh = c["B"] * c["H"]
+    flops = 4 * c["dh"] * pairs * bh
+    bytes_ = 4 * bh * c["S"] * c["dh"] * 2
+    return dict(launch=launch, flops=flops, bytes=bytes_, tokens=c["B"] * c["S"],
+                keep=(qkv, out, row_ptr, entries), q=q, k=k, v=v)
+
+
+def setup_dx_sddmm(dev):
+    c = CFG4
+    pat = BlockELLPattern.sample(c["seed"], c["n_brow"], c["n_bcol"], c["width"])
+    K, N, M = BS * c["n_brow"], BS * c["n_bcol"], c["M"]
+    X = gen((M, K), c["seed"] + 1).to(dev)
+    dY = gen((M, N), c["seed"] + 2).to(dev)
+    V = gen((c["n_brow"], c["width"], BS, BS), c["seed"] + 3, 0.02).to(dev)
+    dX = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+    dV = torch.empty(c["n_brow"], c["width"], BS, BS, dtype=torch.float32, device=dev)
+    idx = pat.device_index(dev)
+    L = _lib.lib()
+    ws_bytes = _sddmm_workspace_bytes(L, M, c["n_brow"], c["n_bcol"], c["width"])
+    ws = torch.empty(ws_bytes // 4 + 4, dtype=torch.float32, device=dev)
+    stream = _lib.stream_ptr(dev)
+    dx_args = (_lib.ptr(dY), N, _lib.ptr(V), _lib.ptr(idx["col_idx"]), _lib.ptr(dX), K, M,
+               c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, stream)
+    sd_args = (_lib.ptr(X), K, _lib.ptr(dY), N, _lib.ptr(idx["col_idx"]), _lib.ptr(dV), _lib.F32,
+               _lib.ptr(ws), ws.numel() * 4, M, c["n_brow"], c["n_bcol"], c["width"], _lib.BF16,
+               stream)
+
+    def launch_dx():
+        rc = L.tmac_bell_dx(*dx_args)
+        if rc:
+            _lib.check(rc, "tmac_bell_dx")
+
+    def launch_sddmm():
+        rc = L.tmac_bell_sddmm(*sd_args)
+        if rc:
+            _lib.check(rc, "tmac_bell_sddmm")
+
+    nnz = c["n_brow"] * c["width"]
+    flops = 2 * M * nnz * BS * BS
+    dx_bytes = M * N * 2 + nnz * BS * BS * 2 + M * K * 2
+    sd_bytes = M * K * 2 + M * N * 2 + nnz * BS * BS * 4
+    return dict(dx=launch_dx, sddmm=launch_sddmm, flops=flops, dx_bytes=dx_bytes,
+                sd_bytes=sd_bytes, keep=(X, dY, V, dX, dV, ws, idx))
+
+
+def dense_attention_baseline(att, steps: int, warmup: int, stream):
+    """ms of the reference's dense path on this GPU: masked SDPA, and bmm -> softmax -> bmm."""
+    c = CFG3
+    S = c["S"]
+    i = torch.arange(S, device=att["q"].device)
+    j = i[None, :]
+    i = i[:, None]
+    Np, w = c["n_persistent"], c["window"]
+    allowed = (j < Np) | ((i >= Np) & (j >= Np) & (j >= i - w) & (j <= i))
+    add = torch.zeros(S, S, dtype=torch.bfloat16, device=i.device).masked_fill(~allowed, float("-inf"))
+    q, k, v = att["q"], att["k"], att["v"]
+    res = {}
+    sdpa = lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=add)  # noqa: E731
+    res["sdpa_masked_ms"] = timed(sdpa, max(2, steps // 10), 2, stream)
+    B, H, dh = c["B"], c["H"], c["dh"]
+    qb = q.reshape(B * H, S, dh)
+    kt = k.reshape(B * H, S, dh).transpose(1, 2).contiguous()
+    vb = v.reshape(B * H, S, dh)
+
+    def bmm_path():
+        s = torch.bmm(qb, kt) * (1.0 / dh ** 0.5) + add
+        return torch.bmm(torch.softmax(s, dim=-1), vb)
+
+    res["bmm_softmax_bmm_ms"] = timed(bmm_path, max(2, steps // 10), 2, stream)
+    return res
+
+
+def cpu_baseline(spmm) -> dict:
+    """The oracle's dense restatement (fp32 numpy X @ to_dense(W)) on the host cores."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import block_ell as ob  # the checker / CPU baseline only
+    try:
+        from threadpoolctl import threadpool_info, threadpool_limits
+    except ImportError:  # pragma: no cover
+        threadpool_info = threadpool_limits = None
+    c = CFG2
+    cores = min(os.cpu_count() or 1, 16)
+    X = spmm["X_cpu"].float().numpy()
+    W = ob.to_dense(spmm["pat"].col_idx, spmm["V_cpu"].float().numpy(), c["n_bcol"])
+    import contextlib
+    ob_rows = 2048
+    Xs = np.ascontiguousarray(X[:ob_rows])
+    limit = threadpool_limits(limits=cores) if threadpool_limits else contextlib.nullcontext()
+    with limit:
+        used = cores
+        if threadpool_info:
+            used = max([p.get("num_threads", 1) for p in threadpool_info()] or [cores])
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            _ = Xs @ W
+            reps += 1
+            el = time.perf_counter() - t0
+            if el > 10.0 or reps >= 40:
+                break
+    eff = 2 * ob_rows * c["n_brow"] * c["width"] * BS * BS
+    return {"value": round(eff * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(used),
+            "kind": "port",
+            "sample": f"oracle dense fp32 X[{ob_rows},2560] @ to_dense(W)[2560,10240], {reps} reps "
+                      f"in {el:.1f} s; effective (stored-block) FLOPs counted, as on the GPU"}
+
+
+def load_traffic() -> dict | None:
+    p = ROOT / "profiles" / "traffic.json"
+    if not p.exists():
+        return None
+    try:
+        return json.loads(p.read_text())
+    except (ValueError, OSError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description="TitanMAC sparse hot path benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "dx", "sddmm", "copy"])
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the hot path's kernels run on one MI355X and this "
+              "build has no multi-GPU code path; run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.current_stream(dev)
+    K, W = args.steps, args.warmup
+
+    if args.mode == "copy":
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)  # 1 GiB
+        dst = torch.empty_like(src)
+        ms = timed(lambda: dst.copy_(src), K, W, stream)
+        print(json.dumps({"mode": "copy", "bytes_read": src.numel() * 2, "bytes_written": dst.numel() * 2,
+                          "ms": ms, "GB/s": 2 * src.numel() * 2 / ms / 1e6}))
+        return 0
+
+    out = {}
+    if args.mode in ("all", "spmm"):
+        spmm = setup_spmm(dev)
+        ms = timed(spmm["launch"], K, W, stream)
+        out["spmm"] = dict(ms=ms, tflops=spmm["flops"] / ms / 1e9, flops=spmm["flops"],
+                           bytes=spmm["bytes"])
+    if args.mode in ("all", "attn"):
+        att = setup_attn(dev)
+        ms = timed(att["launch"], K, W, stream)
+        out["attn"] = dict(ms=ms, tokens_per_s=att["tokens"] / ms * 1e3,
+                           tflops=att["flops"] / ms / 1e9, gbs=att["bytes"] / ms / 1e6)
+        if args.mode == "all":
+            out["attn"].update(dense_attention_baseline(att, K, W, stream))
+    if args.mode in ("all", "dx", "sddmm"):
+        bw = setup_dx_sddmm(dev)
+        if args.mode in ("all", "dx"):
+            ms = timed(bw["dx"], K, W, stream)
+            out["dx"] = dict(ms=ms, tflops=bw["flops"] / ms / 1e9, gbs=bw["dx_bytes"] / ms / 1e6)
+        if args.mode in ("all", "sddmm"):
+            ms = timed(bw["sddmm"], K, W, stream)
+            out["sddmm"] = dict(ms=ms, tflops=bw["flops"] / ms / 1e9, gbs=bw["sd_bytes"] / ms / 1e6)
+
+    if args.mode != "all":
+        print(json.dumps({"mode": args.mode, **out}))
+        return 0
+
+    s = out["spmm"]
+    a = out["attn"]
+    dense_ms = min(a["sdpa_masked_ms"], a["bmm_softmax_bmm_ms"])
+    traffic = load_traffic()
+    line = {
+        "metric": METRIC,
+        "value": round(s["tflops"], 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(s["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) block values, splitmix64 pattern)",
+        "config": {"workload": "Block-ELL SpMM forward, BASELINE config 2: X[8192,2560] bf16 . "
+                               "W[2560,10240] Block-ELL 64x64, width 40 of 160 (25%), fp32 "
+                               "accumulate, bf16 out",
+                   "M": CFG2["M"], "K": 2560, "N": 10240, "block": 64, "width": CFG2["width"],
+                   "seed": CFG2["seed"]},
+        "roofline": {"bound": "mfma", "achieved": round(s["tflops"], 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(s["tflops"] / PEAK_BF16_TFLOPS, 4),
+                     "traffic": (traffic or {}).get("bell_fwd_cfg2_bytes")},
+        "secondary": {
+            "windowed_attn_fwd_tokens_per_s": round(a["tokens_per_s"], 1),
+            "windowed_attn_fwd_ms": round(a["ms"], 5),
+            "windowed_attn_fwd_tflops_algorithmic": round(a["tflops"], 3),
+            "windowed_attn_fwd_hbm_gbs_compulsory": round(a["gbs"], 1),
+            "dense_masked_sdpa_ms": round(a["sdpa_masked_ms"], 4),
+            "dense_bmm_softmax_bmm_ms": round(a["bmm_softmax_bmm_ms"], 4),
+            "attn_speedup_vs_dense": round(dense_ms / a["ms"], 2),
+            "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),
+            "bell_dx_cfg4_tflops": round(out["dx"]["tflops"], 3),
+            "bell_dx_cfg4_hbm_gbs_compulsory": round(out["dx"]["gbs"], 1),
+            "bell_sddmm_cfg4_ms": round(out["sddmm"]["ms"], 5),
+            "bell_sddmm_cfg4_tflops": round(out["sddmm"]["tflops"], 3),
+            "bell_sddmm_cfg4_hbm_gbs_compulsory": round(out["sddmm"]["gbs"], 1),
+        },
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(spmm)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

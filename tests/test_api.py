@@ -1,0 +1,158 @@
+"""Drop-in API on the CPU: TitanMACConfig, WindowedAttention / MLPBlock /
+BlockELLLinear construction and state_dicts, build_band_mask, dense <-> ELL
+conversion, meta shapes of the torch ops, and that the hot path refuses CPU
+tensors instead of falling back."""
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import titans_core as tc
+from oracle import block_ell as ob
+from oracle import masks as om
+from titans_core.attn.windowed_attention import (WindowConfig, WindowedAttention, build_band_mask,
+                                                 convert_mask_to_sdpa_format)
+from titans_core.blocks.mlp import MLPBlock
+from titans_core.kernels.block_ell import BlockELLLinear, bell_fwd
+
+# Field defaults of the reference dataclass (config.py:80-158).
+REFERENCE_DEFAULTS = dict(
+    vocab_size=128000, d_model=640, n_heads=10, n_layers=16, d_ff=2560, max_seq_len=4096,
+    window_size=512, n_persistent=16, use_block_sparse=True, block_size=64, dropout=0.0,
+    tie_weights=True, use_memory_bank=False, enable_test_time_memory=False, memory_mlp_expansion=4,
+    memory_lambda_decay=0.95, memory_eta_lr=0.01, memory_rank_ratio=0.25, norm_eps=1e-5,
+    attention_dropout=0.0, causal=True, use_neural_memory=False, n_memory_layers=2, d_memory=None,
+    memory_theta_lr=0.01, memory_forget_hidden=32, memory_decay_hidden=32, memory_capacity=512,
+    titans_variant="MAC", use_parallel_memory=True, segment_size=512, n_memory_tokens=32,
+    use_dmgd=False, dmgd_hidden_dim=64, dmgd_n_groups=2, use_cms=False, cms_frequencies=None)
+
+
+def test_config_defaults_match_reference():
+    cfg = tc.TitanMACConfig()
+    d = cfg.to_dict()
+    for k, v in REFERENCE_DEFAULTS.items():
+        assert d[k] == v, k
+    new = set(d) - set(REFERENCE_DEFAULTS)
+    assert new == {"mlp_block_ell", "mlp_density", "mlp_block_size", "mlp_ell_seed"}
+    assert cfg.d_head == 64
+    cfg.validate()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(d_model=641), "must be divisible by n_heads"), (dict(n_persistent=4096), "must be < max_seq_len"),
+    (dict(window_size=-1), "window_size must be non-negative"), (dict(d_ff=0), "d_ff must be positive"),
+    (dict(dropout=1.5), "dropout must be in"), (dict(memory_lambda_decay=1.0), "memory_lambda_decay"),
+    (dict(titans_variant="XYZ"), "titans_variant must be one of"),
+    (dict(use_cms=True, cms_frequencies={0: 0}), "CMS frequency must be positive"),
+    (dict(mlp_block_ell=True, mlp_density=0.0), "mlp_density"),
+    (dict(mlp_block_ell=True, d_ff=2500), "multiple of mlp_block_size")])
+def test_config_validate_errors(kw, msg):
+    with pytest.raises(ValueError, match=msg):
+        tc.TitanMACConfig(**kw).validate()
+
+
+def test_config_from_cfg_and_repr():
+    cfg = tc.TitanMACConfig.from_cfg({"vocab_size": 50000, "d_model": 512, "n_heads": 8, "bogus": 1})
+    assert cfg.vocab_size == 50000 and cfg.d_head == 64
+    obj = type("O", (), {"d_model": 256, "n_heads": 4})()
+    assert tc.TitanMACConfig.from_cfg(obj).d_model == 256
+    assert repr(tc.TitanMACConfig()).startswith("TitanMACConfig(d_model=640, n_heads=10")
+    with pytest.raises(ValueError):
+        tc.TitanMACConfig(d_model=641).d_head
+
+
+def test_windowed_attention_construction_and_state_dict():
+    a = WindowedAttention(WindowConfig(window_size=256, num_heads=8, head_dim=64, n_persistent=16))
+    sd = a.state_dict()
+    assert set(sd) == {"qkv_proj.weight", "out_proj.weight"}
+    assert sd["qkv_proj.weight"].shape == (1536, 512) and sd["out_proj.weight"].shape == (512, 512)
+    b = WindowedAttention(tc.TitanMACConfig(d_model=640, n_heads=10, window_size=512))
+    assert (b.n_heads, b.d_head, b.window_size, b.num_persistent, b.causal) == (10, 64, 512, 16, True)
+    with pytest.raises(AssertionError):
+        WindowedAttention(type("C", (), {"d_model": 100, "n_heads": 3, "d_head": 33, "window_size": 4,
+                                         "n_persistent": 0, "causal": True, "attention_dropout": 0.0})())
+
+
+def test_hot_path_refuses_cpu_tensors():
+    a = WindowedAttention(WindowConfig(window_size=8, num_heads=2, head_dim=64, n_persistent=2))
+    with pytest.raises(RuntimeError, match="runs only on the GPU"):
+        a(torch.randn(1, 16, 128))
+    with pytest.raises(NotImplementedError):
+        a(torch.randn(1, 16, 128), attn_mask=torch.ones(16, 16, dtype=torch.bool))
+    lin = BlockELLLinear(128, 128, density=0.5).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="runs only on the GPU"):
+        lin(torch.randn(3, 128).to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("S,w,Np,causal", [(64, 8, 4, True), (100, 30, 0, False), (4096, 512, 16, True),
+                                           (17, 100, 16, True)])
+def test_build_band_mask_bit_exact(S, w, Np, causal):
+    m = build_band_mask(S, w, Np, device="cpu", causal=causal)
+    assert m.dtype == torch.bool and m.shape == (S, S)
+    assert np.array_equal(m.numpy(), om.band_mask(S, w, Np, causal))
+    with pytest.raises(ValueError):
+        build_band_mask(8, 2, 8, device="cpu")
+    add = convert_mask_to_sdpa_format(m[:8, :8])
+    assert add.dtype == torch.float32 and (add[m[:8, :8]] == 0).all() and torch.isinf(add[~m[:8, :8]]).all()
+
+
+def test_mlp_block_dense_matches_reference_layout():
+    m = MLPBlock(128, 512)
+    sd = m.state_dict()
+    assert {k: tuple(v.shape) for k, v in sd.items()} == {
+        "fc1.weight": (512, 128), "fc1.bias": (512,), "fc2.weight": (128, 512), "fc2.bias": (128,)}
+    x = torch.randn(2, 3, 128)
+    ref = m.fc2(nn.functional.gelu(m.fc1(x)))
+    assert torch.allclose(m(x), ref)
+
+
+def test_mlp_block_ell_construction():
+    cfg = tc.TitanMACConfig(d_model=640, d_ff=2560, mlp_block_ell=True, mlp_density=0.5)
+    m = MLPBlock.from_config(cfg)
+    assert isinstance(m.fc1, BlockELLLinear) and m.fc1.values.shape == (10, 20, 64, 64)
+    assert m.fc2.values.shape == (40, 5, 64, 64)
+    assert not np.array_equal(m.fc1.col_idx.numpy()[:5, :5], m.fc2.col_idx.numpy()[:5, :5])
+
+
+def test_block_ell_linear_dense_round_trip_and_pruning():
+    torch.manual_seed(0)
+    lin = nn.Linear(256, 384)
+    e = BlockELLLinear.from_linear(lin, density=0.5, seed=3)
+    W = e.to_dense_weight()
+    assert W.shape == (384, 256)
+    mask = np.kron(ob.block_mask(e.col_idx.numpy(), 6), np.ones((64, 64), dtype=bool)).T  # [out, in]
+    assert torch.equal(W[torch.from_numpy(mask)], lin.weight.detach()[torch.from_numpy(mask)])
+    assert (W[~torch.from_numpy(mask)] == 0).all()
+    back = e.to_linear()
+    assert torch.equal(back.weight, W) and torch.equal(back.bias, lin.bias)
+    # oracle view of the same layer: values are the [in, out] orientation blocks
+    Wkn = ob.to_dense(e.col_idx.numpy(), e.values.detach().numpy(), 6)
+    assert np.array_equal(Wkn, W.t().numpy())
+    mag = BlockELLLinear.from_linear(lin, width=2, select="magnitude")
+    norms = lin.weight.detach().t().reshape(4, 64, 6, 64).pow(2).sum(dim=(1, 3))
+    want = np.sort(np.argsort(-norms.numpy(), axis=1, kind="stable")[:, :2], axis=1)
+    assert np.array_equal(mag.col_idx.numpy(), want)
+
+
+def test_block_ell_state_dict_round_trip_with_other_pattern():
+    a = BlockELLLinear(128, 256, density=0.5, seed=1)
+    b = BlockELLLinear(128, 256, density=0.25, seed=2)
+    b.load_state_dict(a.state_dict())
+    assert torch.equal(b.col_idx, a.col_idx) and torch.equal(b.values, a.values)
+    assert np.array_equal(b.pattern.col_idx, a.col_idx.numpy())
+
+
+def test_ops_fake_shapes():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    with FakeTensorMode():
+        x = torch.empty(2, 7, 128, dtype=torch.bfloat16)
+        v = torch.empty(2, 3, 64, 64, dtype=torch.bfloat16)
+        i = torch.empty(6, dtype=torch.int32)
+        tp = torch.empty(5, dtype=torch.int32)
+        y = bell_fwd(x, v, i, tp, i, i, tp[:4], None, False)
+        assert y.shape == (2, 7, 256)
+        q = torch.empty(2, 3, 100, 64, dtype=torch.bfloat16)
+        from titans_core.kernels.window_attn import window_attn_fwd
+        assert window_attn_fwd(q, q, q, 8, 2, True, 0, 64, 0.125).shape == (2, 100, 3, 64)

@@ -1,0 +1,171 @@
+"""GPU parity of the Block-ELL kernels (forward, dX, dW-SDDMM) against the oracle.
+
+Tolerance for 16-bit outputs against the fp64 oracle on the same (16-bit
+rounded) inputs: |got - want| <= 2e-2 + 1e-2 |want| (bf16 bar; fp16 is
+tighter in practice). fp32 SDDMM output: rtol 1e-4 of the block's scale.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import block_ell as ob
+from titans_core.kernels import block_ell as kb
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def close(got, want, atol=ATOL, rtol=RTOL):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    err = np.abs(got - want)
+    ok = err <= atol + rtol * np.abs(want)
+    assert ok.all(), f"max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+def data(M, n_brow, n_bcol, width, dtype, seed, vscale=0.05):
+    g = torch.Generator().manual_seed(seed)
+    pat = kb.BlockELLPattern.sample(seed, n_brow, n_bcol, width)
+    X = torch.randn(M, 64 * n_brow, generator=g).to(dtype)
+    V = (torch.randn(n_brow, width, 64, 64, generator=g) * vscale).to(dtype)
+    dY = torch.randn(M, 64 * n_bcol, generator=g).to(dtype)
+    b = (torch.randn(64 * n_bcol, generator=g) * 0.1).to(dtype)
+    return pat, X, V, dY, b
+
+
+SHAPES = [  # M, n_brow, n_bcol, width
+    (1, 1, 1, 1), (37, 2, 3, 1), (256, 3, 5, 2), (300, 4, 6, 6), (513, 10, 40, 20), (1000, 5, 7, 3)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,n_brow,n_bcol,width", SHAPES)
+def test_fwd_dx_sddmm_parity(dev, dtype, M, n_brow, n_bcol, width):
+    pat, X, V, dY, b = data(M, n_brow, n_bcol, width, dtype, seed=M + width)
+    Xn, Vn, dYn, bn = (t.float().numpy() for t in (X, V, dY, b))
+    idx = pat.device_index(dev)
+    Xd, Vd, dYd, bd = (t.to(dev) for t in (X, V, dY, b))
+    y = kb.block_ell_mm(Xd, Vd, pat)
+    yb = kb.block_ell_mm(Xd, Vd, pat, bd)
+    yg = kb.block_ell_mm(Xd, Vd, pat, bd, activation="gelu")
+    dx = kb.bell_dx(dYd, Vd, idx["col_idx"], n_bcol)
+    dv = kb.bell_sddmm(Xd, dYd, idx["col_idx"], n_brow, width, torch.float32)
+    torch.cuda.synchronize()
+    ref = ob.fwd(Xn, pat.col_idx, Vn, n_bcol)
+    close(y.float().cpu(), ref)
+    close(yb.float().cpu(), ref + bn)
+    close(yg.float().cpu(), ob.gelu_erf(ref + bn))
+    close(dx.float().cpu(), ob.dx(dYn, pat.col_idx, Vn, n_bcol))
+    want = ob.sddmm(Xn, dYn, pat.col_idx)
+    close(dv.cpu(), want, atol=1e-4 * max(1.0, np.abs(want).max()), rtol=1e-4)
+
+
+def test_empty_columns_get_bias_only(dev):
+    # width 1 of 8: most block-columns have no stored block; Y there is bias (then GELU).
+    ci = np.array([[3], [3]], dtype=np.int32)
+    pat = kb.BlockELLPattern(ci, 8)
+    g = torch.Generator().manual_seed(1)
+    X = torch.randn(70, 128, generator=g).to(torch.bfloat16)
+    V = (torch.randn(2, 1, 64, 64, generator=g) * 0.1).to(torch.bfloat16)
+    b = torch.randn(512, generator=g).to(torch.bfloat16)
+    y = kb.block_ell_mm(X.to(dev), V.to(dev), pat, b.to(dev), activation="gelu").float().cpu()
+    ref = ob.gelu_erf(ob.fwd(X.float().numpy(), ci, V.float().numpy(), 8) + b.float().numpy())
+    close(y, ref)
+
+
+def test_output_fully_written_and_deterministic(dev):
+    pat, X, V, dY, _ = data(777, 6, 9, 4, torch.bfloat16, seed=5)
+    Xd, Vd, dYd = X.to(dev), V.to(dev), dY.to(dev)
+    idx = pat.device_index(dev)
+    y1 = kb.block_ell_mm(Xd, Vd, pat)
+    assert torch.isfinite(y1).all()
+    y2 = kb.block_ell_mm(Xd, Vd, pat)
+    d1 = kb.bell_dx(dYd, Vd, idx["col_idx"], 9)
+    d2 = kb.bell_dx(dYd, Vd, idx["col_idx"], 9)
+    s1 = kb.bell_sddmm(Xd, dYd, idx["col_idx"], 6, 4, torch.float32)
+    s2 = kb.bell_sddmm(Xd, dYd, idx["col_idx"], 6, 4, torch.float32)
+    assert torch.equal(y1, y2) and torch.equal(d1, d2) and torch.equal(s1, s2)
+    assert torch.isfinite(d1).all() and torch.isfinite(s1).all()
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_sddmm_16bit_output(dev, out_dtype):
+    pat, X, V, dY, _ = data(2000, 3, 4, 2, torch.bfloat16, seed=11)
+    idx = pat.device_index(dev)
+    dv = kb.bell_sddmm(X.to(dev), dY.to(dev), idx["col_idx"], 3, 2, out_dtype)
+    assert dv.dtype == out_dtype
+    want = ob.sddmm(X.float().numpy(), dY.float().numpy(), pat.col_idx)
+    close(dv.float().cpu(), want, atol=2e-2 * np.abs(want).max() / 8, rtol=1e-2)
+
+
+def test_linear_autograd_matches_dense_fp32(dev):
+    torch.manual_seed(0)
+    lin = kb.BlockELLLinear(256, 320, density=0.4, seed=2).to(dev, torch.bfloat16)
+    x = torch.randn(3, 41, 256, device=dev).to(torch.bfloat16).requires_grad_(True)
+    y = lin(x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    W = lin.to_dense_weight().float().detach().requires_grad_(True)
+    bias = lin.bias.float().detach().requires_grad_(True)
+    xf = x.detach().float().requires_grad_(True)
+    yf = torch.nn.functional.linear(xf, W, bias)
+    yf.backward(gy.float())
+    close(y.detach().float().cpu(), yf.detach().cpu())
+    close(x.grad.float().cpu(), xf.grad.cpu())
+    close(lin.bias.grad.float().cpu(), bias.grad.cpu(), atol=0.1, rtol=1e-2)
+    # dW on the stored blocks equals the dense weight gradient there ([out, in] -> [in, out] blocks)
+    gW = W.grad.t().contiguous().cpu().numpy()
+    want = ob.from_dense(gW, lin.col_idx.cpu().numpy())
+    close(lin.values.grad.float().cpu(), want, atol=0.1, rtol=1e-2)
+
+
+def test_mlp_block_ell_forward(dev):
+    from titans_core.blocks.mlp import MLPBlock
+    torch.manual_seed(1)
+    m = MLPBlock(128, 512, block_ell=True, density=0.5, seed=3).to(dev, torch.bfloat16).eval()
+    x = torch.randn(2, 33, 128, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y = m(x).float().cpu().numpy()
+    f1, f2 = m.fc1, m.fc2
+    h = ob.fwd(x.float().cpu().numpy().reshape(-1, 128), f1.col_idx.cpu().numpy(),
+               f1.values.float().cpu().numpy(), 8, f1.bias.float().cpu().numpy(), gelu=True)
+    h = torch.from_numpy(h).to(torch.bfloat16).float().numpy()  # fc1's output is stored in bf16
+    want = ob.fwd(h, f2.col_idx.cpu().numpy(), f2.values.float().cpu().numpy(), 2,
+                  f2.bias.float().cpu().numpy())
+    close(y.reshape(-1, 128), want)
+
+
+def test_cfg2_full_size(dev):
+    """BASELINE config 2 at full size: sampled rows against the oracle, plus the
+    column-sum identity colsum(Y) = colsum(X) · W over all 8192 rows."""
+    pat = kb.BlockELLPattern.sample(0, 40, 160, 40)
+    g = torch.Generator().manual_seed(1)
+    X = torch.randn(8192, 2560, generator=g).to(torch.bfloat16)
+    V = (torch.randn(40, 40, 64, 64, generator=g) * 0.02).to(torch.bfloat16)
+    Y = kb.block_ell_mm(X.to(dev), V.to(dev), pat)
+    Yc = Y.float().cpu().numpy()
+    W = ob.to_dense(pat.col_idx, V.float().numpy(), 160)
+    rows = np.random.default_rng(0).choice(8192, 384, replace=False)
+    rows = np.concatenate([rows, [0, 255, 256, 8191]])
+    close(Yc[rows], X.float().numpy()[rows].astype(np.float64) @ W)
+    colsum_want = X.float().numpy().astype(np.float64).sum(0) @ W
+    err = np.abs(Yc.astype(np.float64).sum(0) - colsum_want)
+    assert (err <= 0.5 + 2e-3 * np.abs(colsum_want)).all(), err.max()
+
+
+def test_cfg4_full_size_dx_sddmm(dev):
+    """dX sampled rows, dW-SDDMM on all 200 blocks (M = 32768)."""
+    pat = kb.BlockELLPattern.sample(4, 10, 40, 20)
+    g = torch.Generator().manual_seed(2)
+    X = torch.randn(32768, 640, generator=g).to(torch.bfloat16)
+    dY = torch.randn(32768, 2560, generator=g).to(torch.bfloat16)
+    V = (torch.randn(10, 20, 64, 64, generator=g) * 0.02).to(torch.bfloat16)
+    idx = pat.device_index(dev)
+    dX = kb.bell_dx(dY.to(dev), V.to(dev), idx["col_idx"], 40).float().cpu().numpy()
+    dV = kb.bell_sddmm(X.to(dev), dY.to(dev), idx["col_idx"], 10, 20, torch.float32).cpu().numpy()
+    rows = np.random.default_rng(1).choice(32768, 256, replace=False)
+    W = ob.to_dense(pat.col_idx, V.float().numpy(), 40)
+    close(dX[rows], dY.float().numpy()[rows].astype(np.float64) @ W.T)
+    want = ob.sddmm(X.float().numpy(), dY.float().numpy(), pat.col_idx, dtype=np.float32)
+    scale = np.abs(want).max()
+    close(dV, want, atol=2e-5 * scale, rtol=1e-4)

@@ -1,0 +1,167 @@
+"""The C-ABI library on the CPU: it loads, exports every symbol include/tmac.h
+declares, its host index construction is bit-exact with the oracle, and its
+device entry points reject bad arguments before touching any device memory."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import block_ell as ob
+from oracle import masks as om
+from titans_core.kernels import _lib
+from titans_core.kernels.block_ell import BlockELLPattern
+from titans_core.kernels.window_attn import tile_kinds, work_list
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "tmac.h"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmac_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_symbols()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(lib, n), n
+        assert n in _lib.SIGNATURES or n == "tmac_status_string", f"{n} has no ctypes signature"
+    assert lib.tmac_abi_version() == _lib.ABI_VERSION
+
+
+def test_status_strings(lib):
+    for code in range(0, -9, -1):
+        s = lib.tmac_status_string(code).decode()
+        assert s and s != "unknown tmac status"
+    assert lib.tmac_status_string(-99).decode() == "unknown tmac status"
+
+
+@pytest.mark.parametrize("seed,n_brow,n_bcol,width", [(0, 40, 160, 40), (4, 10, 40, 20), (1, 1, 1, 1),
+                                                      (123456789, 17, 33, 32), (2**64 - 1, 5, 9, 9)])
+def test_sampler_and_transpose_bit_exact(seed, n_brow, n_bcol, width):
+    pat = BlockELLPattern.sample(seed, n_brow, n_bcol, width)
+    ci = ob.sample_col_idx(seed, n_brow, n_bcol, width)
+    assert np.array_equal(pat.col_idx, ci)
+    for got, want in zip((pat.t_ptr, pat.t_row, pat.t_vblk, pat.order), ob.transpose(ci, n_bcol)):
+        assert np.array_equal(got, want)
+
+
+def test_sampler_matches_golden():
+    assert np.array_equal(BlockELLPattern.sample(0, 40, 160, 40).col_idx,
+                          np.load(GOLDEN / "bell_col_idx_cfg2.npy"))
+    assert np.array_equal(BlockELLPattern.sample(4, 10, 40, 20).col_idx,
+                          np.load(GOLDEN / "bell_col_idx_cfg4.npy"))
+
+
+@pytest.mark.parametrize("ci", [[[0, 0]], [[2, 1]], [[0, 4]], [[-1, 2]]])
+def test_pattern_validation_rejects(ci):
+    with pytest.raises(ValueError):
+        BlockELLPattern(np.array(ci, dtype=np.int32), 4)
+
+
+def test_sampler_shape_errors(lib):
+    buf = np.zeros(4, dtype=np.int32)
+    assert lib.tmac_bell_sample_col_idx(0, 1, 3, 4, buf.ctypes.data) == -2
+    assert lib.tmac_bell_sample_col_idx(0, 1, 3, 1, None) == -1
+
+
+CASES = [(4096, 512, 16, True, "band", 64), (4112, 512, 16, True, "band", 64), (560, 512, 16, True, "band", 64),
+         (300, 64, 0, False, "band", 64), (1, 0, 0, True, "band", 64), (129, 3, 128, True, "band", 64),
+         (4096, 512, 16, True, "blockwin", 64), (333, 128, 5, False, "blockwin", 32),
+         (250, 0, 1, True, "blockwin", 64)]
+
+
+@pytest.mark.parametrize("S,w,Np,causal,pattern,bs", CASES)
+def test_tile_kinds_bit_exact(S, w, Np, causal, pattern, bs):
+    m = om.make_mask(S, w, Np, causal, pattern, bs)
+    for tq, tk in [(64, 64), (32, 64), (128, 64), (16, 32)]:
+        assert np.array_equal(tile_kinds(S, w, Np, causal, pattern, bs, tq, tk), om.tile_kinds(m, tq, tk))
+
+
+@pytest.mark.parametrize("S,w,Np,causal,pattern,bs", CASES)
+def test_work_list_bit_exact(S, w, Np, causal, pattern, bs):
+    m = om.make_mask(S, w, Np, causal, pattern, bs)
+    rp, ent = work_list(S, w, Np, causal, pattern, bs)
+    rp2, ent2 = om.schedule(m, 128, 32, 64)
+    assert np.array_equal(rp, rp2) and np.array_equal(ent, ent2)
+
+
+def test_tile_map_golden():
+    assert np.array_equal(tile_kinds(4096, 512, 16), np.load(GOLDEN / "wattn_tiles_cfg3.npy"))
+    g = np.load(GOLDEN / "wattn_worklist_cfg3.npz")
+    rp, ent = work_list(4096, 512, 16)
+    assert np.array_equal(rp, g["row_ptr"]) and np.array_equal(ent, g["entries"])
+
+
+def test_tile_map_value_errors():
+    with pytest.raises(ValueError):
+        tile_kinds(16, 4, 16)
+    with pytest.raises(ValueError):
+        tile_kinds(16, -1, 0)
+    with pytest.raises(ValueError):
+        work_list(64, 8, 0, pattern="nope")
+
+
+def test_schedule_capacity_error(lib):
+    rp = np.zeros(33, dtype=np.int32)
+    ent = np.zeros(3, dtype=np.int32)
+    n = ctypes.c_int(0)
+    rc = lib.tmac_wattn_schedule(4096, 512, 16, 1, 0, 64, 128, 32, rp.ctypes.data, ent.ctypes.data, 3,
+                                 ctypes.byref(n))
+    assert rc == -7
+
+
+# Device entry points: argument errors come back before any device access, so
+# these run without a GPU. Fake pointers are never dereferenced on these paths.
+FAKE = ctypes.c_void_p(1 << 20)
+MISALIGNED = ctypes.c_void_p((1 << 20) + 2)
+
+
+def test_bell_fwd_argument_errors(lib):
+    ok = [FAKE, 2560, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 10240, 8192, 40, 160, 40, 1, 0, None]
+    assert lib.tmac_bell_fwd(*[None if i == 0 else a for i, a in enumerate(ok)]) == -1
+    bad = list(ok); bad[13] = 161
+    assert lib.tmac_bell_fwd(*bad) == -2          # width > n_bcol
+    bad = list(ok); bad[14] = 0
+    assert lib.tmac_bell_fwd(*bad) == -4          # fp32 not supported by the MFMA kernel
+    bad = list(ok); bad[15] = 7
+    assert lib.tmac_bell_fwd(*bad) == -8          # unknown epilogue
+    bad = list(ok); bad[1] = 2000
+    assert lib.tmac_bell_fwd(*bad) == -2          # ldx < K
+    bad = list(ok); bad[0] = MISALIGNED
+    assert lib.tmac_bell_fwd(*bad) == -5
+    bad = list(ok); bad[1] = 2564
+    assert lib.tmac_bell_fwd(*bad) == -5          # ldx not a multiple of 8
+
+
+def test_bell_dx_and_sddmm_argument_errors(lib):
+    assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 0, 10, 40, 20, 1, None) == -2
+    assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 100, 10, 40, 20, 0, None) == -4
+    ws = ctypes.c_size_t(0)
+    assert lib.tmac_bell_sddmm_workspace(32768, 10, 40, 20, ctypes.byref(ws)) == 0 and ws.value > 0
+    args = [FAKE, 640, FAKE, 2560, FAKE, FAKE, 0, FAKE, ws.value - 1, 32768, 10, 40, 20, 1, None]
+    assert lib.tmac_bell_sddmm(*args) == -6      # workspace too small
+    args[8] = ws.value; args[6] = 5
+    assert lib.tmac_bell_sddmm(*args) == -4      # unknown output dtype
+
+
+def test_wattn_fwd_argument_errors(lib):
+    st = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1920)
+    base = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, None, 8, 10, 4096, 64, 512, 16, 1, 0, 64, 0.125,
+            FAKE, FAKE, 1, None]
+    a = list(base); a[12] = 32
+    assert lib.tmac_wattn_fwd(*a) == -2           # head_dim must be 64
+    a = list(base); a[14] = 4096
+    assert lib.tmac_wattn_fwd(*a) == -8           # n_persistent >= S
+    a = list(base); a[13] = -1
+    assert lib.tmac_wattn_fwd(*a) == -8           # negative window
+    a = list(base); a[21] = 9
+    assert lib.tmac_wattn_fwd(*a) == -4
+    a = list(base); a[1] = (ctypes.c_int64 * 3)(4096 * 1920, 60, 1920)
+    assert lib.tmac_wattn_fwd(*a) == -5           # head stride not 16-byte aligned
+    a = list(base); a[19] = None
+    assert lib.tmac_wattn_fwd(*a) == -1
