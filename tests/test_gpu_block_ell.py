@@ -128,10 +128,10 @@ def test_mlp_block_ell_forward(dev):
         y = m(x).float().cpu().numpy()
     f1, f2 = m.fc1, m.fc2
     h = ob.fwd(x.float().cpu().numpy().reshape(-1, 128), f1.col_idx.cpu().numpy(),
-               f1.values.float().cpu().numpy(), 8, f1.bias.float().cpu().numpy(), gelu=True)
+               f1.values.detach().float().cpu().numpy(), 8, f1.bias.detach().float().cpu().numpy(), gelu=True)
     h = torch.from_numpy(h).to(torch.bfloat16).float().numpy()  # fc1's output is stored in bf16
-    want = ob.fwd(h, f2.col_idx.cpu().numpy(), f2.values.float().cpu().numpy(), 2,
-                  f2.bias.float().cpu().numpy())
+    want = ob.fwd(h, f2.col_idx.cpu().numpy(), f2.values.detach().float().cpu().numpy(), 2,
+                  f2.bias.detach().float().cpu().numpy())
     close(y.reshape(-1, 128), want)
 
 
