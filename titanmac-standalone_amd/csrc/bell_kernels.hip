@@ -12,12 +12,15 @@
 //   - forward: output block-column c; list = the block-rows holding a block in
 //     column c (transposed index, precomputed on the host), reduction over K;
 //   - dX: output block-row r; list = row r's own width blocks, reduction over N.
-// Each wave owns 64 rows. Its activations (X or dY) go straight from HBM into
-// MFMA operand registers (16 bytes per lane, already in the B-operand layout),
-// prefetched one block ahead. The 64x64 weight block is shared by the four
-// waves, so it is staged once through LDS (double-buffered) and read as the A
-// operand: with ds_read_b64_tr_b16 for the forward (W is N-contiguous but the
-// reduction runs over K) and with plain 16-byte reads for dX (reduction over N).
+// Each wave owns 64 rows. Per list entry the workgroup loads the 256x64
+// activation tile (X or dY) and the 64x64 weight block with coalesced 16-byte
+// loads (eight lanes per 128-byte row: a lane-per-row load pattern would cost
+// the L1 one tag lookup per lane), stages both in LDS (the activation tile
+// XOR-swizzled, the weight block padded) and feeds the MFMAs from there. The
+// next entry's tiles are loaded into registers during the current entry's
+// math. The weight block is the A operand: read with ds_read_b64_tr_b16 for the
+// forward (W is N-contiguous but the reduction runs over K) and with plain
+// 16-byte reads for dX (reduction over N).
 // The MFMA computes the transposed tile Cᵀ[n][m], so each lane ends up with
 // four consecutive output columns per row; the tile is packed through LDS and
 // written with full 128-byte row segments.
@@ -39,18 +42,36 @@ using namespace tmac;
 
 namespace {
 
-constexpr int kBM = 256;  // output rows per gather-GEMM workgroup (4 waves x 64)
+constexpr int kBM = 256;        // output rows per gather-GEMM workgroup (4 waves x 64)
+constexpr int kMaxList = 1024;  // longest block list of one output block (checked on the host)
+
+// Activation tile of the gather GEMM in LDS: kBM rows of 64 16-bit values
+// (128 bytes) without padding. The 16-byte chunk c of row r sits at chunk
+// position c ^ ((r >> 1) & 7): a 16-lane phase of the operand reads (16
+// consecutive rows, one chunk each) then covers all 64 banks once, and each
+// 8-row group written by one store instruction stays a contiguous 1 KB.
+__device__ __forceinline__ int xswz(int row, int chunk) {
+  return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
+}
 
 template <int DT, bool FWD>
-__global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
+__global__ __launch_bounds__(256, 3) void bell_gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
     const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ in_blk,
     const int32_t* __restrict__ t_vblk, const int32_t* __restrict__ order,
     const uint16_t* __restrict__ bias, int epi, uint16_t* __restrict__ Y, int64_t ldy, int M,
     int n_out, int width, int n_mtiles, int per_xcd) {
-  // Two weight buffers during the main loop; four per-wave 64x64 output
-  // staging tiles in the epilogue (same memory).
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+  // Main loop: the activation tile (kBM x 64, swizzled) and the weight tile
+  // (64 x kPitch). Epilogue: four per-wave 64x64 staging tiles over the same
+  // memory.
+  constexpr int kXElems = kBM * 64;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[kXElems + kTileElems];
+  // The workgroup's list of non-zero blocks, copied once: activation block
+  // index and weight block index per entry.
+  __shared__ int32_t s_in[kMaxList];
+  __shared__ int32_t s_vb[kMaxList];
+  uint16_t* const xt = smem;
+  uint16_t* const wt = smem + kXElems;
 
   const int logical = xcd_logical_id(per_xcd);
   if (logical >= n_mtiles * n_out) return;
@@ -64,16 +85,38 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   const int wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile
-  const int m_base = mtile * kBM + wave * 64;
+  const int m_tile0 = mtile * kBM;
+  const int m_base = m_tile0 + wave * 64;
 
-  // Rows past M are clamped onto row M-1: they load valid memory and their
-  // results are never stored.
-  const uint16_t* arow[2];
-#pragma unroll
-  for (int mi = 0; mi < 2; ++mi) {
-    const int row = min(m_base + 32 * mi + l32, M - 1);
-    arow[mi] = A + static_cast<int64_t>(row) * lda + 8 * h;
+  for (int i = tid; i < e1 - e0; i += 256) {
+    s_in[i] = in_blk[e0 + i];
+    s_vb[i] = FWD ? t_vblk[e0 + i] : e0 + i;
   }
+
+  // Coalesced tile loads: thread t moves 16-byte chunk (t & 7) of rows
+  // 32j + (t >> 3), j = 0..7, of the activation tile, and of rows t >> 3 and
+  // 32 + (t >> 3) of the weight block. Rows past M are clamped onto row M-1:
+  // they load valid memory and their results are never stored.
+  const int lrow = tid >> 3, lch = tid & 7;
+  const uint16_t* xsrc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    xsrc[j] = A + static_cast<int64_t>(min(m_tile0 + 32 * j + lrow, M - 1)) * lda + 8 * lch;
+  u32x4 xr[8], wr[2];
+  auto gload = [&](int i) {
+    const int64_t col = static_cast<int64_t>(s_in[i]) * 64;
+    const uint16_t* wsrc = vals + static_cast<int64_t>(s_vb[i]) * 4096 + tid * 8;
+    wr[0] = ldg16(wsrc);
+    wr[1] = ldg16(wsrc + 2048);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xr[j] = ldg16(xsrc[j] + col);
+  };
+  auto sstore = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sts16(xt + xswz(32 * j + lrow, lch), xr[j]);
+    sts16(wt + lrow * kPitch + lch * 8, wr[0]);
+    sts16(wt + (32 + lrow) * kPitch + lch * 8, wr[1]);
+  };
 
   f32x16 acc[2][2];
 #pragma unroll
@@ -81,69 +124,64 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
 
-  u32x4 abuf0[2][4], abuf1[2][4];
-  u32x4 wreg[2];
-  uint16_t* const wtile[2] = {smem, smem + kTileElems};
-
-  auto load_a = [&](u32x4(&dst)[2][4], int e) {
-    const int64_t col = static_cast<int64_t>(in_blk[e]) * 64;
+  // MFMA operands of k-step kk: the wave's activation rows (B operand, 16-byte
+  // reads of the swizzled tile) and the weight block (A operand: transpose
+  // reads for the forward, where W is N-contiguous but the reduction runs over
+  // K; plain 16-byte reads for dX, whose reduction runs over N).
+  auto read_ops = [&](u32x4(&xa)[2], u32x4(&wf)[2], int kk) {
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
+    for (int mi = 0; mi < 2; ++mi) xa[mi] = lds16(xt + xswz(wave * 64 + 32 * mi + l32, 2 * kk + h));
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) dst[mi][kk] = ldg16(arow[mi] + col + 16 * kk);
+    for (int ni = 0; ni < 2; ++ni) {
+      if constexpr (FWD)
+        wf[ni] = lds_read_tr8(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+      else
+        wf[ni] = lds16(wt + (32 * ni + l32) * kPitch + 16 * kk + 8 * h);
+    }
   };
-  auto load_w = [&](int e) {
-    const int vb = FWD ? t_vblk[e] : e;
-    const uint16_t* src = vals + static_cast<int64_t>(vb) * 4096;
-    wreg[0] = ldg16(src + tid * 8);
-    wreg[1] = ldg16(src + (tid + 256) * 8);
-  };
-  auto store_w = [&](uint16_t* dst) {
-    sts16(dst + (tid >> 3) * kPitch + (tid & 7) * 8, wreg[0]);
-    sts16(dst + (32 + (tid >> 3)) * kPitch + (tid & 7) * 8, wreg[1]);
-  };
-  auto compute = [&](const uint16_t* wt, const u32x4(&a)[2][4]) {
+  // The reads of k-step kk+1 are issued before the MFMAs of k-step kk, and
+  // the scheduling group barriers keep that order.
+  auto compute = [&]() {
+    u32x4 xa[2][2], wf[2][2];
+    read_ops(xa[0], wf[0], 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      u32x4 wf[2];
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni) {
-        if constexpr (FWD)  // A[n][k] = W[k][n]: transpose read of the K-major tile
-          wf[ni] = lds_read_tr8(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
-        else  // A[k][n] = W[k][n]: the tile row is the operand row
-          wf[ni] = lds16(wt + (32 * ni + l32) * kPitch + 16 * kk + 8 * h);
-      }
+      if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], kk + 1);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = Mfma<DT>::run(wf[ni], a[mi][kk], acc[mi][ni]);
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = Mfma<DT>::run(wf[kk & 1][ni], xa[kk & 1][mi], acc[mi][ni]);
     }
-  };
-  // One list entry: prefetch the next entry's activations (registers) and
-  // weight block (registers, then the idle LDS buffer), compute this one.
-  int buf = 0;
-  auto step = [&](int e, const u32x4(&cur)[2][4], u32x4(&nxt)[2][4]) {
-    const bool more = e + 1 < e1;
-    if (more) {
-      load_a(nxt, e + 1);
-      load_w(e + 1);
+    constexpr int kDs = FWD ? 6 : 4;  // LDS read instructions per k-step
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * kDs, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      if (kk + 2 < 4) __builtin_amdgcn_sched_group_barrier(0x100, kDs, 0);
     }
-    compute(wtile[buf], cur);
-    if (more) store_w(wtile[buf ^ 1]);
-    __syncthreads();
-    buf ^= 1;
   };
 
-  if (e0 < e1) {
-    load_a(abuf0, e0);
-    load_w(e0);
-    store_w(wtile[0]);
-  }
-  __syncthreads();
-  for (int e = e0; e < e1; e += 2) {
-    step(e, abuf0, abuf1);
-    if (e + 1 >= e1) break;
-    step(e + 1, abuf1, abuf0);
+  // One LDS copy of the tiles: entry i+1's tiles are loaded into registers
+  // while entry i is computed, then written once every wave is done reading.
+  __syncthreads();  // index lists visible
+  const int n = e1 - e0;
+  if (n > 0) {
+    gload(0);
+    sstore();
+    __syncthreads();
+    for (int i = 0; i < n; ++i) {
+      const bool more = i + 1 < n;
+      if (more) gload(i + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute();
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+      if (more) {
+        sstore();
+        __syncthreads();
+      }
+    }
   }
 
   // Epilogue: bias, activation, conversion, then pack through this wave's LDS
@@ -357,6 +395,7 @@ extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
   if (st != TMAC_OK) return st;
   if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
   if (epi != TMAC_EPI_NONE && epi != TMAC_EPI_GELU) return TMAC_ERR_VALUE;
+  if (n_brow > kMaxList) return TMAC_ERR_SHAPE;  // a column's list has up to n_brow entries
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (ldx < K || ldy < N) return TMAC_ERR_SHAPE;
   if (!aligned16(d_X) || !aligned16(d_vals) || !aligned16(d_Y) || (ldx % 8) || (ldy % 8))
@@ -389,6 +428,7 @@ extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
   if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (width > kMaxList) return TMAC_ERR_SHAPE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (lddy < N || lddx < K) return TMAC_ERR_SHAPE;
   if (!aligned16(d_dY) || !aligned16(d_vals) || !aligned16(d_dX) || (lddy % 8) || (lddx % 8))
