@@ -107,7 +107,7 @@ int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int wi
  * epi = TMAC_EPI_GELU, also the erf GELU between them (blocks/mlp.py:42,61).
  * X, Y row-major with leading dimensions ldx, ldy; bias (nullable) has N
  * entries of the same dtype. dtype: TMAC_BF16 or TMAC_F16.
- * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary; n_brow <= 1024.
+ * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary.
  * t_ptr/t_row/t_vblk/order: device copies of tmac_bell_transpose's output. */
 int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
                   const int32_t* d_t_ptr, const int32_t* d_t_row,
@@ -120,7 +120,7 @@ int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
  * Replaces autograd's grad_input of F.linear in the MLP backward
  * (loss.backward() at train_titanmac_nested.py:462 through blocks/mlp.py:58,64).
  * For block-row r: dX[:, 64r:64r+64] = Σ_s dY[:, 64·col_idx[r][s] + :] · W[r,s]ᵀ.
- * d_col_idx: device copy of the row-major index. width <= 1024. */
+ * d_col_idx: device copy of the row-major index. */
 int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
                  const int32_t* d_col_idx, void* d_dX, int64_t lddx,
                  int M, int n_brow, int n_bcol, int width, int dtype, void* stream);

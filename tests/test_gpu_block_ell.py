@@ -35,7 +35,9 @@ def data(M, n_brow, n_bcol, width, dtype, seed, vscale=0.05):
 
 
 SHAPES = [  # M, n_brow, n_bcol, width
-    (1, 1, 1, 1), (37, 2, 3, 1), (256, 3, 5, 2), (300, 4, 6, 6), (513, 10, 40, 20), (1000, 5, 7, 3)]
+    (1, 1, 1, 1), (37, 2, 3, 1), (256, 3, 5, 2), (300, 4, 6, 6), (513, 10, 40, 20), (1000, 5, 7, 3),
+    # lists longer than 64 entries (forward: 70 block-rows per column; dX: width 100)
+    (300, 70, 3, 3), (260, 3, 130, 100)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

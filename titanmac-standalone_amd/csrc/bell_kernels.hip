@@ -16,7 +16,7 @@
 // activation tile (X or dY) and the 64x64 weight block with coalesced 16-byte
 // loads (eight lanes per 128-byte row: a lane-per-row load pattern would cost
 // the L1 one tag lookup per lane), stages both in LDS (the activation tile
-// XOR-swizzled, the weight block padded) and feeds the MFMAs from there. The
+// and the weight block XOR-swizzled) and feeds the MFMAs from there. The
 // next entry's tiles are loaded into registers during the current entry's
 // math. The weight block is the A operand: read with ds_read_b64_tr_b16 for the
 // forward (W is N-contiguous but the reduction runs over K) and with plain
@@ -43,35 +43,64 @@ using namespace tmac;
 namespace {
 
 constexpr int kBM = 256;        // output rows per gather-GEMM workgroup (4 waves x 64)
-constexpr int kMaxList = 1024;  // longest block list of one output block (checked on the host)
 
-// Activation tile of the gather GEMM in LDS: kBM rows of 64 16-bit values
-// (128 bytes) without padding. The 16-byte chunk c of row r sits at chunk
-// position c ^ ((r >> 1) & 7): a 16-lane phase of the operand reads (16
-// consecutive rows, one chunk each) then covers all 64 banks once, and each
-// 8-row group written by one store instruction stays a contiguous 1 KB.
+// LDS tiles of the gather GEMM, 64 16-bit values (128 bytes) per row without
+// padding; 16-byte chunks are XOR-swizzled for the 64 four-byte banks.
+//   activation tile (kBM rows): chunk c of row r at c ^ ((r >> 1) & 7), so a
+//     16-lane phase of the operand reads (16 consecutive rows, one chunk each)
+//     covers all 64 banks once;
+//   weight block (64 rows): chunk c of row r at c ^ w(r >> 1), w(a) =
+//     ((a & 1) << 2) | ((a >> 1) & 3): conflict-free both for the forward's
+//     transpose reads (4 consecutive rows x 64 bytes per 32-lane phase) and for
+//     dX's 16-byte row reads (16 consecutive rows per phase).
+// Every 16-lane phase of the tile stores writes 256 contiguous bytes.
 __device__ __forceinline__ int xswz(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
+__device__ __forceinline__ int wswz(int row, int chunk) {
+  const int a = (row >> 1) & 7;
+  return row * 64 + ((chunk ^ (((a & 1) << 2) | (a >> 1))) << 3);
+}
+
+// Transpose read of rows r0..r0+7 (r0 a multiple of 8) x 16 columns of a
+// wswz tile: lane (lane % 16) of each 16-lane group receives column
+// c0 + lane % 16 of those rows, as one MFMA operand (see lds_read_tr8).
+__device__ __forceinline__ u32x4 lds_read_tr8_wswz(const uint16_t* tile, int r0, int c0, int lane) {
+  const int i = lane & 15;
+  const int col = c0 + 4 * (i & 3);
+  const int ra = r0 + (i >> 2), rb = ra + 4;
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + wswz(ra, col >> 3) + (col & 7)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + wswz(rb, col >> 3) + (col & 7)));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// Direct HBM/L2 -> LDS copy of 1 KB: lane L of the wave moves the 16 bytes at
+// src (its own address) to lds_base + 16 L. lds_base must be wave-uniform.
+__device__ __forceinline__ void dma16(const uint16_t* src, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds_base), 16, 0, 0);
+}
 
 template <int DT, bool FWD>
-__global__ __launch_bounds__(256, 3) void bell_gemm_kernel(
+__global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
     const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ in_blk,
     const int32_t* __restrict__ t_vblk, const int32_t* __restrict__ order,
     const uint16_t* __restrict__ bias, int epi, uint16_t* __restrict__ Y, int64_t ldy, int M,
     int n_out, int width, int n_mtiles, int per_xcd) {
-  // Main loop: the activation tile (kBM x 64, swizzled) and the weight tile
-  // (64 x kPitch). Epilogue: four per-wave 64x64 staging tiles over the same
-  // memory.
+  // Two buffers, each the activation tile (kBM x 64, xswz) and the weight
+  // block (64 x 64, wswz); the epilogue's four per-wave 64x64 staging tiles
+  // (pitch kPitch) reuse the same memory.
+  // The buffers are separate arrays so the compiler can tell that copies into
+  // one do not alias reads of the other (and does not wait for them).
   constexpr int kXElems = kBM * 64;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[kXElems + kTileElems];
-  // The workgroup's list of non-zero blocks, copied once: activation block
-  // index and weight block index per entry.
-  __shared__ int32_t s_in[kMaxList];
-  __shared__ int32_t s_vb[kMaxList];
-  uint16_t* const xt = smem;
-  uint16_t* const wt = smem + kXElems;
+  constexpr int kBufElems = kXElems + 4096;
+  static_assert(kBufElems >= 4 * kTileElems, "staging tiles must fit");
+  __shared__ __attribute__((aligned(16))) uint16_t smem0[kBufElems];
+  __shared__ __attribute__((aligned(16))) uint16_t smem1[kBufElems];
 
   const int logical = xcd_logical_id(per_xcd);
   if (logical >= n_mtiles * n_out) return;
@@ -88,34 +117,54 @@ __global__ __launch_bounds__(256, 3) void bell_gemm_kernel(
   const int m_tile0 = mtile * kBM;
   const int m_base = m_tile0 + wave * 64;
 
-  for (int i = tid; i < e1 - e0; i += 256) {
-    s_in[i] = in_blk[e0 + i];
-    s_vb[i] = FWD ? t_vblk[e0 + i] : e0 + i;
-  }
-
-  // Coalesced tile loads: thread t moves 16-byte chunk (t & 7) of rows
-  // 32j + (t >> 3), j = 0..7, of the activation tile, and of rows t >> 3 and
-  // 32 + (t >> 3) of the weight block. Rows past M are clamped onto row M-1:
-  // they load valid memory and their results are never stored.
-  const int lrow = tid >> 3, lch = tid & 7;
+  // Tile copies, eight 1 KB wave instructions for the wave's own 64
+  // activation rows and two for rows 16w..16w+15 of the weight block. Lane L
+  // of an instruction covering rows R..R+7 fills LDS chunk position L & 7 of
+  // row R + L / 8, so it fetches the global chunk that the swizzle stores
+  // there; the eight lanes of a row still read its 128 bytes contiguously.
+  // Activation rows past M are clamped onto row M-1 (valid memory, results
+  // never stored).
+  const int drow = lane >> 3, dpos = lane & 7;
   const uint16_t* xsrc[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    xsrc[j] = A + static_cast<int64_t>(min(m_tile0 + 32 * j + lrow, M - 1)) * lda + 8 * lch;
-  u32x4 xr[8], wr[2];
-  auto gload = [&](int i) {
-    const int64_t col = static_cast<int64_t>(s_in[i]) * 64;
-    const uint16_t* wsrc = vals + static_cast<int64_t>(s_vb[i]) * 4096 + tid * 8;
-    wr[0] = ldg16(wsrc);
-    wr[1] = ldg16(wsrc + 2048);
+  for (int j = 0; j < 8; ++j) {
+    const int row = wave * 64 + 8 * j + drow;
+    const int chunk = dpos ^ ((row >> 1) & 7);
+    xsrc[j] = A + static_cast<int64_t>(min(m_tile0 + row, M - 1)) * lda + 8 * chunk;
+  }
+  int woff[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) xr[j] = ldg16(xsrc[j] + col);
+  for (int j = 0; j < 2; ++j) {
+    const int row = wave * 16 + 8 * j + drow;
+    const int a = (row >> 1) & 7;
+    woff[j] = row * 64 + 8 * (dpos ^ (((a & 1) << 2) | (a >> 1)));
+  }
+  auto dma_tiles = [&](int blk_in, int blk_w, uint16_t* buf) {
+    const int64_t col = static_cast<int64_t>(blk_in) * 64;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(xsrc[j] + col, buf + (wave * 64 + 8 * j) * 64);
+    const uint16_t* wsrc = vals + static_cast<int64_t>(blk_w) * 4096;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) dma16(wsrc + woff[j], buf + kXElems + (wave * 16 + 8 * j) * 64);
   };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sts16(xt + xswz(32 * j + lrow, lch), xr[j]);
-    sts16(wt + lrow * kPitch + lch * 8, wr[0]);
-    sts16(wt + (32 + lrow) * kPitch + lch * 8, wr[1]);
+  // Block indices of the list, 64 entries at a time in a VGPR pair (lane L
+  // holds entry base + L) and taken out with readlane: loads issued after the
+  // tile copies cannot use the scalar cache, and a vector load there would
+  // make the next wait cover the copies too. Indices are fetched right after
+  // a barrier, when no copy is in flight, so a window reload (once per 64
+  // entries) waits only for itself.
+  const int n_list = e1 - e0;
+  int win_base = 0, win_in = 0, win_w = 0;
+  auto load_window = [&](int base) {
+    win_base = base;
+    const int i = min(base + lane, n_list - 1);
+    win_in = in_blk[e0 + i];
+    win_w = FWD ? t_vblk[e0 + i] : e0 + i;
+  };
+  auto fetch_idx = [&](int i, int& bin, int& bw) {
+    if (i - win_base >= 64) load_window(i & ~63);
+    bin = __builtin_amdgcn_readlane(win_in, i - win_base);
+    bw = __builtin_amdgcn_readlane(win_w, i - win_base);
   };
 
   f32x16 acc[2][2];
@@ -128,25 +177,26 @@ __global__ __launch_bounds__(256, 3) void bell_gemm_kernel(
   // reads of the swizzled tile) and the weight block (A operand: transpose
   // reads for the forward, where W is N-contiguous but the reduction runs over
   // K; plain 16-byte reads for dX, whose reduction runs over N).
-  auto read_ops = [&](u32x4(&xa)[2], u32x4(&wf)[2], int kk) {
+  auto read_ops = [&](u32x4(&xa)[2], u32x4(&wf)[2], const uint16_t* buf, int kk) {
+    const uint16_t* wt = buf + kXElems;
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi) xa[mi] = lds16(xt + xswz(wave * 64 + 32 * mi + l32, 2 * kk + h));
+    for (int mi = 0; mi < 2; ++mi) xa[mi] = lds16(buf + xswz(wave * 64 + 32 * mi + l32, 2 * kk + h));
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
       if constexpr (FWD)
-        wf[ni] = lds_read_tr8(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+        wf[ni] = lds_read_tr8_wswz(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
       else
-        wf[ni] = lds16(wt + (32 * ni + l32) * kPitch + 16 * kk + 8 * h);
+        wf[ni] = lds16(wt + wswz(32 * ni + l32, 2 * kk + h));
     }
   };
   // The reads of k-step kk+1 are issued before the MFMAs of k-step kk, and
   // the scheduling group barriers keep that order.
-  auto compute = [&]() {
+  auto compute = [&](const uint16_t* buf) {
     u32x4 xa[2][2], wf[2][2];
-    read_ops(xa[0], wf[0], 0);
+    read_ops(xa[0], wf[0], buf, 0);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], kk + 1);
+      if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], buf, kk + 1);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -162,31 +212,47 @@ __global__ __launch_bounds__(256, 3) void bell_gemm_kernel(
     }
   };
 
-  // One LDS copy of the tiles: entry i+1's tiles are loaded into registers
-  // while entry i is computed, then written once every wave is done reading.
-  __syncthreads();  // index lists visible
+  // Double-buffered pipeline with one barrier per list entry: the copies of
+  // entry i+1 fly into the idle buffer while entry i is computed; the barrier
+  // (which waits for this wave's copies) then publishes the new buffer and
+  // retires the old one.
   const int n = e1 - e0;
   if (n > 0) {
-    gload(0);
-    sstore();
+    int bin, bw;
+    load_window(0);
+    fetch_idx(0, bin, bw);
+    dma_tiles(bin, bw, smem0);
     __syncthreads();
-    for (int i = 0; i < n; ++i) {
-      const bool more = i + 1 < n;
-      if (more) gload(i + 1);
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      // entry i from buffer 0 while entry i+1 flies into buffer 1
+      fetch_idx(i + 1, bin, bw);
       __builtin_amdgcn_sched_barrier(0);
-      compute();
+      dma_tiles(bin, bw, smem1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(smem0);
       __builtin_amdgcn_sched_barrier(0);
       __syncthreads();
-      if (more) {
-        sstore();
-        __syncthreads();
+      // entry i+1 from buffer 1 while entry i+2 (if any) flies into buffer 0
+      if (i + 2 < n) {
+        fetch_idx(i + 2, bin, bw);
+        __builtin_amdgcn_sched_barrier(0);
+        dma_tiles(bin, bw, smem0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      compute(smem1);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    }
+    if (i < n) {
+      compute(smem0);
+      __syncthreads();
     }
   }
 
   // Epilogue: bias, activation, conversion, then pack through this wave's LDS
   // staging tile and store 128-byte row segments.
-  uint16_t* stage = smem + wave * kTileElems;
+  uint16_t* stage = smem0 + wave * kTileElems;
   const int64_t col0 = static_cast<int64_t>(ob) * 64;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
@@ -395,7 +461,6 @@ extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
   if (st != TMAC_OK) return st;
   if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
   if (epi != TMAC_EPI_NONE && epi != TMAC_EPI_GELU) return TMAC_ERR_VALUE;
-  if (n_brow > kMaxList) return TMAC_ERR_SHAPE;  // a column's list has up to n_brow entries
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (ldx < K || ldy < N) return TMAC_ERR_SHAPE;
   if (!aligned16(d_X) || !aligned16(d_vals) || !aligned16(d_Y) || (ldx % 8) || (ldy % 8))
@@ -428,7 +493,6 @@ extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
   if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
-  if (width > kMaxList) return TMAC_ERR_SHAPE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (lddy < N || lddx < K) return TMAC_ERR_SHAPE;
   if (!aligned16(d_dY) || !aligned16(d_vals) || !aligned16(d_dX) || (lddy % 8) || (lddx % 8))
