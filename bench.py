@@ -58,17 +58,34 @@ def band_pairs(S: int, w: int, Np: int) -> int:
 
 
 def timed(launch, steps: int, warmup: int, stream) -> float:
-    """Mean ms per launch over `steps` back-to-back launches on `stream`."""
+    """Mean ms per launch: each of `steps` back-to-back launches on `stream` is
+    bracketed by its own pair of HIP events (torch.cuda.Event records on the
+    stream it is given, which is the stream the kernels are launched on), so
+    the figure is the kernel's own duration, as a kernel trace reports it."""
     for _ in range(warmup):
         launch()
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for a, b in ev:
+        a.record(stream)
+        launch()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / steps
+
+
+def timed_wall(launch, steps: int, stream) -> float:
+    """ms per launch over `steps` back-to-back launches between two events
+    (includes the gaps between launches)."""
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
     for _ in range(steps):
         launch()
-    end.record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    return a.elapsed_time(b) / steps
 
 
 def gen(shape, seed, scale=1.0, dtype=torch.bfloat16):
@@ -224,11 +241,11 @@ def cpu_baseline(spmm) -> dict:
         if threadpool_info:
             used = max([p.get("num_threads", 1) for p in threadpool_info()] or [cores])
         reps, t0 = 0, time.perf_counter()
-        while True:
+        while True:  # about 12 s of CPU work
             _ = Xs @ W
             reps += 1
             el = time.perf_counter() - t0
-            if el > 10.0 or reps >= 40:
+            if el > 12.0:
                 break
     eff = 2 * ob_rows * c["n_brow"] * c["width"] * BS * BS
     return {"value": round(eff * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(used),
@@ -237,13 +254,13 @@ def cpu_baseline(spmm) -> dict:
                       f"in {el:.1f} s; effective (stored-block) FLOPs counted, as on the GPU"}
 
 
-def load_traffic() -> dict | None:
+def load_traffic(kind: str) -> float | None:
+    """HBM bytes per launch of the kernel behind `kind`, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json), or None."""
     p = ROOT / "profiles" / "traffic.json"
-    if not p.exists():
-        return None
     try:
-        return json.loads(p.read_text())
-    except (ValueError, OSError):
+        return float(json.loads(p.read_text())[kind]["traffic_bytes"])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -280,7 +297,7 @@ def main() -> int:
         spmm = setup_spmm(dev)
         ms = timed(spmm["launch"], K, W, stream)
         out["spmm"] = dict(ms=ms, tflops=spmm["flops"] / ms / 1e9, flops=spmm["flops"],
-                           bytes=spmm["bytes"])
+                           bytes=spmm["bytes"], wall_ms=timed_wall(spmm["launch"], K, stream))
     if args.mode in ("all", "attn"):
         att = setup_attn(dev)
         ms = timed(att["launch"], K, W, stream)
@@ -304,7 +321,7 @@ def main() -> int:
     s = out["spmm"]
     a = out["attn"]
     dense_ms = min(a["sdpa_masked_ms"], a["bmm_softmax_bmm_ms"])
-    traffic = load_traffic()
+    traffic = load_traffic("spmm")
     line = {
         "metric": METRIC,
         "value": round(s["tflops"], 3),
@@ -325,8 +342,9 @@ def main() -> int:
                    "seed": CFG2["seed"]},
         "roofline": {"bound": "mfma", "achieved": round(s["tflops"], 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(s["tflops"] / PEAK_BF16_TFLOPS, 4),
-                     "traffic": (traffic or {}).get("bell_fwd_cfg2_bytes")},
+                     "traffic": traffic},
         "secondary": {
+            "spmm_ms_back_to_back": round(s["wall_ms"], 5),
             "windowed_attn_fwd_tokens_per_s": round(a["tokens_per_s"], 1),
             "windowed_attn_fwd_ms": round(a["ms"], 5),
             "windowed_attn_fwd_tflops_algorithmic": round(a["tflops"], 3),
