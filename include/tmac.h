@@ -151,7 +151,9 @@ int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, int64_t lddy
  * TMAC_PATTERN_BAND and the effective mask of BlockSparseAttention
  * (attn/block_sparse_attention.py:277-334, block size `block_size`) for
  * TMAC_PATTERN_BLOCKWIN. Raises TMAC_ERR_VALUE where build_band_mask raises
- * ValueError (n_persistent >= S, window < 0). */
+ * ValueError (n_persistent >= S, window < 0); the block-window pattern also
+ * accepts n_persistent == S (a sequence of persistent tokens only), as
+ * BlockSparseAttention does (attn/block_sparse_attention.py:250-267). */
 int tmac_wattn_tile_kinds(int S, int window, int n_persistent, int causal,
                           int pattern, int block_size, int tq, int tk,
                           uint8_t* h_kind);
@@ -189,6 +191,24 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
                    int causal, int pattern, int block_size, float scale,
                    const int32_t* d_row_ptr, const int32_t* d_entries,
                    int dtype, void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Causal depthwise convolution (device).                                     */
+/* ------------------------------------------------------------------------- */
+
+/* out[b, t, c] = Σ_{j<ksize} w[c][j] · in[b, t - (ksize-1) + j, c], with rows
+ * before t = 0 taken as zero; fp32 accumulation, output in the input dtype.
+ * Replaces BlockSparseAttention's causal depthwise Conv1d on q, k and v
+ * (nn.Conv1d(d, d, ksize, padding=ksize-1, groups=d, bias=False) on the
+ * [B, d, T] transpose, trimmed to T outputs: attn/block_sparse_attention.py
+ * :87-98, :227-241), on the [B, T, C] layout without transposes; q, k and v
+ * go through one launch as C = 3d channels of the fused projection.
+ * in / out: [B, T, C] with row strides ld_in / ld_out (elements; batch stride
+ * T * ld); w: [C, ksize] in the same dtype. 1 <= ksize <= 8; C and the row
+ * strides multiples of 8 (16-bit) or 4 (fp32); in and out 16-byte aligned and
+ * not overlapping. dtype: TMAC_F32, TMAC_BF16 or TMAC_F16. */
+int tmac_dwconv_causal(const void* d_in, int64_t ld_in, const void* d_w, void* d_out,
+                       int64_t ld_out, int B, int T, int C, int ksize, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -62,3 +62,78 @@ def allowed_pairs(mask: np.ndarray) -> int:
 def attention_flops(pairs: int, batch_heads: int, dh: int = 64) -> int:
     """4·dh per allowed pair (QKᵀ and PV multiply-adds) over all (b, h)."""
     return 4 * dh * pairs * batch_heads
+
+
+def causal_dwconv(x: np.ndarray, w: np.ndarray, dtype=np.float64) -> np.ndarray:
+    """out[b, t, c] = sum_j w[c, j] * x[b, t - (k-1) + j, c] (x before t = 0 is zero).
+
+    The function of BlockSparseAttention's Conv1d(d, d, k, padding=k-1, groups=d,
+    bias=False) on the [B, d, T] transpose, trimmed to T outputs
+    (attn/block_sparse_attention.py:87-98, :227-241), written tap by tap.
+    """
+    x = np.asarray(x, dtype=dtype)
+    w = np.asarray(w, dtype=dtype)
+    if w.ndim == 3:
+        w = w[:, 0, :]
+    B, T, C = x.shape
+    k = w.shape[1]
+    out = np.zeros_like(x)
+    for j in range(k):
+        shift = k - 1 - j          # tap j reads row t - shift
+        if shift >= T:
+            continue
+        out[:, shift:, :] += w[None, None, :, j] * x[:, :T - shift, :]
+    return out
+
+
+def block_sparse_attention_module(x: np.ndarray, w_qkv: np.ndarray, w_out: np.ndarray,
+                                  n_heads: int, window_size: int, block_size: int,
+                                  n_persistent: int, causal: bool = True, conv=None,
+                                  dtype=np.float64) -> np.ndarray:
+    """BlockSparseAttention.forward (no dropout), re-executed step by step.
+
+    attn/block_sparse_attention.py:222 (qkv projection), :227-241 (causal
+    depthwise convs on q, k, v; conv = (w_q, w_k, w_v) or None when use_conv is
+    False), :245-247 (heads), :250-267 (persistent / sequence split), :277-286
+    (persistent queries attend to all keys, no mask), :289-334 (per query block:
+    context = persistent keys + sequence keys [max(0, b0 - w), b_end), the causal
+    mask of :149-161 on the sequence part when causal), :337-343 (merge, out_proj).
+    x [B, T, d]; w_qkv [3d, d], w_out [d, d] in nn.Linear's [out, in] layout.
+    """
+    x = np.asarray(x, dtype=dtype)
+    B, T, d = x.shape
+    dh = d // n_heads
+    scale = 1.0 / np.sqrt(dh)
+    qkv = x @ np.asarray(w_qkv, dtype=dtype).T
+    q, k, v = np.split(qkv, 3, axis=-1)
+    if conv is not None:
+        q, k, v = (causal_dwconv(t, cw, dtype) for t, cw in zip((q, k, v), conv))
+    q, k, v = (t.reshape(B, T, n_heads, dh).transpose(0, 2, 1, 3) for t in (q, k, v))
+    Np = n_persistent
+    out = np.zeros((B, n_heads, T, dh), dtype=dtype)
+
+    def attend(qb, kc, vc, mask):
+        s = (qb @ np.swapaxes(kc, -1, -2)) * scale
+        if mask is not None:
+            s = np.where(mask, s, -np.inf)
+        s = s - s.max(axis=-1, keepdims=True)
+        p = np.exp(s)
+        p = p / p.sum(axis=-1, keepdims=True)
+        return p @ vc
+
+    if Np > 0:
+        out[:, :, :Np] = attend(q[:, :, :Np], k, v, None)
+    q_seq, k_seq, v_seq = q[:, :, Np:], k[:, :, Np:], v[:, :, Np:]
+    t_seq = T - Np
+    for b0 in range(0, t_seq, block_size):
+        b1 = min(b0 + block_size, t_seq)
+        c0, c1 = max(0, b0 - window_size), b1
+        kc = np.concatenate([k[:, :, :Np], k_seq[:, :, c0:c1]], axis=2)
+        vc = np.concatenate([v[:, :, :Np], v_seq[:, :, c0:c1]], axis=2)
+        mask = None
+        if causal:
+            mask = np.ones((b1 - b0, Np + c1 - c0), dtype=bool)
+            mask[:, Np:] = np.arange(b0, b1)[:, None] >= np.arange(c0, c1)[None, :]
+        out[:, :, Np + b0:Np + b1] = attend(q_seq[:, :, b0:b1], kc, vc, mask)
+    o = out.transpose(0, 2, 1, 3).reshape(B, T, d)
+    return o @ np.asarray(w_out, dtype=dtype).T

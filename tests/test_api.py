@@ -156,3 +156,25 @@ def test_ops_fake_shapes():
         q = torch.empty(2, 3, 100, 64, dtype=torch.bfloat16)
         from titans_core.kernels.window_attn import window_attn_fwd
         assert window_attn_fwd(q, q, q, 8, 2, True, 0, 64, 0.125).shape == (2, 100, 3, 64)
+
+
+def test_block_sparse_attention_construction_and_state_dict():
+    m = tc.BlockSparseAttention(640, 10, window_size=512, block_size=64, n_persistent=16)
+    sd = m.state_dict()
+    # the reference's keys and shapes (attn/block_sparse_attention.py:84-101)
+    assert set(sd) == {"qkv_proj.weight", "conv_q.weight", "conv_k.weight", "conv_v.weight",
+                       "out_proj.weight"}
+    assert sd["qkv_proj.weight"].shape == (1920, 640) and sd["conv_q.weight"].shape == (640, 1, 4)
+    assert set(tc.BlockSparseAttention(128, 2, use_conv=False).state_dict()) == {
+        "qkv_proj.weight", "out_proj.weight"}
+    with pytest.raises(ValueError, match="divisible"):
+        tc.BlockSparseAttention(100, 3)
+    cfg = tc.TitanMACConfig()
+    m2 = tc.create_block_sparse_attention(cfg)
+    assert (m2.block_size, m2.window_size, m2.n_persistent, m2.n_heads) == (64, 512, 16, 10)
+
+
+def test_block_sparse_attention_refuses_cpu_tensors():
+    m = tc.BlockSparseAttention(128, 2, window_size=16, block_size=16, n_persistent=2)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m(torch.randn(1, 20, 128))

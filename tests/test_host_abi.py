@@ -165,3 +165,27 @@ def test_wattn_fwd_argument_errors(lib):
     assert lib.tmac_wattn_fwd(*a) == -5           # head stride not 16-byte aligned
     a = list(base); a[19] = None
     assert lib.tmac_wattn_fwd(*a) == -1
+
+
+def test_dwconv_argument_errors(lib):
+    # in, ld_in, w, out, ld_out, B, T, C, ksize, dtype, stream
+    ok = [FAKE, 1920, FAKE, FAKE, 1920, 8, 4096, 1920, 4, 1, None]
+    bad = list(ok); bad[0] = None
+    assert lib.tmac_dwconv_causal(*bad) == -1
+    bad = list(ok); bad[8] = 9
+    assert lib.tmac_dwconv_causal(*bad) == -8      # ksize above 8
+    bad = list(ok); bad[7] = 1921
+    assert lib.tmac_dwconv_causal(*bad) == -2      # C not a multiple of the 16-byte vector
+    bad = list(ok); bad[1] = 1000
+    assert lib.tmac_dwconv_causal(*bad) == -2      # row stride < C
+    bad = list(ok); bad[0] = MISALIGNED
+    assert lib.tmac_dwconv_causal(*bad) == -5
+    bad = list(ok); bad[9] = 7
+    assert lib.tmac_dwconv_causal(*bad) == -4
+
+
+def test_only_persistent_tokens_allowed_for_blockwin_only():
+    k = tile_kinds(24, 8, 24, True, "blockwin", 16, tq=8, tk=8)
+    assert k.shape == (3, 3) and (k == 1).all()     # every pair allowed
+    with pytest.raises(ValueError):
+        tile_kinds(24, 8, 24, True, "band", 64)

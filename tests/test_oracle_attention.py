@@ -1,5 +1,8 @@
-"""Pins of oracle.attention: torch's SDPA (a library routine) with the same mask,
-and closed forms (one allowed key, constant scores)."""
+"""Pins of oracle.attention: torch's SDPA and conv1d (library routines), closed
+forms (one allowed key, constant scores), and golden vectors of the reference's
+own BlockSparseAttention module."""
+from pathlib import Path
+
 import numpy as np
 import pytest
 import torch
@@ -66,3 +69,54 @@ def test_module_forward_matches_torch_composition():
     o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=add)
     want = (o.transpose(1, 2).reshape(B, T, d) @ torch.from_numpy(wo).T).numpy()
     assert np.allclose(got, want, rtol=1e-10, atol=1e-12)
+
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "bsa_golden.npz"
+
+
+def _bsa_case(z, name):
+    B, T, d, H, w, bs, Np, causal, use_conv = (int(v) for v in z[f"{name}/config"])
+    conv = None
+    if use_conv:
+        conv = tuple(z[f"{name}/w_conv_{t}"] for t in "qkv")
+    return dict(x=z[f"{name}/x"], w_qkv=z[f"{name}/w_qkv"], w_out=z[f"{name}/w_out"], n_heads=H,
+                window_size=w, block_size=bs, n_persistent=Np, causal=bool(causal), conv=conv), z[f"{name}/y"]
+
+
+def test_block_sparse_module_matches_reference_golden_vectors():
+    """The restatement reproduces the reference module's own outputs
+    (tests/golden/make_bsa_golden.py ran the reference BlockSparseAttention)."""
+    z = np.load(GOLDEN)
+    names = sorted({k.split("/")[0] for k in z.files})
+    assert len(names) == 5
+    for name in names:
+        kw, y = _bsa_case(z, name)
+        got = oa.block_sparse_attention_module(**kw)
+        np.testing.assert_allclose(got, y, rtol=1e-4, atol=1e-6, err_msg=name)
+
+
+def test_causal_dwconv_is_torch_conv1d_trimmed():
+    """Against the library routine: Conv1d(groups=C, padding=k-1) on the [B, C, T]
+    transpose, first T outputs."""
+    rng = np.random.default_rng(3)
+    for T, C, k in [(17, 8, 4), (3, 5, 4), (40, 6, 1), (9, 4, 7)]:
+        x = rng.standard_normal((2, T, C))
+        w = rng.standard_normal((C, k))
+        want = torch.nn.functional.conv1d(torch.from_numpy(x).transpose(1, 2), torch.from_numpy(w)[:, None, :],
+                                          padding=k - 1, groups=C)[:, :, :T].transpose(1, 2).numpy()
+        np.testing.assert_allclose(oa.causal_dwconv(x, w), want, rtol=1e-12, atol=1e-12)
+
+
+def test_block_sparse_module_is_sdpa_with_blockwin_mask():
+    """The block loop equals one masked attention over the effective block-window mask."""
+    z = np.load(GOLDEN)
+    kw, _ = _bsa_case(z, "two_heads_partial_block")
+    x, H = kw["x"], kw["n_heads"]
+    B, T, d = x.shape
+    dh = d // H
+    qkv = x.astype(np.float64) @ kw["w_qkv"].T.astype(np.float64)
+    q, k, v = (oa.causal_dwconv(t, cw) for t, cw in zip(np.split(qkv, 3, axis=-1), kw["conv"]))
+    q, k, v = (t.reshape(B, T, H, dh).transpose(0, 2, 1, 3) for t in (q, k, v))
+    mask = om.blockwin_mask(T, kw["window_size"], kw["block_size"], kw["n_persistent"], kw["causal"])
+    o = oa.masked_attention(q, k, v, mask).transpose(0, 2, 1, 3).reshape(B, T, d)
+    np.testing.assert_allclose(o @ kw["w_out"].T, oa.block_sparse_attention_module(**kw), rtol=1e-10, atol=1e-12)

@@ -1,0 +1,183 @@
+// Causal depthwise 1-D convolution over the sequence axis, for gfx950.
+//
+//   out[b, t, c] = Σ_{j=0}^{k-1} w[c, j] · in[b, t - (k-1) + j, c]   (in[b, <0, c] = 0)
+//
+// This is what BlockSparseAttention applies to q, k and v after the fused
+// projection: nn.Conv1d(d, d, k, padding=k-1, groups=d, bias=False) on the
+// [B, d, T] transpose, trimmed to the first T outputs
+// (attn/block_sparse_attention.py:87-98, 227-241). Here it runs directly on
+// the [B, T, C] activation layout (C = 3d: q, k and v channels in one launch),
+// so no transposes are needed.
+//
+// Memory-bound stencil: each thread owns one 16-byte vector of channels and a
+// chunk of 64 consecutive positions, keeps the last k input rows in registers
+// (fp32) and writes each output row once; consecutive threads read consecutive
+// 16-byte pieces of a row, so every row is read with full coalescing. The
+// halo (k-1 rows before the chunk) is the only re-read.
+
+#include "tmac_device.h"
+
+using namespace tmac;
+
+namespace {
+
+constexpr int kChunk = 64;  // positions per thread
+
+template <int DT>
+struct Vec;
+
+template <>
+struct Vec<TMAC_F32> {
+  static constexpr int N = 4;
+  static __device__ __forceinline__ void load(const void* p, float (&v)[4]) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(p);
+    v[0] = x.x;
+    v[1] = x.y;
+    v[2] = x.z;
+    v[3] = x.w;
+  }
+  static __device__ __forceinline__ void store(void* p, const float (&v)[4]) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  }
+};
+
+template <int DT16>
+struct Vec16 {
+  static constexpr int N = 8;
+  static __device__ __forceinline__ void load(const void* p, float (&v)[8]) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(p);
+    const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = Mfma<DT16>::to_f32(static_cast<uint16_t>(w[i] & 0xffff));
+      v[2 * i + 1] = Mfma<DT16>::to_f32(static_cast<uint16_t>(w[i] >> 16));
+    }
+  }
+  static __device__ __forceinline__ void store(void* p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = static_cast<uint32_t>(Mfma<DT16>::from_f32(v[2 * i])) |
+             (static_cast<uint32_t>(Mfma<DT16>::from_f32(v[2 * i + 1])) << 16);
+    *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
+  }
+};
+template <>
+struct Vec<TMAC_BF16> : Vec16<TMAC_BF16> {};
+template <>
+struct Vec<TMAC_F16> : Vec16<TMAC_F16> {};
+
+template <int DT, int KS>
+__global__ __launch_bounds__(256) void dwconv_causal_kernel(const uint8_t* __restrict__ in,
+                                                            int64_t ld_in, const uint8_t* __restrict__ w,
+                                                            uint8_t* __restrict__ out, int64_t ld_out,
+                                                            int T, int C, int n_chunks) {
+  using V = Vec<DT>;
+  constexpr int N = V::N;
+  constexpr int E = DT == TMAC_F32 ? 4 : 2;  // bytes per element
+  const int vc = blockIdx.y * 256 + threadIdx.x;
+  if (vc * N >= C) return;
+  const int b = blockIdx.x / n_chunks;
+  const int t0 = (blockIdx.x - b * n_chunks) * kChunk;
+  const int c0 = vc * N;
+
+  // Taps of this thread's channels: wt[j][i] = w[c0 + i][j] (weights are
+  // [C, KS], so the KS taps of one channel are contiguous).
+  float wt[KS][N];
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      const uint8_t* p = w + (static_cast<int64_t>(c0 + i) * KS + j) * E;
+      if constexpr (DT == TMAC_F32)
+        wt[j][i] = *reinterpret_cast<const float*>(p);
+      else
+        wt[j][i] = Mfma<DT>::to_f32(*reinterpret_cast<const uint16_t*>(p));
+    }
+
+  const uint8_t* ib = in + (static_cast<int64_t>(b) * T) * ld_in * E + static_cast<int64_t>(c0) * E;
+  uint8_t* ob = out + (static_cast<int64_t>(b) * T) * ld_out * E + static_cast<int64_t>(c0) * E;
+  // ring[j] holds input row t - (KS-1) + j for the row t being produced.
+  float ring[KS][N];
+#pragma unroll
+  for (int j = 0; j < KS - 1; ++j) {
+    const int t = t0 - (KS - 1) + j;
+    if (t >= 0)
+      V::load(ib + static_cast<int64_t>(t) * ld_in * E, ring[j]);
+    else
+#pragma unroll
+      for (int i = 0; i < N; ++i) ring[j][i] = 0.f;
+  }
+  const int t1 = min(t0 + kChunk, T);
+  for (int t = t0; t < t1; ++t) {
+    V::load(ib + static_cast<int64_t>(t) * ld_in * E, ring[KS - 1]);
+    float o[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < KS; ++j) acc = fmaf(wt[j][i], ring[j][i], acc);
+      o[i] = acc;
+    }
+    V::store(ob + static_cast<int64_t>(t) * ld_out * E, o);
+#pragma unroll
+    for (int j = 0; j < KS - 1; ++j)
+#pragma unroll
+      for (int i = 0; i < N; ++i) ring[j][i] = ring[j + 1][i];
+  }
+}
+
+template <int DT>
+int launch_dwconv(const void* d_in, int64_t ld_in, const void* d_w, void* d_out, int64_t ld_out,
+                  int B, int T, int C, int ks, hipStream_t s) {
+  constexpr int N = Vec<DT>::N;
+  const int n_vec = C / N;
+  const int n_chunks = (T + kChunk - 1) / kChunk;
+  const int64_t gx = static_cast<int64_t>(B) * n_chunks;
+  const int gy = (n_vec + 255) / 256;
+  if (gx > (1ll << 31) - 1 || gy > 65535) return TMAC_ERR_SHAPE;
+  const dim3 grid(static_cast<unsigned>(gx), gy);
+  const auto* in = static_cast<const uint8_t*>(d_in);
+  const auto* w = static_cast<const uint8_t*>(d_w);
+  auto* out = static_cast<uint8_t*>(d_out);
+#define TMAC_DWCONV_CASE(KS)                                                                   \
+  case KS:                                                                                     \
+    hipLaunchKernelGGL((dwconv_causal_kernel<DT, KS>), grid, dim3(256), 0, s, in, ld_in, w, out, \
+                       ld_out, T, C, n_chunks);                                                \
+    break;
+  switch (ks) {
+    TMAC_DWCONV_CASE(1)
+    TMAC_DWCONV_CASE(2)
+    TMAC_DWCONV_CASE(3)
+    TMAC_DWCONV_CASE(4)
+    TMAC_DWCONV_CASE(5)
+    TMAC_DWCONV_CASE(6)
+    TMAC_DWCONV_CASE(7)
+    TMAC_DWCONV_CASE(8)
+    default:
+      return TMAC_ERR_VALUE;
+  }
+#undef TMAC_DWCONV_CASE
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int tmac_dwconv_causal(const void* d_in, int64_t ld_in, const void* d_w, void* d_out,
+                                  int64_t ld_out, int B, int T, int C, int ksize, int dtype,
+                                  void* stream) {
+  if (!d_in || !d_w || !d_out) return TMAC_ERR_NULL;
+  if (B <= 0 || T <= 0 || C <= 0) return TMAC_ERR_SHAPE;
+  if (ksize < 1 || ksize > 8) return TMAC_ERR_VALUE;
+  if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  const int vec = dtype == TMAC_F32 ? 4 : 8;
+  if (C % vec || ld_in < C || ld_out < C) return TMAC_ERR_SHAPE;
+  if ((ld_in % vec) || (ld_out % vec) || !aligned16(d_in) || !aligned16(d_out)) return TMAC_ERR_ALIGN;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == TMAC_F32) return launch_dwconv<TMAC_F32>(d_in, ld_in, d_w, d_out, ld_out, B, T, C, ksize, s);
+  if (dtype == TMAC_BF16) return launch_dwconv<TMAC_BF16>(d_in, ld_in, d_w, d_out, ld_out, B, T, C, ksize, s);
+  return launch_dwconv<TMAC_F16>(d_in, ld_in, d_w, d_out, ld_out, B, T, C, ksize, s);
+}

@@ -180,7 +180,9 @@ inline int span_count(const RowSpan& sp, int k0, int k1) {
 int check_mask_args(int S, int window, int n_persistent, int pattern, int block_size) {
   if (S <= 0) return TMAC_ERR_SHAPE;
   if (n_persistent < 0) return TMAC_ERR_VALUE;
-  if (n_persistent >= S) return TMAC_ERR_VALUE;  // windowed_attention.py:97-100
+  // build_band_mask raises for n_persistent >= S (windowed_attention.py:97-100);
+  // BlockSparseAttention accepts a sequence made only of persistent tokens.
+  if (n_persistent > S || (pattern == TMAC_PATTERN_BAND && n_persistent == S)) return TMAC_ERR_VALUE;
   if (window < 0) return TMAC_ERR_VALUE;         // windowed_attention.py:102-103
   if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
   if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;

@@ -335,8 +335,9 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
     return TMAC_ERR_NULL;
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
   if (dh != 64) return TMAC_ERR_SHAPE;
-  if (n_persistent < 0 || n_persistent >= S || window < 0) return TMAC_ERR_VALUE;
   if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
+  if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
+  if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
   if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
   if (!(scale > 0.f)) return TMAC_ERR_VALUE;
   if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;

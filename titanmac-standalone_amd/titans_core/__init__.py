@@ -6,13 +6,16 @@ Drop-in Python API of the reference's hot path over hand-written HIP kernels:
 ``TitanMACConfig``. Importing the package does not load the GPU library; the
 first kernel call does, and raises if libtmac.so is missing.
 """
-from .attn import WindowConfig, WindowedAttention, build_band_mask
+from .attn import (BlockSparseAttention, WindowConfig, WindowedAttention, build_band_mask,
+                   create_block_sparse_attention)
 from .blocks import MLPBlock
 from .config import TITANS_VARIANTS, TitanMACConfig
-from .kernels import BlockELLLinear, BlockELLPattern, block_ell_mm, windowed_attention
+from .kernels import (BlockELLLinear, BlockELLPattern, block_ell_mm, causal_dwconv,
+                      windowed_attention)
 
 __version__ = "0.1.0"
 
 __all__ = ["TitanMACConfig", "TITANS_VARIANTS", "WindowedAttention", "WindowConfig",
-           "build_band_mask", "MLPBlock", "BlockELLLinear", "BlockELLPattern", "block_ell_mm",
+           "build_band_mask", "BlockSparseAttention", "create_block_sparse_attention", "MLPBlock",
+           "BlockELLLinear", "BlockELLPattern", "block_ell_mm", "causal_dwconv",
            "windowed_attention"]

@@ -1,6 +1,7 @@
 """HIP kernels of the TitanMAC sparse hot path (libtmac.so, gfx950), with their torch ops."""
 from .block_ell import BlockELLLinear, BlockELLPattern, block_ell_mm
+from .conv import causal_dwconv
 from .window_attn import tile_kinds, windowed_attention, work_list
 
-__all__ = ["BlockELLLinear", "BlockELLPattern", "block_ell_mm", "windowed_attention",
-           "tile_kinds", "work_list"]
+__all__ = ["BlockELLLinear", "BlockELLPattern", "block_ell_mm", "causal_dwconv",
+           "windowed_attention", "tile_kinds", "work_list"]

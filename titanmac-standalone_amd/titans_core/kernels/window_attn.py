@@ -154,15 +154,18 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
     """softmax(q·kᵀ·scale + mask)·v on allowed pairs only; q/k/v and result [B, H, S, dh].
 
     scale defaults to 1/sqrt(head_dim), SDPA's default (attn/windowed_attention.py:318-323).
-    Raises ValueError where build_band_mask does (n_persistent >= S, window_size < 0).
+    Raises ValueError where build_band_mask does (n_persistent >= S, window_size < 0);
+    the block-window pattern also accepts n_persistent == S (only persistent
+    tokens), as BlockSparseAttention does.
     """
     S = q.shape[2]
-    if n_persistent >= S:
+    code = _pattern_code(pattern)
+    if n_persistent > S or (code == _lib.PATTERN_BAND and n_persistent == S):
         raise ValueError(f"num_persistent_tokens ({n_persistent}) must be < seq_len ({S})")
     if window_size < 0:
         raise ValueError(f"window_size must be non-negative, got {window_size}")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     out = window_attn_fwd(q, k, v, int(window_size), int(n_persistent), bool(causal),
-                          _pattern_code(pattern), int(block_size), float(scale))
+                          code, int(block_size), float(scale))
     return out.transpose(1, 2)
