@@ -170,6 +170,18 @@ int tmac_wattn_schedule(int S, int window, int n_persistent, int causal,
                         int32_t* h_row_ptr, int32_t* h_entries, int capacity,
                         int* n_entries);
 
+/* Key-major work list of the attention backward (dK, dV): for key block kb
+ * (k_block keys), entries e in [col_ptr[kb], col_ptr[kb+1]) name every 64-row
+ * query tile with at least one allowed pair for the block, ascending.
+ * entries[e] & 0xffff is the query-tile index; bits 16+2j..17+2j hold the kind
+ * (0/1/2 as in tmac_wattn_tile_kinds) of the query tile against the j-th
+ * `sub_cols`-key slice of the block. k_block must be a multiple of sub_cols and
+ * k_block/sub_cols <= 8. With h_entries == NULL only *n_entries is computed. */
+int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int causal,
+                           int pattern, int block_size, int k_block, int sub_cols,
+                           int32_t* h_col_ptr, int32_t* h_entries, int capacity,
+                           int* n_entries);
+
 /* Attention forward: O = softmax(Q·Kᵀ·scale + mask)·V over the allowed pairs
  * only, fp32 accumulation and online softmax. Replaces
  * F.scaled_dot_product_attention(q, k, v, attn_mask=additive band mask,
@@ -190,6 +202,37 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
                    int B, int H, int S, int dh, int window, int n_persistent,
                    int causal, int pattern, int block_size, float scale,
                    const int32_t* d_row_ptr, const int32_t* d_entries,
+                   int dtype, void* stream);
+
+/* Attention backward: given dO, recomputes P = exp(Q·Kᵀ·scale − lse) on the
+ * allowed pairs and writes
+ *   dV = Pᵀ·dO,  dS = P ⊙ (dO·Vᵀ − rowsum(dO ⊙ O)),
+ *   dK = scale · dSᵀ·Q,  dQ = scale · dS·K.
+ * Replaces the autograd backward of the masked SDPA call in
+ * WindowedAttention.forward (attn/windowed_attention.py:318-323) and of
+ * BlockSparseAttention's per-block matmul/softmax loop
+ * (attn/block_sparse_attention.py:277-334). Three launches on `stream`
+ * (row sums, then dK/dV, then dQ), no atomics: results are deterministic.
+ * Q, K, V, O, dO, dQ, dK, dV: [B, H, S, dh] addressed by strides as in
+ * tmac_wattn_fwd; dQ, dK, dV must not overlap each other or the inputs.
+ * lse: fp32 [B, H, S] from tmac_wattn_fwd of the same Q, K, V and mask.
+ * delta: fp32 [B, H, S] workspace (overwritten).
+ * row_ptr/entries: tmac_wattn_schedule with q_block = 128, sub_rows = 32;
+ * col_ptr/entries_kv: tmac_wattn_schedule_kv with k_block = 128,
+ * sub_cols = 32 (device copies). dtype: TMAC_BF16 or TMAC_F16; dh = 64. */
+int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
+                   const void* d_K, const int64_t k_strides[3],
+                   const void* d_V, const int64_t v_strides[3],
+                   const void* d_O, const int64_t o_strides[3],
+                   const void* d_dO, const int64_t do_strides[3],
+                   const float* d_lse, float* d_delta,
+                   void* d_dQ, const int64_t dq_strides[3],
+                   void* d_dK, const int64_t dk_strides[3],
+                   void* d_dV, const int64_t dv_strides[3],
+                   int B, int H, int S, int dh, int window, int n_persistent,
+                   int causal, int pattern, int block_size, float scale,
+                   const int32_t* d_row_ptr, const int32_t* d_entries,
+                   const int32_t* d_col_ptr, const int32_t* d_entries_kv,
                    int dtype, void* stream);
 
 /* ------------------------------------------------------------------------- */

@@ -36,6 +36,30 @@ def masked_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, mask: np.ndarr
     return out
 
 
+def masked_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.ndarray,
+                           mask: np.ndarray, scale: float | None = None, dtype=np.float64):
+    """(dq, dk, dv) of masked_attention for the output gradient `do`.
+
+    The gradient the reference gets from autograd through the masked SDPA call
+    (attn/windowed_attention.py:318-323) and through BlockSparseAttention's
+    matmul/masked_fill/softmax/matmul loop (attn/block_sparse_attention.py
+    :277-334), written out: with P = softmax(S), S = q·kᵀ·scale + mask,
+    dV = Pᵀ·dO, dP = dO·Vᵀ, dS = P ⊙ (dP − rowsum(P ⊙ dP)),
+    dq = scale·dS·k, dk = scale·dSᵀ·q. Masked pairs have P = 0 and get no gradient.
+    """
+    q, k, v, do = (np.asarray(t, dtype=dtype) for t in (q, k, v, do))
+    if scale is None:
+        scale = 1.0 / np.sqrt(q.shape[-1])
+    s = (q @ np.swapaxes(k, -1, -2)) * scale
+    s = np.where(mask, s, -np.inf)
+    p = np.exp(s - s.max(axis=-1, keepdims=True))
+    p /= p.sum(axis=-1, keepdims=True)
+    dv = np.swapaxes(p, -1, -2) @ do
+    dp = do @ np.swapaxes(v, -1, -2)
+    ds = p * (dp - (p * dp).sum(axis=-1, keepdims=True))
+    return scale * (ds @ k), scale * (np.swapaxes(ds, -1, -2) @ q), dv
+
+
 def windowed_attention_module(x: np.ndarray, w_qkv: np.ndarray, w_out: np.ndarray, n_heads: int,
                               window_size: int, n_persistent: int, causal: bool = True,
                               dtype=np.float64) -> np.ndarray:

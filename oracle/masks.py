@@ -131,3 +131,15 @@ def schedule(mask: np.ndarray, q_block: int = 128, sub_rows: int = 32, k_tile: i
                 entries.append(kt | (word << 16))
         row_ptr.append(len(entries))
     return np.asarray(row_ptr, dtype=np.int32), np.asarray(entries, dtype=np.int64).astype(np.int32)
+
+
+def schedule_kv(mask: np.ndarray, k_block: int = 128, sub_cols: int = 32, q_tile: int = 64):
+    """Key-major work list of the attention backward's dK/dV pass:
+    (col_ptr int32 [n_kb+1], entries int32 [nnz]).
+
+    entries = q_tile_index | (kind of key slice j against that query tile) << (16 + 2j),
+    listed for every query tile with a non-empty slice, ascending per key block.
+    A tile's kind depends only on its allowed-pair count, which transposing the
+    mask keeps, so this is the query-major list of the transposed mask.
+    """
+    return schedule(np.ascontiguousarray(mask.T), k_block, sub_cols, q_tile)

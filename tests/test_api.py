@@ -155,7 +155,11 @@ def test_ops_fake_shapes():
         assert y.shape == (2, 7, 256)
         q = torch.empty(2, 3, 100, 64, dtype=torch.bfloat16)
         from titans_core.kernels.window_attn import window_attn_fwd
-        assert window_attn_fwd(q, q, q, 8, 2, True, 0, 64, 0.125).shape == (2, 100, 3, 64)
+        o, lse = window_attn_fwd(q, q, q, 8, 2, True, 0, 64, 0.125, True)
+        assert o.shape == (2, 100, 3, 64) and lse.shape == (2, 3, 100) and lse.dtype == torch.float32
+        from titans_core.kernels.window_attn import window_attn_bwd
+        grads = window_attn_bwd(o, q, q, q, o, lse, 8, 2, True, 0, 64, 0.125)
+        assert [g.shape for g in grads] == [(2, 3, 100, 64)] * 3
 
 
 def test_block_sparse_attention_construction_and_state_dict():

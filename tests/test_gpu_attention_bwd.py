@@ -1,0 +1,159 @@
+"""GPU parity of the windowed-attention backward (dQ, dK, dV) against the oracle.
+
+Bars: bf16/fp16 gradients |got - want| <= 2e-2 + 1e-2 |want| against the fp64
+oracle (oracle.attention.masked_attention_grads, pinned against torch
+autograd) on the same 16-bit-rounded q, k, v and output gradient, both
+divided by max(1, max |want|) of the tensor (a gradient's rounding error
+scales with its largest entries: P and dS enter the MFMAs as 16-bit values,
+O is 16-bit in rowsum(dO ⊙ O)); the
+forward's fp32 log-sum-exp within 1e-3 absolute of the fp64 one; repeated
+calls bit-identical (no atomics).
+"""
+import numpy as np
+import pytest
+import torch
+
+import titans_core as tc
+from oracle import attention as oa
+from oracle import masks as om
+from titans_core.kernels.window_attn import window_attn_fwd, windowed_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, atol=2e-2, rtol=1e-2, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    sc = max(1.0, float(np.abs(want).max())) if want.size else 1.0
+    got, want = got / sc, want / sc
+    err = np.abs(got - want)
+    ok = err <= atol + rtol * np.abs(want)
+    assert ok.all(), f"{what} max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+def tensors(shape, dtype, seed, n=4):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(*shape, generator=g).to(dtype) for _ in range(n)]
+
+
+def run_bwd(dev, q, k, v, do, w, Np, causal, pattern, bs, scale=None):
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = windowed_attention(qd, kd, vd, w, Np, causal, pattern, bs, scale)
+    o.backward(do.to(dev))
+    return o.detach(), qd.grad, kd.grad, vd.grad
+
+
+GRID = [  # B, H, S, w, Np, causal, pattern, block_size
+    (1, 1, 1, 0, 0, True, "band", 64), (1, 2, 17, 3, 1, True, "band", 64),
+    (2, 1, 64, 0, 0, True, "band", 64), (1, 1, 127, 63, 16, True, "band", 64),
+    (1, 2, 129, 200, 16, True, "band", 64), (2, 3, 300, 100, 5, True, "band", 64),
+    (1, 2, 300, 100, 5, False, "band", 64), (1, 1, 257, 40, 0, False, "band", 64),
+    (1, 1, 400, 1000, 130, True, "band", 64), (1, 2, 1000, 512, 16, True, "band", 64),
+    (1, 2, 333, 128, 16, True, "blockwin", 64), (1, 1, 333, 128, 16, False, "blockwin", 64),
+    (1, 1, 500, 96, 3, True, "blockwin", 32), (1, 1, 200, 0, 0, True, "blockwin", 64),
+    (1, 1, 40, 8, 40, True, "blockwin", 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,S,w,Np,causal,pattern,bs", GRID)
+def test_backward_parity_16bit(dev, dtype, B, H, S, w, Np, causal, pattern, bs):
+    q, k, v, do = tensors((B, H, S, 64), dtype, seed=3 * S + w + Np)
+    _, dq, dk, dv = run_bwd(dev, q, k, v, do, w, Np, causal, pattern, bs)
+    mask = om.make_mask(S, w, Np, causal, pattern, bs)
+    want = oa.masked_attention_grads(*(t.float().numpy() for t in (q, k, v, do)), mask)
+    for got, ref, name in zip((dq, dk, dv), want, "qkv"):
+        assert got.shape == (B, H, S, 64) and got.dtype == dtype
+        close(got.float().cpu(), ref, what=f"d{name}")
+
+
+def test_lse_matches_oracle(dev):
+    B, H, S, w, Np = 2, 3, 300, 100, 5
+    q, k, v = tensors((B, H, S, 64), torch.bfloat16, seed=11, n=3)
+    _, lse = window_attn_fwd(q.to(dev), k.to(dev), v.to(dev), w, Np, True, 0, 64, 0.125, True)
+    _, want = oa.masked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(),
+                                  om.band_mask(S, w, Np), return_lse=True)
+    assert lse.shape == (B, H, S) and np.abs(lse.cpu().numpy() - want).max() <= 1e-3
+
+
+def test_backward_custom_scale(dev):
+    q, k, v, do = tensors((1, 2, 200, 64), torch.bfloat16, seed=12)
+    _, dq, dk, dv = run_bwd(dev, q, k, v, do, 50, 4, True, "band", 64, scale=0.3)
+    want = oa.masked_attention_grads(*(t.float().numpy() for t in (q, k, v, do)),
+                                     om.band_mask(200, 50, 4), scale=0.3)
+    for got, ref in zip((dq, dk, dv), want):
+        close(got.float().cpu(), ref)
+
+
+def test_backward_deterministic(dev):
+    q, k, v, do = tensors((2, 2, 700, 64), torch.bfloat16, seed=13)
+    first = run_bwd(dev, q, k, v, do, 256, 16, True, "band", 64)[1:]
+    second = run_bwd(dev, q, k, v, do, 256, 16, True, "band", 64)[1:]
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+
+
+def test_backward_through_fused_qkv_views(dev):
+    """q, k, v as strided views of one [B, S, 3*H*64] projection buffer: the gradient
+    reaching the buffer equals the gradients of contiguous copies, bit for bit."""
+    B, S, H = 2, 260, 3
+    g = torch.Generator().manual_seed(14)
+    buf = torch.randn(B, S, 3 * H * 64, generator=g).to(torch.bfloat16).to(dev).requires_grad_()
+    do = torch.randn(B, H, S, 64, generator=g).to(torch.bfloat16).to(dev)
+    q, k, v = (t.view(B, S, H, 64).transpose(1, 2) for t in buf.chunk(3, dim=-1))
+    o = windowed_attention(q, k, v, 96, 8, True)
+    o.backward(do)
+    qc, kc, vc = (t.detach().contiguous().requires_grad_() for t in (q, k, v))
+    windowed_attention(qc, kc, vc, 96, 8, True).backward(do)
+    want = torch.cat([t.grad.transpose(1, 2).reshape(B, S, H * 64) for t in (qc, kc, vc)], dim=-1)
+    assert torch.equal(buf.grad, want)
+
+
+def test_backward_full_size_cfg3(dev):
+    """Config-3 shape (B=8, H=10, S=4096, w=512, Np=16, band): finite everywhere;
+    (b, h) = (0, 0) and (7, 9) in full against the oracle."""
+    B, H, S, w, Np = 8, 10, 4096, 512, 16
+    q, k, v, do = tensors((B, H, S, 64), torch.bfloat16, seed=15)
+    _, dq, dk, dv = run_bwd(dev, q, k, v, do, w, Np, True, "band", 64)
+    grads = [t.float().cpu() for t in (dq, dk, dv)]
+    assert all(torch.isfinite(t).all() for t in grads)
+    mask = om.band_mask(S, w, Np)
+    for b, h in [(0, 0), (7, 9)]:
+        want = oa.masked_attention_grads(*(t[b, h].float().numpy() for t in (q, k, v, do)), mask)
+        for got, ref in zip(grads, want):
+            close(got[b, h].numpy(), ref)
+
+
+def _module_grads_fp64(m, x, dy, mask, conv=False):
+    """fp64 CPU autograd of the attention module's function on the module's own weights."""
+    w_qkv = m.qkv_proj.weight.detach().double().cpu().requires_grad_()
+    w_out = m.out_proj.weight.detach().double().cpu().requires_grad_()
+    xd = x.detach().double().cpu().requires_grad_()
+    B, T, D = x.shape
+    H, dh = m.n_heads, D // m.n_heads
+    qkv = xd @ w_qkv.T
+    q, k, v = (t.reshape(B, T, H, dh).transpose(1, 2) for t in qkv.chunk(3, dim=-1))
+    add = torch.zeros(T, T, dtype=torch.float64).masked_fill(~torch.from_numpy(mask), float("-inf"))
+    o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=add)
+    y = o.transpose(1, 2).reshape(B, T, D) @ w_out.T
+    y.backward(dy.double().cpu())
+    return xd.grad.numpy(), w_qkv.grad.numpy(), w_out.grad.numpy()
+
+
+def test_windowed_attention_module_training_step_bf16(dev):
+    """WindowedAttention (d=128, 2 heads, w=64, Np=8) in bf16: x and weight gradients
+    against fp64 autograd of the same function."""
+    cfg = tc.WindowConfig(window_size=64, num_heads=2, head_dim=64, n_persistent=8)
+    m = tc.WindowedAttention(cfg)
+    g = torch.Generator().manual_seed(16)
+    with torch.no_grad():
+        m.qkv_proj.weight.copy_(torch.randn(384, 128, generator=g) * 0.08)
+        m.out_proj.weight.copy_(torch.randn(128, 128, generator=g) * 0.08)
+    m = m.to(dev, torch.bfloat16).train()
+    x = torch.randn(2, 300, 128, generator=g).to(torch.bfloat16)
+    dy = torch.randn(2, 300, 128, generator=g).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_()
+    m(xd).backward(dy.to(dev))
+    want = _module_grads_fp64(m, x, dy, om.band_mask(300, 64, 8))
+    got = (xd.grad, m.qkv_proj.weight.grad, m.out_proj.weight.grad)
+    for a, b, name in zip(got, want, ("x", "w_qkv", "w_out")):
+        close(a.float().cpu().numpy(), b, atol=2e-2, rtol=2e-2, what=name)

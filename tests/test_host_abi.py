@@ -12,7 +12,7 @@ from oracle import block_ell as ob
 from oracle import masks as om
 from titans_core.kernels import _lib
 from titans_core.kernels.block_ell import BlockELLPattern
-from titans_core.kernels.window_attn import tile_kinds, work_list
+from titans_core.kernels.window_attn import tile_kinds, work_list, work_list_kv
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "tmac.h"
 GOLDEN = Path(__file__).resolve().parent / "golden"
@@ -88,6 +88,49 @@ def test_work_list_bit_exact(S, w, Np, causal, pattern, bs):
     rp, ent = work_list(S, w, Np, causal, pattern, bs)
     rp2, ent2 = om.schedule(m, 128, 32, 64)
     assert np.array_equal(rp, rp2) and np.array_equal(ent, ent2)
+
+
+@pytest.mark.parametrize("S,w,Np,causal,pattern,bs", CASES)
+def test_work_list_kv_bit_exact(S, w, Np, causal, pattern, bs):
+    m = om.make_mask(S, w, Np, causal, pattern, bs)
+    cp, ent = work_list_kv(S, w, Np, causal, pattern, bs)
+    cp2, ent2 = om.schedule_kv(m, 128, 32, 64)
+    assert np.array_equal(cp, cp2) and np.array_equal(ent, ent2)
+
+
+@pytest.mark.parametrize("S,w,Np,causal,pattern,bs", [(700, 200, 16, True, "band", 64),
+                                                      (333, 40, 5, False, "blockwin", 32)])
+def test_work_list_kv_covers_every_allowed_pair_once(S, w, Np, causal, pattern, bs):
+    """Every allowed (query, key) pair lies in exactly one listed (key slice, query tile)
+    of its key block whose kind is non-zero, and full slices hold only allowed pairs."""
+    m = om.make_mask(S, w, Np, causal, pattern, bs)
+    cp, ent = work_list_kv(S, w, Np, causal, pattern, bs)
+    cover = np.zeros((S, S), dtype=np.int32)
+    for kb in range(len(cp) - 1):
+        qts = [int(e) & 0xffff for e in ent[cp[kb]:cp[kb + 1]]]
+        assert qts == sorted(qts) and len(set(qts)) == len(qts)
+        for e in ent[cp[kb]:cp[kb + 1]]:
+            e = int(e) & 0xffffffff
+            qt = e & 0xffff
+            for j in range(4):
+                kind = (e >> (16 + 2 * j)) & 3
+                k0 = kb * 128 + 32 * j
+                blk = m[qt * 64:qt * 64 + 64, k0:k0 + 32]
+                if kind == 0:
+                    assert not blk.any()
+                    continue
+                if kind == 1:
+                    assert blk.shape == (64, 32) and blk.all()
+                cover[qt * 64:qt * 64 + 64, k0:k0 + 32] += 1
+    assert np.array_equal(cover[m], np.ones(int(m.sum()), dtype=np.int32))
+
+
+def test_work_list_kv_shape_errors(lib):
+    cp = np.zeros(40, dtype=np.int32)
+    n = ctypes.c_int(0)
+    for kb, sc in [(128, 48), (512, 32), (0, 32)]:
+        assert lib.tmac_wattn_schedule_kv(4096, 512, 16, 1, 0, 64, kb, sc, cp.ctypes.data, None, 0,
+                                          ctypes.byref(n)) == -2
 
 
 def test_tile_map_golden():

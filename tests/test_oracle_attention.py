@@ -24,6 +24,31 @@ def test_against_torch_sdpa(S, w, Np, causal, pattern):
     assert np.allclose(got, want, rtol=1e-10, atol=1e-12)
 
 
+@pytest.mark.parametrize("S,w,Np,causal,pattern", [(50, 8, 4, True, "band"), (77, 100, 0, False, "band"),
+                                                    (90, 16, 5, True, "blockwin"),
+                                                    (70, 10, 3, False, "blockwin")])
+def test_grads_against_torch_autograd(S, w, Np, causal, pattern):
+    """The written-out backward against torch autograd through fp64 SDPA."""
+    rng = np.random.default_rng(5)
+    q, k, v, do = (rng.standard_normal((2, 3, S, 64)) for _ in range(4))
+    mask = om.make_mask(S, w, Np, causal, pattern, block_size=16)
+    got = oa.masked_attention_grads(q, k, v, do, mask, scale=0.2)
+    add = torch.zeros(S, S, dtype=torch.float64).masked_fill(~torch.from_numpy(mask), float("-inf"))
+    qt, kt, vt = (torch.from_numpy(t).requires_grad_() for t in (q, k, v))
+    o = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=add, scale=0.2)
+    o.backward(torch.from_numpy(do))
+    for g, t in zip(got, (qt, kt, vt)):
+        assert np.allclose(g, t.grad.numpy(), rtol=1e-9, atol=1e-11)
+
+
+def test_grads_single_allowed_key():
+    """Each row sees only itself: P = 1, so dv = do, dS = 0 and dq = dk = 0."""
+    rng = np.random.default_rng(6)
+    q, k, v, do = (rng.standard_normal((1, 1, 20, 64)) for _ in range(4))
+    dq, dk, dv = oa.masked_attention_grads(q, k, v, do, om.band_mask(20, 0, 0))
+    assert np.allclose(dv, do) and np.abs(dq).max() < 1e-12 and np.abs(dk).max() < 1e-12
+
+
 def test_single_allowed_key_returns_that_value():
     # Np = 0, w = 0: every row sees only itself.
     rng = np.random.default_rng(1)

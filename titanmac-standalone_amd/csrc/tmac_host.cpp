@@ -261,3 +261,43 @@ extern "C" int tmac_wattn_schedule(int S, int window, int n_persistent, int caus
   *n_entries = count;
   return TMAC_OK;
 }
+
+extern "C" int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int causal,
+                                      int pattern, int block_size, int k_block, int sub_cols,
+                                      int32_t* h_col_ptr, int32_t* h_entries, int capacity,
+                                      int* n_entries) {
+  if (!h_col_ptr || !n_entries) return TMAC_ERR_NULL;
+  int st = check_mask_args(S, window, n_persistent, pattern, block_size);
+  if (st != TMAC_OK) return st;
+  if (k_block <= 0 || sub_cols <= 0 || k_block % sub_cols != 0 || k_block / sub_cols > 8)
+    return TMAC_ERR_SHAPE;
+  const int n_sub = k_block / sub_cols;
+  const int n_kb = (S + k_block - 1) / k_block;
+  const int n_qt = (S + TMAC_BLOCK - 1) / TMAC_BLOCK;
+  if (n_qt > 0xffff) return TMAC_ERR_SHAPE;
+  std::vector<RowSpan> spans(S);
+  for (int i = 0; i < S; ++i)
+    spans[i] = row_span(i, S, window, n_persistent, causal != 0, pattern, block_size);
+  int count = 0;
+  h_col_ptr[0] = 0;
+  for (int kb = 0; kb < n_kb; ++kb) {
+    for (int qt = 0; qt < n_qt; ++qt) {
+      uint32_t kinds = 0;
+      for (int j = 0; j < n_sub; ++j) {
+        const int k0 = kb * k_block + j * sub_cols;
+        const uint8_t k = tile_kind(spans, S, qt * TMAC_BLOCK, qt * TMAC_BLOCK + TMAC_BLOCK, k0,
+                                    k0 + sub_cols);
+        kinds |= static_cast<uint32_t>(k) << (2 * j);
+      }
+      if (kinds == 0) continue;
+      if (h_entries) {
+        if (count >= capacity) return TMAC_ERR_CAPACITY;
+        h_entries[count] = static_cast<int32_t>(static_cast<uint32_t>(qt) | (kinds << 16));
+      }
+      ++count;
+    }
+    h_col_ptr[kb + 1] = count;
+  }
+  *n_entries = count;
+  return TMAC_OK;
+}

@@ -319,6 +319,354 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   if (lse) lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + log2f(l_run)) * kLn2;
 }
 
+// ---------------------------------------------------------------------------
+// Backward (16-bit MFMA path). With P = softmax(S) recomputed from the
+// forward's log-sum-exp, Δ = rowsum(dO ⊙ O):
+//   dV = Pᵀ·dO,  dS = P ⊙ (dO·Vᵀ − Δ),  dK = scale·dSᵀ·Q,  dQ = scale·dS·K.
+// Two kernels, no atomics (results are deterministic): wattn_bwd_kv_kernel
+// owns 128 keys and walks the query tiles that touch them (key-major work
+// list, tmac_wattn_schedule_kv); wattn_bwd_q_kernel owns 128 queries and walks
+// the forward's work list. Both recompute S and dP with MFMAs.
+// ---------------------------------------------------------------------------
+
+// Δ[b, h, q] = Σ_d dO[b, h, q, d] · O[b, h, q, d] in fp32: eight lanes per row.
+template <int DT>
+__global__ __launch_bounds__(256) void wattn_bwd_delta_kernel(
+    const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO, float* __restrict__ delta,
+    int64_t osb, int64_t osh, int64_t oss, int64_t gsb, int64_t gsh, int64_t gss, int H, int S,
+    int64_t n_rows) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 32 + (threadIdx.x >> 3);
+  const int ch = threadIdx.x & 7;
+  float acc = 0.f;
+  if (row < n_rows) {
+    const int64_t bh = row / S;
+    const int q = static_cast<int>(row - bh * S);
+    const int b = static_cast<int>(bh / H), hd = static_cast<int>(bh - static_cast<int64_t>(b) * H);
+    const u32x4 o = ldg16(O + b * osb + hd * osh + static_cast<int64_t>(q) * oss + 8 * ch);
+    const u32x4 g = ldg16(dO + b * gsb + hd * gsh + static_cast<int64_t>(q) * gss + 8 * ch);
+    const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] & 0xffff)),
+                 Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] & 0xffff)), acc);
+      acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] >> 16)),
+                 Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] >> 16)), acc);
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (row < n_rows && ch == 0) delta[row] = acc;
+}
+
+// Packs accumulator values v[j0 + 2t], v[j0 + 2t + 1] (t = 0..3) into one
+// 16-bit MFMA operand (eight values, in the permuted key/query order of the
+// 32x32 accumulator layout).
+template <int DT>
+__device__ __forceinline__ u32x4 pack8(const f32x16& v, int j0) {
+  uint32_t w[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    w[t] = static_cast<uint32_t>(Mfma<DT>::from_f32(v[j0 + 2 * t])) |
+           (static_cast<uint32_t>(Mfma<DT>::from_f32(v[j0 + 2 * t + 1])) << 16);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// Stores the transposed accumulators acc[dt] (lane = row `row`, entries
+// 32dt + 8(j/4) + 4h + j%4 of the 64 columns) into row `row` of a 16-bit
+// tensor, multiplied by `mul`: four consecutive columns per 8-byte store.
+template <int DT>
+__device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 (&acc)[2], float mul,
+                                            int h) {
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      u32x2 packed;
+      packed.x = static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg] * mul)) |
+                 (static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 1] * mul)) << 16);
+      packed.y = static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 2] * mul)) |
+                 (static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 3] * mul)) << 16);
+      *reinterpret_cast<u32x2*>(rowp + 32 * dt + 8 * jg + 4 * h) = packed;
+    }
+}
+
+// dK, dV. Workgroup = (b, h, 128 keys); wave w owns keys 32w..32w+31 of the
+// block, held in registers as the B operands of S = Q·Kᵀ and dP = dO·Vᵀ
+// (lane = key). Per listed 64-query tile, Q and dO (plus LSE and Δ of those
+// queries) are staged in LDS; for each 32-query half the wave computes S and dP
+// (lane = key, 16 queries per lane), P = exp2(S·c − LSE·log2e) and dS, then
+// dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, with dOᵀ and Qᵀ read by transpose reads in the
+// accumulator's permuted query order and P, dS packed straight from registers.
+template <int DT>
+__global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
+    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
+    int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
+    int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries, int n_kb,
+    int n_work, int per_xcd) {
+  // [buffer][Q, dO] 64x64 tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+  __shared__ float stat[2][2][64];
+
+  const int logical = xcd_logical_id(per_xcd);
+  if (logical >= n_work) return;
+  const int bh = logical / n_kb;
+  const int kb = logical - bh * n_kb;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int grp = (lane >> 4) & 1;
+  const int key = kb * 128 + wave * 32 + l32;  // this lane's key
+
+  u32x4 kf[4], vf[4];
+  {
+    const int kc = min(key, S - 1);
+    const uint16_t* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + 8 * h;
+    const uint16_t* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      kf[kk] = ldg16(kp + 16 * kk);
+      vf[kk] = ldg16(vp + 16 * kk);
+    }
+  }
+  const uint16_t* Qbh = Q + b * qsb + hd * qsh;
+  const uint16_t* Gbh = dO + b * gsb + hd * gsh;
+  const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
+  const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
+
+  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+
+  u32x4 pre[4];
+  float st_pre = 0.f;
+  auto gload = [&](int qt) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 32 * (p & 1);
+      const int qr = min(qt * 64 + row, S - 1);  // rows past S: valid memory, always masked
+      const uint16_t* src = (p < 2 ? Qbh + qr * qss : Gbh + qr * gss) + (tid & 7) * 8;
+      pre[p] = ldg16(src);
+    }
+    if (tid < 128) {
+      const int qr = min(qt * 64 + (tid & 63), S - 1);
+      st_pre = tid < 64 ? lse_bh[qr] * kLog2e : dl_bh[qr];
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 32 * (p & 1);
+      sts16(smem + (2 * buf + (p >> 1)) * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
+    }
+    if (tid < 128) stat[buf][tid >> 6][tid & 63] = st_pre;
+  };
+
+  f32x16 dkt[2], dvt[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    dkt[dt] = f32x16{};
+    dvt[dt] = f32x16{};
+  }
+
+  if (e0 < e1) {
+    gload(entries[e0] & 0xffff);
+    sstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int qt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    const bool more = e + 1 < e1;
+    if (more) gload(entries[e + 1] & 0xffff);
+
+    if (kind != 0) {
+      const uint16_t* q_lds = smem + (2 * buf) * kTileElems;
+      const uint16_t* g_lds = smem + (2 * buf + 1) * kTileElems;
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const u32x4 qa = lds16(q_lds + (32 * qh + l32) * kPitch + 16 * kk + 8 * h);
+          const u32x4 ga = lds16(g_lds + (32 * qh + l32) * kPitch + 16 * kk + 8 * h);
+          s = Mfma<DT>::run(qa, kf[kk], s);
+          dp = Mfma<DT>::run(ga, vf[kk], dp);
+        }
+        // s[j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4.
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int ql = 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
+          const float l2 = stat[buf][0][ql];
+          float pj = (l2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s[j] * scale_log2 - l2);
+          if (kind == 2 && !allowed(mp, qt * 64 + ql, key)) pj = 0.f;
+          s[j] = pj;
+          dp[j] = pj * (dp[j] - stat[buf][1][ql]);
+        }
+        // dVᵀ[d][key] += Σ_q dO[q][d] P[q][key]; dKᵀ[d][key] += Σ_q Q[q][d] dS[q][key].
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const u32x4 pb = pack8<DT>(s, 8 * ks);
+          const u32x4 db = pack8<DT>(dp, 8 * ks);
+#pragma unroll
+          for (int dt = 0; dt < 2; ++dt) {
+            const int r0 = 32 * qh + 16 * ks + 4 * h;
+            const u32x4 ga = lds_read_tr4x2(g_lds, r0, r0 + 8, 32 * dt + 16 * grp, lane);
+            const u32x4 qa = lds_read_tr4x2(q_lds, r0, r0 + 8, 32 * dt + 16 * grp, lane);
+            dvt[dt] = Mfma<DT>::run(ga, pb, dvt[dt]);
+            dkt[dt] = Mfma<DT>::run(qa, db, dkt[dt]);
+          }
+        }
+      }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if (key >= S) return;
+  store_row64<DT>(dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss, dkt, scale, h);
+  store_row64<DT>(dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss, dvt, 1.f, h);
+}
+
+// dQ. Workgroup = (b, h, 128 queries) as in the forward; wave w owns queries
+// 32w..32w+31, Q and dO rows in registers (B operands of Sᵀ = K·Qᵀ and
+// dPᵀ = V·dOᵀ, lane = query). Per listed 64-key tile (the forward's work list),
+// K and V are staged in LDS; the wave computes Sᵀ, dPᵀ, P and dSᵀ (lane = query,
+// 16 keys per lane), then dQᵀ += Kᵀ·dSᵀ with Kᵀ read by transpose reads in the
+// accumulator's permuted key order.
+template <int DT>
+__global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    uint16_t* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
+    int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
+    int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
+    float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    int n_qb, int n_work, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+
+  const int logical = xcd_logical_id(per_xcd);
+  if (logical >= n_work) return;
+  const int bh = logical / n_qb;
+  const int qb = n_qb - 1 - (logical - bh * n_qb);
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int grp = (lane >> 4) & 1;
+  const int q_row = qb * 128 + wave * 32 + l32;
+
+  u32x4 qf[4], gf[4];
+  {
+    const int qc = min(q_row, S - 1);
+    const uint16_t* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss + 8 * h;
+    const uint16_t* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      qf[kk] = ldg16(qp + 16 * kk);
+      gf[kk] = ldg16(gp + 16 * kk);
+    }
+  }
+  const float l2 = lse[static_cast<int64_t>(bh) * S + min(q_row, S - 1)] * kLog2e;
+  const float dl = delta[static_cast<int64_t>(bh) * S + min(q_row, S - 1)];
+  const uint16_t* Kbh = K + b * ksb + hd * ksh;
+  const uint16_t* Vbh = V + b * vsb + hd * vsh;
+  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+
+  u32x4 pre[4];
+  auto gload = [&](int kt) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 32 * (p & 1);
+      const int kr = min(kt * 64 + row, S - 1);
+      const uint16_t* src = (p < 2 ? Kbh + kr * kss : Vbh + kr * vss) + (tid & 7) * 8;
+      pre[p] = ldg16(src);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 32 * (p & 1);
+      sts16(smem + (2 * buf + (p >> 1)) * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
+    }
+  };
+
+  f32x16 dqt[2];
+  dqt[0] = f32x16{};
+  dqt[1] = f32x16{};
+
+  if (e0 < e1) {
+    gload(entries[e0] & 0xffff);
+    sstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int kt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    const bool more = e + 1 < e1;
+    if (more) gload(entries[e + 1] & 0xffff);
+
+    if (kind != 0) {
+      const uint16_t* k_lds = smem + (2 * buf) * kTileElems;
+      const uint16_t* v_lds = smem + (2 * buf + 1) * kTileElems;
+      f32x16 s[2], dp[2];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        s[kh] = f32x16{};
+        dp[kh] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const u32x4 ka = lds16(k_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
+          const u32x4 va = lds16(v_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
+          s[kh] = Mfma<DT>::run(ka, qf[kk], s[kh]);
+          dp[kh] = Mfma<DT>::run(va, gf[kk], dp[kh]);
+        }
+      }
+      // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4.
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float pj = (l2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s[kh][j] * scale_log2 - l2);
+          if (kind == 2) {
+            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+            if (!allowed(mp, q_row, key)) pj = 0.f;
+          }
+          dp[kh][j] = pj * (dp[kh][j] - dl);
+        }
+      // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 db = pack8<DT>(dp[ks >> 1], 8 * (ks & 1));
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) {
+          const u32x4 ka = lds_read_tr4x2(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
+                                          32 * dt + 16 * grp, lane);
+          dqt[dt] = Mfma<DT>::run(ka, db, dqt[dt]);
+        }
+      }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if (q_row >= S) return;
+  store_row64<DT>(dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss, dqt, scale, h);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -382,6 +730,81 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
                        os[2], H, mp, scale_log2, d_row_ptr, d_entries, n_qb,
                        static_cast<int>(n_work), per_xcd);
   }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
+}
+
+extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const void* d_K,
+                              const int64_t k_strides[3], const void* d_V,
+                              const int64_t v_strides[3], const void* d_O,
+                              const int64_t o_strides[3], const void* d_dO,
+                              const int64_t do_strides[3], const float* d_lse, float* d_delta,
+                              void* d_dQ, const int64_t dq_strides[3], void* d_dK,
+                              const int64_t dk_strides[3], void* d_dV,
+                              const int64_t dv_strides[3], int B, int H, int S, int dh, int window,
+                              int n_persistent, int causal, int pattern, int block_size,
+                              float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
+                              const int32_t* d_col_ptr, const int32_t* d_entries_kv, int dtype,
+                              void* stream) {
+  if (!d_Q || !d_K || !d_V || !d_O || !d_dO || !d_lse || !d_delta || !d_dQ || !d_dK || !d_dV ||
+      !q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides ||
+      !dk_strides || !dv_strides || !d_row_ptr || !d_entries || !d_col_ptr || !d_entries_kv)
+    return TMAC_ERR_NULL;
+  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
+  if (dh != 64) return TMAC_ERR_SHAPE;
+  if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
+  if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
+  if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
+  if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
+  if (!(scale > 0.f)) return TMAC_ERR_VALUE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides,
+                           do_strides, dq_strides, dk_strides, dv_strides};
+  for (const int64_t* st : all)
+    for (int i = 0; i < 3; ++i)
+      if (st[i] < 0 || st[i] % 8) return TMAC_ERR_ALIGN;
+  const void* ptrs[8] = {d_Q, d_K, d_V, d_O, d_dO, d_dQ, d_dK, d_dV};
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return TMAC_ERR_ALIGN;
+
+  const int n_qb = (S + 127) / 128;  // 128-query blocks (dQ) and 128-key blocks (dK, dV)
+  const int64_t n_work = static_cast<int64_t>(B) * H * n_qb;
+  if (n_work > (1ll << 30)) return TMAC_ERR_SHAPE;
+  const int per_xcd = static_cast<int>((n_work + 7) / 8);
+  const MaskParams mp{S, window, n_persistent, causal ? 1 : 0, pattern, block_size};
+  const float scale_log2 = scale * kLog2e;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* Q = static_cast<const uint16_t*>(d_Q);
+  const auto* K = static_cast<const uint16_t*>(d_K);
+  const auto* V = static_cast<const uint16_t*>(d_V);
+  const auto* O = static_cast<const uint16_t*>(d_O);
+  const auto* G = static_cast<const uint16_t*>(d_dO);
+  auto* dQ = static_cast<uint16_t*>(d_dQ);
+  auto* dK = static_cast<uint16_t*>(d_dK);
+  auto* dV = static_cast<uint16_t*>(d_dV);
+  const int64_t *qs = q_strides, *ks = k_strides, *vs = v_strides, *os = o_strides,
+                *gs = do_strides, *dqs = dq_strides, *dks = dk_strides, *dvs = dv_strides;
+  const int64_t n_rows = static_cast<int64_t>(B) * H * S;
+  const unsigned dgrid = static_cast<unsigned>((n_rows + 31) / 32);
+#define TMAC_WATTN_BWD(DTV)                                                                          \
+  do {                                                                                               \
+    hipLaunchKernelGGL((wattn_bwd_delta_kernel<DTV>), dim3(dgrid), dim3(256), 0, s, O, G, d_delta,   \
+                       os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);                      \
+    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV>), dim3(8 * per_xcd), dim3(256), 0, s, Q, K, V, G,   \
+                       d_lse, d_delta, dK, dV, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],      \
+                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],    \
+                       dvs[2], H, mp, scale, scale_log2, d_col_ptr, d_entries_kv, n_qb,              \
+                       static_cast<int>(n_work), per_xcd);                                           \
+    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV>), dim3(8 * per_xcd), dim3(256), 0, s, Q, K, V, G,    \
+                       d_lse, d_delta, dQ, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],   \
+                       vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H, mp, scale, scale_log2, \
+                       d_row_ptr, d_entries, n_qb, static_cast<int>(n_work), per_xcd);               \
+  } while (0)
+  if (dtype == TMAC_BF16)
+    TMAC_WATTN_BWD(TMAC_BF16);
+  else
+    TMAC_WATTN_BWD(TMAC_F16);
+#undef TMAC_WATTN_BWD
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }

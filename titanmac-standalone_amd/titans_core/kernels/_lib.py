@@ -45,6 +45,11 @@ SIGNATURES = {
     "tmac_wattn_schedule": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
     "tmac_wattn_fwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                        _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp],
+    "tmac_wattn_schedule_kv": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
+    "tmac_wattn_bwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                       _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _vp,
+                       _i, _vp],
     "tmac_dwconv_causal": [_vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
 }
 

@@ -91,61 +91,165 @@ def _device_work_list(S, window, n_persistent, causal, code, block_size, device)
         return _sched_cache[key]
 
 
+def work_list_kv(seq_len: int, window_size: int, n_persistent: int, causal: bool = True,
+                 pattern="band", block_size: int = 64, k_block: int = Q_BLOCK,
+                 sub_cols: int = SUB_ROWS):
+    """(col_ptr int32 [n_kb+1], entries int32 [nnz]): the key-major work list of the
+    backward's dK/dV kernel (query tiles of 64 rows per 128-key block)."""
+    L = _lib.lib()
+    code = _pattern_code(pattern)
+    n_kb = -(-seq_len // k_block) if seq_len > 0 else 0
+    col_ptr = np.zeros(n_kb + 1, dtype=np.int32)
+    n = ctypes.c_int(0)
+    args = (seq_len, window_size, n_persistent, int(causal), code, block_size, k_block, sub_cols)
+    _lib.check(L.tmac_wattn_schedule_kv(*args, col_ptr.ctypes.data, None, 0, ctypes.byref(n)),
+               "tmac_wattn_schedule_kv")
+    entries = np.zeros(max(n.value, 1), dtype=np.int32)
+    _lib.check(L.tmac_wattn_schedule_kv(*args, col_ptr.ctypes.data, entries.ctypes.data,
+                                        entries.size, ctypes.byref(n)), "tmac_wattn_schedule_kv")
+    return col_ptr, entries[:n.value]
+
+
+def _device_work_list_kv(S, window, n_persistent, causal, code, block_size, device):
+    key = ("kv", S, window, n_persistent, bool(causal), code, block_size, str(device))
+    hit = _sched_cache.get(key)
+    if hit is not None:
+        return hit
+    with _sched_lock:
+        if key not in _sched_cache:
+            cp, ent = work_list_kv(S, window, n_persistent, causal, code, block_size)
+            if ent.size == 0:
+                ent = np.zeros(1, dtype=np.int32)
+            _sched_cache[key] = (torch.from_numpy(cp).to(device), torch.from_numpy(ent).to(device))
+        return _sched_cache[key]
+
+
 def _strides3(t: torch.Tensor):
     """(batch, head, seq) strides in elements of a [B, H, S, dh] tensor."""
     return (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))
 
 
-@torch.library.custom_op("titanmac::window_attn_fwd", mutates_args=())
-def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
-                    n_persistent: int, causal: bool, pattern: int, block_size: int,
-                    scale: float) -> torch.Tensor:
-    """Masked attention over q/k/v [B, H, S, dh]; returns a contiguous [B, S, H, dh]."""
+def _check_qkv(q, k, v):
     if q.dim() != 4 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError(f"q, k, v must share one [B, H, S, dh] shape; got "
                          f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share one dtype")
-    B, H, S, dh = (int(s) for s in q.shape)
-    if dh != 64:
-        raise ValueError(f"the attention kernel is built for head_dim 64, got {dh}")
+    if int(q.shape[3]) != 64:
+        raise ValueError(f"the attention kernel is built for head_dim 64, got {int(q.shape[3])}")
     for t in (q, k, v):
         if t.stride(3) != 1:
             raise ValueError("q, k, v need a contiguous last (head_dim) dimension")
+
+
+@torch.library.custom_op("titanmac::window_attn_fwd", mutates_args=())
+def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
+                    n_persistent: int, causal: bool, pattern: int, block_size: int,
+                    scale: float, need_lse: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+    """Masked attention over q/k/v [B, H, S, dh].
+
+    Returns (out, lse): out a contiguous [B, S, H, dh]; lse the fp32 [B, H, S]
+    natural-log log-sum-exp of each row when need_lse (what the backward
+    needs), else an empty tensor.
+    """
+    _check_qkv(q, k, v)
+    B, H, S, dh = (int(s) for s in q.shape)
     dev = _lib.require_device(q, k, v, what="windowed_attention")
     out = torch.empty((B, S, H, dh), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, H, S) if need_lse else (0,), dtype=torch.float32, device=dev)
     if B * H * S == 0:
-        return out
+        return out, lse
     row_ptr, entries = _device_work_list(S, window_size, n_persistent, causal, pattern,
                                          block_size, dev)
     o_view = out.permute(0, 2, 1, 3)  # [B, H, S, dh] view
     with torch.cuda.device(dev):
         rc = _lib.lib().tmac_wattn_fwd(
             _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
-            _lib.ptr(out), _strides3(o_view), None, B, H, S, dh, window_size, n_persistent,
-            int(causal), pattern, block_size, float(scale), _lib.ptr(row_ptr), _lib.ptr(entries),
-            _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+            _lib.ptr(out), _strides3(o_view), _lib.ptr(lse) if need_lse else None, B, H, S, dh,
+            window_size, n_persistent, int(causal), pattern, block_size, float(scale),
+            _lib.ptr(row_ptr), _lib.ptr(entries), _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_wattn_fwd")
-    return out
+    return out, lse
 
 
 @window_attn_fwd.register_fake
-def _(q, k, v, window_size, n_persistent, causal, pattern, block_size, scale):
+def _(q, k, v, window_size, n_persistent, causal, pattern, block_size, scale, need_lse=False):
     B, H, S, dh = q.shape
-    return q.new_empty((B, S, H, dh))
+    lse = q.new_empty((B, H, S) if need_lse else (0,), dtype=torch.float32)
+    return q.new_empty((B, S, H, dh)), lse
 
 
-def _no_backward(ctx, grad):
-    raise NotImplementedError(
-        "windowed attention backward (dQ, dK, dV) is not implemented in the MI355X build yet; "
-        "the forward kernel is inference/forward-only")
+@torch.library.custom_op("titanmac::window_attn_bwd", mutates_args=())
+def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    out: torch.Tensor, lse: torch.Tensor, window_size: int, n_persistent: int,
+                    causal: bool, pattern: int, block_size: int,
+                    scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dq, dk, dv), each [B, H, S, dh] (transposed views of [B, S, H, dh] buffers), from
+    grad_out and out [B, S, H, dh] and lse [B, H, S] of window_attn_fwd."""
+    _check_qkv(q, k, v)
+    B, H, S, dh = (int(s) for s in q.shape)
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise NotImplementedError(
+            f"windowed attention backward runs in bfloat16/float16 (MFMA kernels); got {q.dtype}")
+    if out.shape != (B, S, H, dh) or grad_out.shape != (B, S, H, dh):
+        raise ValueError("out and grad_out must be [B, S, H, dh] as window_attn_fwd returns")
+    if lse.shape != (B, H, S) or lse.dtype != torch.float32:
+        raise ValueError("lse must be the fp32 [B, H, S] log-sum-exp from window_attn_fwd")
+    dev = _lib.require_device(grad_out, q, k, v, out, lse, what="windowed_attention backward")
+    grad_out = grad_out.to(q.dtype)
+    if grad_out.stride(3) != 1 or any(s % 8 for s in grad_out.stride()[:3]) \
+            or grad_out.data_ptr() % 16:
+        grad_out = grad_out.contiguous()
+    lse = lse.contiguous()
+    grads = [torch.empty((B, S, H, dh), dtype=q.dtype, device=dev) for _ in range(3)]
+    views = [g.permute(0, 2, 1, 3) for g in grads]
+    if B * H * S == 0:
+        return tuple(views)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    row_ptr, entries = _device_work_list(S, window_size, n_persistent, causal, pattern,
+                                         block_size, dev)
+    col_ptr, entries_kv = _device_work_list_kv(S, window_size, n_persistent, causal, pattern,
+                                               block_size, dev)
+    o_view, g_view = out.permute(0, 2, 1, 3), grad_out.permute(0, 2, 1, 3)
+    with torch.cuda.device(dev):
+        rc = _lib.lib().tmac_wattn_bwd(
+            _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
+            _lib.ptr(out), _strides3(o_view), _lib.ptr(grad_out), _strides3(g_view),
+            _lib.ptr(lse), _lib.ptr(delta),
+            _lib.ptr(grads[0]), _strides3(views[0]), _lib.ptr(grads[1]), _strides3(views[1]),
+            _lib.ptr(grads[2]), _strides3(views[2]),
+            B, H, S, dh, window_size, n_persistent, int(causal), pattern, block_size,
+            float(scale), _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(col_ptr),
+            _lib.ptr(entries_kv), _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_wattn_bwd")
+    return tuple(views)
+
+
+@window_attn_bwd.register_fake
+def _(grad_out, q, k, v, out, lse, window_size, n_persistent, causal, pattern, block_size, scale):
+    B, H, S, dh = q.shape
+    return tuple(q.new_empty((B, S, H, dh)).permute(0, 2, 1, 3) for _ in range(3))
 
 
 def _setup(ctx, inputs, output):
-    pass
+    q, k, v, window_size, n_persistent, causal, pattern, block_size, scale, need_lse = inputs
+    out, lse = output
+    if need_lse:
+        ctx.save_for_backward(q, k, v, out, lse)
+    ctx.args = (window_size, n_persistent, causal, pattern, block_size, scale)
+    ctx.need_lse = need_lse
 
 
-window_attn_fwd.register_autograd(_no_backward, setup_context=_setup)
+def _backward(ctx, grad_out, grad_lse):
+    if not ctx.need_lse:
+        raise RuntimeError("window_attn_fwd was called with need_lse=False; its backward "
+                           "needs the log-sum-exp (windowed_attention sets it under autograd)")
+    q, k, v, out, lse = ctx.saved_tensors
+    dq, dk, dv = window_attn_bwd(grad_out, q, k, v, out, lse, *ctx.args)
+    return dq, dk, dv, None, None, None, None, None, None, None
+
+
+window_attn_fwd.register_autograd(_backward, setup_context=_setup)
 
 
 def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
@@ -166,6 +270,8 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
         raise ValueError(f"window_size must be non-negative, got {window_size}")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
-    out = window_attn_fwd(q, k, v, int(window_size), int(n_persistent), bool(causal),
-                          code, int(block_size), float(scale))
+    need_lse = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
+                                            or v.requires_grad)
+    out, _ = window_attn_fwd(q, k, v, int(window_size), int(n_persistent), bool(causal),
+                             code, int(block_size), float(scale), need_lse)
     return out.transpose(1, 2)
