@@ -11,6 +11,8 @@ The same run also times, as secondary figures:
     Np=16, bf16) in tokens/s, against the dense masked SDPA and the dense
     bmm -> softmax -> bmm path on the same GPU (the faster one is the
     denominator of `attn_speedup_vs_dense`);
+  - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
+    masked bf16 backward (five bmm over the full S x S);
   - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40).
 Inputs are drawn on the CPU from fixed seeds and copied to HBM before timing.
 Kernel time is measured with HIP events on the launch stream (torch's current
@@ -18,7 +20,7 @@ stream) around exactly K back-to-back launches after W warm-up launches.
 The CPU baseline runs the oracle's dense restatement of the reference path
 (X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only.
 
-Modes (for profiling runs): all (default), spmm, attn, dx, sddmm, copy (a
+Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, copy (a
 plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
 """
 from __future__ import annotations
@@ -38,7 +40,8 @@ import torch  # noqa: E402
 
 from titans_core.kernels import _lib  # noqa: E402
 from titans_core.kernels.block_ell import BlockELLPattern, _sddmm_workspace_bytes  # noqa: E402
-from titans_core.kernels.window_attn import _device_work_list  # noqa: E402
+from titans_core.kernels.window_attn import (_device_work_list, _device_work_list_kv,  # noqa: E402
+                                             window_attn_fwd)
 
 METRIC = "Block-ELL SpMM effective TFLOP/s; windowed-attn fwd tokens/s at T=4096,w=512"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
@@ -131,8 +134,8 @@ def setup_attn(dev):
     q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))  # [B, H, S, dh] views
     out = torch.empty(c["B"], c["S"], c["H"], c["dh"], dtype=torch.bfloat16, device=dev)
     o_view = out.permute(0, 2, 1, 3)
-    row_ptr, entries = _device_work_list(c["S"], c["window"], c["n_persistent"], True,
-                                         _lib.PATTERN_BAND, 64, dev)
+    row_ptr, entries, order, n_lead = _device_work_list(c["S"], c["window"], c["n_persistent"],
+                                                        True, _lib.PATTERN_BAND, 64, dev)
     import ctypes
     st = lambda t: (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
     L = _lib.lib()
@@ -140,7 +143,7 @@ def setup_attn(dev):
     args = (_lib.ptr(q), st(q), _lib.ptr(k), st(k), _lib.ptr(v), st(v), _lib.ptr(out), st(o_view),
             None, c["B"], c["H"], c["S"], c["dh"], c["window"], c["n_persistent"], 1,
             _lib.PATTERN_BAND, 64, float(1.0 / np.sqrt(c["dh"])), _lib.ptr(row_ptr),
-            _lib.ptr(entries), _lib.BF16, stream)
+            _lib.ptr(entries), _lib.ptr(order), n_lead, _lib.BF16, stream)
 
     def launch():
         rc = L.tmac_wattn_fwd(*args)
@@ -152,7 +155,78 @@ def setup_attn(dev):
     flops = 4 * c["dh"] * pairs * bh
     bytes_ = 4 * bh * c["S"] * c["dh"] * 2
     return dict(launch=launch, flops=flops, bytes=bytes_, tokens=c["B"] * c["S"],
-                keep=(qkv, out, row_ptr, entries), q=q, k=k, v=v)
+                keep=(qkv, out, row_ptr, entries, order), q=q, k=k, v=v)
+
+
+def setup_attn_bwd(dev, att):
+    """Backward of the config-3 attention (dQ, dK, dV from dO) on the forward's views."""
+    import ctypes
+    c = CFG3
+    B, H, S, dh = c["B"], c["H"], c["S"], c["dh"]
+    q, k, v = att["q"], att["k"], att["v"]
+    scale = float(1.0 / np.sqrt(dh))
+    out, lse = window_attn_fwd(q, k, v, c["window"], c["n_persistent"], True, _lib.PATTERN_BAND,
+                               64, scale, True)
+    do = gen((B, S, H, dh), c["seed"] + 1).to(dev)
+    grads = [torch.empty(B, S, H, dh, dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    delta = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    row_ptr, entries, order, n_lead = _device_work_list(S, c["window"], c["n_persistent"], True,
+                                                        _lib.PATTERN_BAND, 64, dev)
+    col_ptr, entries_kv, order_kv, n_lead_kv = _device_work_list_kv(
+        S, c["window"], c["n_persistent"], True, _lib.PATTERN_BAND, 64, dev)
+    st = lambda t: (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
+    pv = lambda t: st(t.permute(0, 2, 1, 3))  # noqa: E731  [B, S, H, dh] buffer as [B, H, S, dh]
+    L = _lib.lib()
+    args = (_lib.ptr(q), st(q), _lib.ptr(k), st(k), _lib.ptr(v), st(v), _lib.ptr(out), pv(out),
+            _lib.ptr(do), pv(do), _lib.ptr(lse), _lib.ptr(delta),
+            _lib.ptr(grads[0]), pv(grads[0]), _lib.ptr(grads[1]), pv(grads[1]),
+            _lib.ptr(grads[2]), pv(grads[2]), B, H, S, dh, c["window"], c["n_persistent"], 1,
+            _lib.PATTERN_BAND, 64, scale, _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(order),
+            n_lead, _lib.ptr(col_ptr), _lib.ptr(entries_kv), _lib.ptr(order_kv), n_lead_kv,
+            _lib.BF16, _lib.stream_ptr(dev))
+
+    def launch():
+        rc = L.tmac_wattn_bwd(*args)
+        if rc:
+            _lib.check(rc, "tmac_wattn_bwd")
+
+    pairs = band_pairs(S, c["window"], c["n_persistent"])
+    flops = 10 * dh * pairs * B * H  # dS·K, dSᵀ·Q, Pᵀ·dO, dO·Vᵀ, Q·Kᵀ: 5 products of 2·dh per pair
+    return dict(launch=launch, flops=flops, tokens=B * S, do=do, out=out,
+                keep=(out, lse, do, grads, delta, row_ptr, entries, order, col_ptr, entries_kv,
+                      order_kv))
+
+
+def dense_attention_bwd_baseline(att, bwd, steps: int, stream):
+    """ms of the dense masked backward in bf16 on this GPU, the products autograd of the
+    reference's masked SDPA runs: softmax(Q·Kᵀ·scale + mask) recomputed, then dV, dP, dQ
+    and dK as bmm over the full S x S (every transposed operand made contiguous first)."""
+    c = CFG3
+    B, H, S, dh = c["B"], c["H"], c["S"], c["dh"]
+    i = torch.arange(S, device=att["q"].device)
+    j = i[None, :]
+    i = i[:, None]
+    Np, w = c["n_persistent"], c["window"]
+    allowed = (j < Np) | ((i >= Np) & (j >= Np) & (j >= i - w) & (j <= i))
+    add = torch.zeros(S, S, dtype=torch.bfloat16, device=i.device).masked_fill(~allowed, float("-inf"))
+    qb = att["q"].reshape(B * H, S, dh).contiguous()
+    kb = att["k"].reshape(B * H, S, dh).contiguous()
+    vb = att["v"].reshape(B * H, S, dh).contiguous()
+    kt, vt = kb.transpose(1, 2).contiguous(), vb.transpose(1, 2).contiguous()
+    dob = bwd["do"].permute(0, 2, 1, 3).reshape(B * H, S, dh).contiguous()
+    ob = bwd["out"].permute(0, 2, 1, 3).reshape(B * H, S, dh).contiguous()
+    scale = 1.0 / dh ** 0.5
+
+    def dense_bwd():
+        p = torch.softmax(torch.bmm(qb, kt) * scale + add, dim=-1)
+        dv = torch.bmm(p.transpose(1, 2).contiguous(), dob)
+        dp = torch.bmm(dob, vt)
+        ds = p * (dp - (dob * ob).sum(-1, keepdim=True))
+        dq = torch.bmm(ds, kb) * scale
+        dk = torch.bmm(ds.transpose(1, 2).contiguous(), qb) * scale
+        return dq, dk, dv
+
+    return timed(dense_bwd, max(2, steps // 10), 2, stream)
 
 
 def setup_dx_sddmm(dev):
@@ -270,7 +344,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "dx", "sddmm", "copy"])
+    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the hot path's kernels run on one MI355X and this "
@@ -298,13 +372,20 @@ def main() -> int:
         ms = timed(spmm["launch"], K, W, stream)
         out["spmm"] = dict(ms=ms, tflops=spmm["flops"] / ms / 1e9, flops=spmm["flops"],
                            bytes=spmm["bytes"], wall_ms=timed_wall(spmm["launch"], K, stream))
-    if args.mode in ("all", "attn"):
+    if args.mode in ("all", "attn", "attn_bwd"):
         att = setup_attn(dev)
+    if args.mode in ("all", "attn"):
         ms = timed(att["launch"], K, W, stream)
         out["attn"] = dict(ms=ms, tokens_per_s=att["tokens"] / ms * 1e3,
                            tflops=att["flops"] / ms / 1e9, gbs=att["bytes"] / ms / 1e6)
         if args.mode == "all":
             out["attn"].update(dense_attention_baseline(att, K, W, stream))
+    if args.mode in ("all", "attn_bwd"):
+        bwd = setup_attn_bwd(dev, att)
+        ms = timed(bwd["launch"], K, W, stream)
+        out["attn_bwd"] = dict(ms=ms, tokens_per_s=bwd["tokens"] / ms * 1e3,
+                               tflops=bwd["flops"] / ms / 1e9)
+        out["attn_bwd"]["dense_bwd_ms"] = dense_attention_bwd_baseline(att, bwd, K, stream)
     if args.mode in ("all", "dx", "sddmm"):
         bw = setup_dx_sddmm(dev)
         if args.mode in ("all", "dx"):
@@ -352,6 +433,10 @@ def main() -> int:
             "dense_masked_sdpa_ms": round(a["sdpa_masked_ms"], 4),
             "dense_bmm_softmax_bmm_ms": round(a["bmm_softmax_bmm_ms"], 4),
             "attn_speedup_vs_dense": round(dense_ms / a["ms"], 2),
+            "windowed_attn_bwd_ms": round(out["attn_bwd"]["ms"], 5),
+            "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
+            "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
+            "attn_bwd_speedup_vs_dense": round(out["attn_bwd"]["dense_bwd_ms"] / out["attn_bwd"]["ms"], 2),
             "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),
             "bell_dx_cfg4_tflops": round(out["dx"]["tflops"], 3),
             "bell_dx_cfg4_hbm_gbs_compulsory": round(out["dx"]["gbs"], 1),

@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 1
+#define TMAC_ABI_VERSION 2
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -182,6 +182,18 @@ int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int causal,
                            int32_t* h_col_ptr, int32_t* h_entries, int capacity,
                            int* n_entries);
 
+/* Launch order of a work list (tmac_wattn_schedule's row_ptr or
+ * tmac_wattn_schedule_kv's col_ptr, n_blocks + 1 entries): h_order[0..n_blocks)
+ * lists the blocks by list length, longest first (ties by block index), and
+ * *n_lead counts the leading blocks whose list is at least twice the mean
+ * length (the blocks of persistent tokens, which meet every key or query).
+ * The attention kernels launch those n_lead blocks of every (batch, head)
+ * first and spread over the XCDs, then the rest (batch, head)-major, so that
+ * the longest workgroups do not start last. No counterpart in the reference
+ * (the dense SDPA has no work list). */
+int tmac_wattn_launch_order(const int32_t* h_ptr, int n_blocks, int32_t* h_order,
+                            int* n_lead);
+
 /* Attention forward: O = softmax(Q·Kᵀ·scale + mask)·V over the allowed pairs
  * only, fp32 accumulation and online softmax. Replaces
  * F.scaled_dot_product_attention(q, k, v, attn_mask=additive band mask,
@@ -193,7 +205,8 @@ int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int causal,
  * projection (:295-304) are taken without a copy. dh must be 64.
  * lse (nullable): fp32 [B, H, S], natural-log log-sum-exp of each row.
  * row_ptr/entries: device copies of tmac_wattn_schedule's output built with
- * q_block = 128, sub_rows = 32.
+ * q_block = 128, sub_rows = 32; order/n_lead: device copy of
+ * tmac_wattn_launch_order of that row_ptr, and its lead count.
  * dtype: TMAC_BF16 / TMAC_F16 (MFMA path) or TMAC_F32 (fp32 FMA path). */
 int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
@@ -202,7 +215,7 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
                    int B, int H, int S, int dh, int window, int n_persistent,
                    int causal, int pattern, int block_size, float scale,
                    const int32_t* d_row_ptr, const int32_t* d_entries,
-                   int dtype, void* stream);
+                   const int32_t* d_order, int n_lead, int dtype, void* stream);
 
 /* Attention backward: given dO, recomputes P = exp(Q·Kᵀ·scale − lse) on the
  * allowed pairs and writes
@@ -217,9 +230,10 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
  * tmac_wattn_fwd; dQ, dK, dV must not overlap each other or the inputs.
  * lse: fp32 [B, H, S] from tmac_wattn_fwd of the same Q, K, V and mask.
  * delta: fp32 [B, H, S] workspace (overwritten).
- * row_ptr/entries: tmac_wattn_schedule with q_block = 128, sub_rows = 32;
+ * row_ptr/entries/order/n_lead: as for tmac_wattn_fwd;
  * col_ptr/entries_kv: tmac_wattn_schedule_kv with k_block = 128,
- * sub_cols = 32 (device copies). dtype: TMAC_BF16 or TMAC_F16; dh = 64. */
+ * sub_cols = 32, order_kv/n_lead_kv: tmac_wattn_launch_order of col_ptr
+ * (device copies). dtype: TMAC_BF16 or TMAC_F16; dh = 64. */
 int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
                    const void* d_V, const int64_t v_strides[3],
@@ -232,7 +246,9 @@ int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    int B, int H, int S, int dh, int window, int n_persistent,
                    int causal, int pattern, int block_size, float scale,
                    const int32_t* d_row_ptr, const int32_t* d_entries,
+                   const int32_t* d_order, int n_lead,
                    const int32_t* d_col_ptr, const int32_t* d_entries_kv,
+                   const int32_t* d_order_kv, int n_lead_kv,
                    int dtype, void* stream);
 
 /* ------------------------------------------------------------------------- */

@@ -195,19 +195,58 @@ def test_bell_dx_and_sddmm_argument_errors(lib):
 def test_wattn_fwd_argument_errors(lib):
     st = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1920)
     base = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, None, 8, 10, 4096, 64, 512, 16, 1, 0, 64, 0.125,
-            FAKE, FAKE, 1, None]
+            FAKE, FAKE, FAKE, 0, 1, None]
     a = list(base); a[12] = 32
     assert lib.tmac_wattn_fwd(*a) == -2           # head_dim must be 64
     a = list(base); a[14] = 4096
     assert lib.tmac_wattn_fwd(*a) == -8           # n_persistent >= S
     a = list(base); a[13] = -1
     assert lib.tmac_wattn_fwd(*a) == -8           # negative window
-    a = list(base); a[21] = 9
+    a = list(base); a[23] = 9
     assert lib.tmac_wattn_fwd(*a) == -4
+    a = list(base); a[22] = 33
+    assert lib.tmac_wattn_fwd(*a) == -8           # more leading blocks than 128-row blocks
+    a = list(base); a[21] = None
+    assert lib.tmac_wattn_fwd(*a) == -1
     a = list(base); a[1] = (ctypes.c_int64 * 3)(4096 * 1920, 60, 1920)
     assert lib.tmac_wattn_fwd(*a) == -5           # head stride not 16-byte aligned
     a = list(base); a[19] = None
     assert lib.tmac_wattn_fwd(*a) == -1
+
+
+def test_wattn_bwd_argument_errors(lib):
+    st = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1920)
+    base = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, FAKE, FAKE, st, FAKE, st,
+            FAKE, st, 8, 10, 4096, 64, 512, 16, 1, 0, 64, 0.125, FAKE, FAKE, FAKE, 1,
+            FAKE, FAKE, FAKE, 1, 1, None]
+    a = list(base); a[21] = 128
+    assert lib.tmac_wattn_bwd(*a) == -2           # head_dim must be 64
+    a = list(base); a[36] = 0
+    assert lib.tmac_wattn_bwd(*a) == -4           # fp32 backward is not an MFMA path
+    a = list(base); a[23] = 4096
+    assert lib.tmac_wattn_bwd(*a) == -8           # n_persistent >= S (band)
+    a = list(base); a[35] = -1
+    assert lib.tmac_wattn_bwd(*a) == -8
+    a = list(base); a[13] = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1921)
+    assert lib.tmac_wattn_bwd(*a) == -5           # dQ token stride not a multiple of 8
+    a = list(base); a[11] = None
+    assert lib.tmac_wattn_bwd(*a) == -1           # delta workspace
+    a = list(base); a[34] = None
+    assert lib.tmac_wattn_bwd(*a) == -1
+
+
+def test_launch_order():
+    from titans_core.kernels.window_attn import launch_order
+    order, lead = launch_order(np.array([0, 3, 4, 20, 23, 26, 27], dtype=np.int32))
+    # lengths 3, 1, 16, 3, 3, 1 (mean 4.5): longest first, ties by block index
+    assert order.tolist() == [2, 0, 3, 4, 1, 5] and lead == 1
+    order, lead = launch_order(np.array([0, 5, 10, 15], dtype=np.int32))
+    assert order.tolist() == [0, 1, 2] and lead == 0
+    rp, _ = work_list(4096, 512, 16, True, "blockwin", 64)
+    order, lead = launch_order(rp)
+    assert order[0] == 0 and lead == 1 and sorted(order.tolist()) == list(range(32))
+    with pytest.raises(ValueError):
+        launch_order(np.array([0, 3, 2], dtype=np.int32))
 
 
 def test_dwconv_argument_errors(lib):

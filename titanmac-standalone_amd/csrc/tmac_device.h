@@ -118,6 +118,38 @@ __device__ __forceinline__ int xcd_logical_id(int per_xcd) {
   return (b & 7) * per_xcd + (b >> 3);
 }
 
+// Launch map of a per-(b, h) block work list whose lists differ in length.
+// order[0..n_blk) names the blocks heaviest (longest list) first. Workgroup ids
+// [0, n_bh * n_lead) take the n_lead heaviest blocks of every (b, h), so they
+// start first and consecutive ids spread them over the XCDs; ids from lead_pad
+// (n_bh * n_lead rounded up to 8) on take the remaining blocks (b, h)-major,
+// each XCD on one contiguous slice as in xcd_logical_id, so that neighbouring
+// blocks of one head, which share tiles, meet in that XCD's L2.
+struct WorkMap {
+  int n_bh, n_blk, n_lead, lead_pad, per_xcd;
+};
+
+// (bh, block) of this workgroup; false for a padding workgroup.
+__device__ __forceinline__ bool work_item(const WorkMap& m, const int32_t* __restrict__ order,
+                                          int& bh, int& blk) {
+  const int b = blockIdx.x;
+  int rank;
+  if (b < m.lead_pad) {
+    if (b >= m.n_bh * m.n_lead) return false;
+    rank = b / m.n_bh;
+    bh = b - rank * m.n_bh;
+  } else {
+    const int r = b - m.lead_pad;
+    const int logical = (r & 7) * m.per_xcd + (r >> 3);
+    const int rest = m.n_blk - m.n_lead;
+    if (rest <= 0 || logical >= m.n_bh * rest) return false;
+    bh = logical / rest;
+    rank = m.n_lead + (logical - bh * rest);
+  }
+  blk = min(max(order[rank], 0), m.n_blk - 1);
+  return true;
+}
+
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
 }

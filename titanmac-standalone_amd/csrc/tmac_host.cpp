@@ -301,3 +301,24 @@ extern "C" int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int c
   *n_entries = count;
   return TMAC_OK;
 }
+
+extern "C" int tmac_wattn_launch_order(const int32_t* h_ptr, int n_blocks, int32_t* h_order,
+                                       int* n_lead) {
+  if (!h_ptr || !h_order || !n_lead) return TMAC_ERR_NULL;
+  if (n_blocks <= 0) return TMAC_ERR_SHAPE;
+  std::vector<int64_t> len(n_blocks);
+  int64_t total = 0;
+  for (int i = 0; i < n_blocks; ++i) {
+    len[i] = static_cast<int64_t>(h_ptr[i + 1]) - h_ptr[i];
+    if (len[i] < 0) return TMAC_ERR_VALUE;
+    total += len[i];
+  }
+  for (int i = 0; i < n_blocks; ++i) h_order[i] = i;
+  std::stable_sort(h_order, h_order + n_blocks,
+                   [&](int32_t a, int32_t b) { return len[a] > len[b]; });
+  // A block is "leading" when its list is at least twice the mean length.
+  int lead = 0;
+  while (lead < n_blocks && len[h_order[lead]] * n_blocks >= 2 * total && total > 0) ++lead;
+  *n_lead = lead;
+  return TMAC_OK;
+}

@@ -65,15 +65,13 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
     uint16_t* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
-    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries, int n_qb,
-    int n_work, int per_xcd) {
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
   // [buffer][K, V] 64x64 tiles.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
 
-  const int logical = xcd_logical_id(per_xcd);
-  if (logical >= n_work) return;
-  const int bh = logical / n_qb;
-  const int qb = n_qb - 1 - (logical - bh * n_qb);  // later blocks have longer lists: start them first
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
   const int b = bh / H, hd = bh - b * H;
   const int S = mp.S;
 
@@ -233,15 +231,13 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
-    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries, int n_qb,
-    int n_work, int per_xcd) {
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
   __shared__ __attribute__((aligned(16))) float kt_lds[64 * 64];
   __shared__ __attribute__((aligned(16))) float vt_lds[64 * 64];
 
-  const int logical = xcd_logical_id(per_xcd);
-  if (logical >= n_work) return;
-  const int bh = logical / n_qb;
-  const int qb = n_qb - 1 - (logical - bh * n_qb);
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
   const int b = bh / H, hd = bh - b * H;
   const int S = mp.S;
   const int tid = threadIdx.x;
@@ -406,16 +402,14 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
     int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
-    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries, int n_kb,
-    int n_work, int per_xcd) {
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
   // [buffer][Q, dO] 64x64 tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
   __shared__ float stat[2][2][64];
 
-  const int logical = xcd_logical_id(per_xcd);
-  if (logical >= n_work) return;
-  const int bh = logical / n_kb;
-  const int kb = logical - bh * n_kb;
+  int bh, kb;
+  if (!work_item(wm, order, bh, kb)) return;
   const int b = bh / H, hd = bh - b * H;
   const int S = mp.S;
 
@@ -550,13 +544,11 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
     int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    int n_qb, int n_work, int per_xcd) {
+    const int32_t* __restrict__ order, WorkMap wm) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
 
-  const int logical = xcd_logical_id(per_xcd);
-  if (logical >= n_work) return;
-  const int bh = logical / n_qb;
-  const int qb = n_qb - 1 - (logical - bh * n_qb);
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
   const int b = bh / H, hd = bh - b * H;
   const int S = mp.S;
 
@@ -669,6 +661,19 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Launch map and grid size for n_bh heads x n_blk blocks with the n_lead
+// heaviest blocks of each head launched first.
+inline WorkMap make_work_map(int n_bh, int n_blk, int n_lead, unsigned* grid) {
+  WorkMap m;
+  m.n_bh = n_bh;
+  m.n_blk = n_blk;
+  m.n_lead = n_lead;
+  m.lead_pad = (n_bh * n_lead + 7) & ~7;
+  m.per_xcd = (n_bh * (n_blk - n_lead) + 7) / 8;
+  *grid = static_cast<unsigned>(m.lead_pad + 8 * m.per_xcd);
+  return m;
+}
+
 }  // namespace
 
 extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const void* d_K,
@@ -677,9 +682,9 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
                               float* d_lse, int B, int H, int S, int dh, int window,
                               int n_persistent, int causal, int pattern, int block_size,
                               float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
-                              int dtype, void* stream) {
+                              const int32_t* d_order, int n_lead, int dtype, void* stream) {
   if (!d_Q || !d_K || !d_V || !d_O || !q_strides || !k_strides || !v_strides || !o_strides ||
-      !d_row_ptr || !d_entries)
+      !d_row_ptr || !d_entries || !d_order)
     return TMAC_ERR_NULL;
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
   if (dh != 64) return TMAC_ERR_SHAPE;
@@ -698,9 +703,10 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
     return TMAC_ERR_ALIGN;
 
   const int n_qb = (S + 127) / 128;
-  const int64_t n_work = static_cast<int64_t>(B) * H * n_qb;
-  if (n_work > (1ll << 30)) return TMAC_ERR_SHAPE;
-  const int per_xcd = static_cast<int>((n_work + 7) / 8);
+  if (static_cast<int64_t>(B) * H * n_qb > (1ll << 30)) return TMAC_ERR_SHAPE;
+  if (n_lead < 0 || n_lead > n_qb) return TMAC_ERR_VALUE;
+  unsigned grid = 0;
+  const WorkMap wm = make_work_map(B * H, n_qb, n_lead, &grid);
   const MaskParams mp{S, window, n_persistent, causal ? 1 : 0, pattern, block_size};
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -709,26 +715,23 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
   const int64_t* vs = v_strides;
   const int64_t* os = o_strides;
   if (dtype == TMAC_F32) {
-    hipLaunchKernelGGL(wattn_fwd_f32_kernel, dim3(8 * per_xcd), dim3(128), 0, s,
+    hipLaunchKernelGGL(wattn_fwd_f32_kernel, dim3(grid), dim3(128), 0, s,
                        static_cast<const float*>(d_Q), static_cast<const float*>(d_K),
                        static_cast<const float*>(d_V), static_cast<float*>(d_O), d_lse, qs[0],
                        qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2],
-                       H, mp, scale_log2, d_row_ptr, d_entries, n_qb, static_cast<int>(n_work),
-                       per_xcd);
+                       H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
   } else if (dtype == TMAC_BF16) {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16>), dim3(8 * per_xcd), dim3(256), 0, s,
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16>), dim3(grid), dim3(256), 0, s,
                        static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
                        static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
                        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, n_qb,
-                       static_cast<int>(n_work), per_xcd);
+                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
   } else {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16>), dim3(8 * per_xcd), dim3(256), 0, s,
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16>), dim3(grid), dim3(256), 0, s,
                        static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
                        static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
                        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, n_qb,
-                       static_cast<int>(n_work), per_xcd);
+                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
@@ -744,11 +747,13 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
                               const int64_t dv_strides[3], int B, int H, int S, int dh, int window,
                               int n_persistent, int causal, int pattern, int block_size,
                               float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
-                              const int32_t* d_col_ptr, const int32_t* d_entries_kv, int dtype,
-                              void* stream) {
+                              const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
+                              const int32_t* d_entries_kv, const int32_t* d_order_kv,
+                              int n_lead_kv, int dtype, void* stream) {
   if (!d_Q || !d_K || !d_V || !d_O || !d_dO || !d_lse || !d_delta || !d_dQ || !d_dK || !d_dV ||
       !q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides ||
-      !dk_strides || !dv_strides || !d_row_ptr || !d_entries || !d_col_ptr || !d_entries_kv)
+      !dk_strides || !dv_strides || !d_row_ptr || !d_entries || !d_order || !d_col_ptr ||
+      !d_entries_kv || !d_order_kv)
     return TMAC_ERR_NULL;
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
   if (dh != 64) return TMAC_ERR_SHAPE;
@@ -768,9 +773,11 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
     if (!aligned16(p)) return TMAC_ERR_ALIGN;
 
   const int n_qb = (S + 127) / 128;  // 128-query blocks (dQ) and 128-key blocks (dK, dV)
-  const int64_t n_work = static_cast<int64_t>(B) * H * n_qb;
-  if (n_work > (1ll << 30)) return TMAC_ERR_SHAPE;
-  const int per_xcd = static_cast<int>((n_work + 7) / 8);
+  if (static_cast<int64_t>(B) * H * n_qb > (1ll << 30)) return TMAC_ERR_SHAPE;
+  if (n_lead < 0 || n_lead > n_qb || n_lead_kv < 0 || n_lead_kv > n_qb) return TMAC_ERR_VALUE;
+  unsigned grid_q = 0, grid_kv = 0;
+  const WorkMap wm_q = make_work_map(B * H, n_qb, n_lead, &grid_q);
+  const WorkMap wm_kv = make_work_map(B * H, n_qb, n_lead_kv, &grid_kv);
   const MaskParams mp{S, window, n_persistent, causal ? 1 : 0, pattern, block_size};
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -790,15 +797,14 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
   do {                                                                                               \
     hipLaunchKernelGGL((wattn_bwd_delta_kernel<DTV>), dim3(dgrid), dim3(256), 0, s, O, G, d_delta,   \
                        os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);                      \
-    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV>), dim3(8 * per_xcd), dim3(256), 0, s, Q, K, V, G,   \
+    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV>), dim3(grid_kv), dim3(256), 0, s, Q, K, V, G,       \
                        d_lse, d_delta, dK, dV, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],      \
                        vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],    \
-                       dvs[2], H, mp, scale, scale_log2, d_col_ptr, d_entries_kv, n_qb,              \
-                       static_cast<int>(n_work), per_xcd);                                           \
-    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV>), dim3(8 * per_xcd), dim3(256), 0, s, Q, K, V, G,    \
+                       dvs[2], H, mp, scale, scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv); \
+    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV>), dim3(grid_q), dim3(256), 0, s, Q, K, V, G,         \
                        d_lse, d_delta, dQ, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],   \
                        vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H, mp, scale, scale_log2, \
-                       d_row_ptr, d_entries, n_qb, static_cast<int>(n_work), per_xcd);               \
+                       d_row_ptr, d_entries, d_order, wm_q);                                         \
   } while (0)
   if (dtype == TMAC_BF16)
     TMAC_WATTN_BWD(TMAC_BF16);

@@ -14,7 +14,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -43,13 +43,15 @@ SIGNATURES = {
     "tmac_bell_sddmm": [_vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _sz, _i, _i, _i, _i, _i, _vp],
     "tmac_wattn_tile_kinds": [_i, _i, _i, _i, _i, _i, _i, _i, _vp],
     "tmac_wattn_schedule": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
+    "tmac_wattn_launch_order": [_vp, _i, _vp, ctypes.POINTER(_i)],
     "tmac_wattn_fwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
-                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _i, _vp],
+                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
+                       _i, _vp],
     "tmac_wattn_schedule_kv": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
     "tmac_wattn_bwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
                        _vp, _i64p, _vp, _i64p, _vp, _i64p,
-                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _vp,
-                       _i, _vp],
+                       _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
+                       _vp, _vp, _vp, _i, _i, _vp],
     "tmac_dwconv_causal": [_vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
 }
 

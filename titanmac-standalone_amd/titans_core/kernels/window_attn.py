@@ -77,7 +77,27 @@ def work_list(seq_len: int, window_size: int, n_persistent: int, causal: bool = 
     return row_ptr, entries[:n.value]
 
 
+def launch_order(ptr: np.ndarray):
+    """(order int32 [n_blocks], n_lead): blocks by list length, longest first, and the
+    number of leading blocks (lists >= twice the mean) the kernels launch first."""
+    ptr = np.ascontiguousarray(ptr, dtype=np.int32)
+    order = np.zeros(max(ptr.size - 1, 1), dtype=np.int32)
+    n_lead = ctypes.c_int(0)
+    _lib.check(_lib.lib().tmac_wattn_launch_order(ptr.ctypes.data, ptr.size - 1, order.ctypes.data,
+                                                  ctypes.byref(n_lead)), "tmac_wattn_launch_order")
+    return order, n_lead.value
+
+
+def _to_device(ptr, ent, device):
+    order, n_lead = launch_order(ptr)
+    if ent.size == 0:
+        ent = np.zeros(1, dtype=np.int32)
+    return (torch.from_numpy(ptr).to(device), torch.from_numpy(ent).to(device),
+            torch.from_numpy(order).to(device), n_lead)
+
+
 def _device_work_list(S, window, n_persistent, causal, code, block_size, device):
+    """(row_ptr, entries, order) on `device` and n_lead, cached per mask and device."""
     key = (S, window, n_persistent, bool(causal), code, block_size, str(device))
     hit = _sched_cache.get(key)
     if hit is not None:
@@ -85,9 +105,7 @@ def _device_work_list(S, window, n_persistent, causal, code, block_size, device)
     with _sched_lock:
         if key not in _sched_cache:
             rp, ent = work_list(S, window, n_persistent, causal, code, block_size)
-            if ent.size == 0:
-                ent = np.zeros(1, dtype=np.int32)
-            _sched_cache[key] = (torch.from_numpy(rp).to(device), torch.from_numpy(ent).to(device))
+            _sched_cache[key] = _to_device(rp, ent, device)
         return _sched_cache[key]
 
 
@@ -111,6 +129,7 @@ def work_list_kv(seq_len: int, window_size: int, n_persistent: int, causal: bool
 
 
 def _device_work_list_kv(S, window, n_persistent, causal, code, block_size, device):
+    """(col_ptr, entries, order) on `device` and n_lead, cached per mask and device."""
     key = ("kv", S, window, n_persistent, bool(causal), code, block_size, str(device))
     hit = _sched_cache.get(key)
     if hit is not None:
@@ -118,9 +137,7 @@ def _device_work_list_kv(S, window, n_persistent, causal, code, block_size, devi
     with _sched_lock:
         if key not in _sched_cache:
             cp, ent = work_list_kv(S, window, n_persistent, causal, code, block_size)
-            if ent.size == 0:
-                ent = np.zeros(1, dtype=np.int32)
-            _sched_cache[key] = (torch.from_numpy(cp).to(device), torch.from_numpy(ent).to(device))
+            _sched_cache[key] = _to_device(cp, ent, device)
         return _sched_cache[key]
 
 
@@ -159,15 +176,16 @@ def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_si
     lse = torch.empty((B, H, S) if need_lse else (0,), dtype=torch.float32, device=dev)
     if B * H * S == 0:
         return out, lse
-    row_ptr, entries = _device_work_list(S, window_size, n_persistent, causal, pattern,
-                                         block_size, dev)
+    row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
+                                                        pattern, block_size, dev)
     o_view = out.permute(0, 2, 1, 3)  # [B, H, S, dh] view
     with torch.cuda.device(dev):
         rc = _lib.lib().tmac_wattn_fwd(
             _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
             _lib.ptr(out), _strides3(o_view), _lib.ptr(lse) if need_lse else None, B, H, S, dh,
             window_size, n_persistent, int(causal), pattern, block_size, float(scale),
-            _lib.ptr(row_ptr), _lib.ptr(entries), _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+            _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(order), n_lead,
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_wattn_fwd")
     return out, lse
 
@@ -206,10 +224,10 @@ def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
     if B * H * S == 0:
         return tuple(views)
     delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
-    row_ptr, entries = _device_work_list(S, window_size, n_persistent, causal, pattern,
-                                         block_size, dev)
-    col_ptr, entries_kv = _device_work_list_kv(S, window_size, n_persistent, causal, pattern,
-                                               block_size, dev)
+    row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
+                                                        pattern, block_size, dev)
+    col_ptr, entries_kv, order_kv, n_lead_kv = _device_work_list_kv(
+        S, window_size, n_persistent, causal, pattern, block_size, dev)
     o_view, g_view = out.permute(0, 2, 1, 3), grad_out.permute(0, 2, 1, 3)
     with torch.cuda.device(dev):
         rc = _lib.lib().tmac_wattn_bwd(
@@ -219,8 +237,9 @@ def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
             _lib.ptr(grads[0]), _strides3(views[0]), _lib.ptr(grads[1]), _strides3(views[1]),
             _lib.ptr(grads[2]), _strides3(views[2]),
             B, H, S, dh, window_size, n_persistent, int(causal), pattern, block_size,
-            float(scale), _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(col_ptr),
-            _lib.ptr(entries_kv), _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
+            float(scale), _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(order), n_lead,
+            _lib.ptr(col_ptr), _lib.ptr(entries_kv), _lib.ptr(order_kv), n_lead_kv,
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_wattn_bwd")
     return tuple(views)
 
