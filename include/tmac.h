@@ -269,6 +269,24 @@ int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
 int tmac_dwconv_causal(const void* d_in, int64_t ld_in, const void* d_w, void* d_out,
                        int64_t ld_out, int B, int T, int C, int ksize, int dtype, void* stream);
 
+/* Bytes of device workspace tmac_dwconv_causal_bwd needs for these sizes. */
+int tmac_dwconv_causal_bwd_workspace(int B, int T, int C, int ksize, size_t* ws_bytes);
+
+/* Backward of tmac_dwconv_causal:
+ *   d_in[b, t, c] = Σ_j w[c][j] · d_out[b, t + (ksize-1) - j, c]  (rows past T zero)
+ *   dw[c][j]     = Σ_{b, t} d_out[b, t, c] · in[b, t - (ksize-1) + j, c]
+ * Replaces autograd's input and weight gradients of the three depthwise
+ * Conv1d calls of BlockSparseAttention (attn/block_sparse_attention.py
+ * :234-236). d_out, in, d_in: [B, T, C] with row strides ld_dout, ld_in,
+ * ld_din, same dtype and alignment rules as tmac_dwconv_causal; w: [C, ksize]
+ * in that dtype; dw: fp32 [C, ksize], overwritten (not accumulated). The
+ * weight gradient is summed per 64-position chunk into the workspace, then
+ * over the chunks in a fixed order, so it is deterministic. */
+int tmac_dwconv_causal_bwd(const void* d_dout, int64_t ld_dout, const void* d_in,
+                           int64_t ld_in, const void* d_w, void* d_din, int64_t ld_din,
+                           float* d_dw, void* d_ws, size_t ws_bytes, int B, int T, int C,
+                           int ksize, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

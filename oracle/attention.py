@@ -110,6 +110,28 @@ def causal_dwconv(x: np.ndarray, w: np.ndarray, dtype=np.float64) -> np.ndarray:
     return out
 
 
+def causal_dwconv_grads(x: np.ndarray, w: np.ndarray, dout: np.ndarray, dtype=np.float64):
+    """(dx, dw) of causal_dwconv for the output gradient `dout`, tap by tap:
+    tap j (shift s = k-1-j) sends dout[t] back to x[t - s] with weight w[c, j], and
+    collects dw[c, j] = sum over b and t >= s of dout[b, t, c] * x[b, t - s, c]."""
+    x = np.asarray(x, dtype=dtype)
+    w = np.asarray(w, dtype=dtype)
+    dout = np.asarray(dout, dtype=dtype)
+    if w.ndim == 3:
+        w = w[:, 0, :]
+    B, T, C = x.shape
+    k = w.shape[1]
+    dx = np.zeros_like(x)
+    dw = np.zeros((C, k), dtype=dtype)
+    for j in range(k):
+        shift = k - 1 - j
+        if shift >= T:
+            continue
+        dx[:, :T - shift, :] += w[None, None, :, j] * dout[:, shift:, :]
+        dw[:, j] = (dout[:, shift:, :] * x[:, :T - shift, :]).sum(axis=(0, 1))
+    return dx, dw
+
+
 def block_sparse_attention_module(x: np.ndarray, w_qkv: np.ndarray, w_out: np.ndarray,
                                   n_heads: int, window_size: int, block_size: int,
                                   n_persistent: int, causal: bool = True, conv=None,

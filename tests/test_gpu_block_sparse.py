@@ -132,3 +132,99 @@ def test_create_from_config(dev):
     with torch.no_grad():
         y = m.to(dev).eval()(x)
     assert y.shape == (1, 50, 128) and torch.isfinite(y).all()
+
+
+def scaled_close(got, want, atol=2e-2, rtol=1e-2, what=""):
+    """close() on both tensors divided by max(1, max |want|)."""
+    want = np.asarray(want, dtype=np.float64)
+    sc = max(1.0, float(np.abs(want).max())) if want.size else 1.0
+    try:
+        close(np.asarray(got, dtype=np.float64) / sc, want / sc, atol, rtol)
+    except AssertionError as e:
+        raise AssertionError(f"{what}: {e}") from None
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,C,k", [(1, 1, 8, 4), (2, 3, 16, 4), (1, 64, 8, 1), (2, 65, 24, 4),
+                                     (1, 300, 1920, 4), (3, 130, 40, 8), (1, 129, 64, 3)])
+def test_dwconv_backward_parity(dev, dtype, B, T, C, k):
+    """grad_x against the oracle (fp32: 1e-5 of the largest entry; 16-bit: close());
+    grad_weight, an fp32 sum of exact 16-bit products, within 1e-4 of its largest entry."""
+    g = torch.Generator().manual_seed(T * 11 + C + k)
+    x = torch.randn(B, T, C, generator=g).to(dtype)
+    w = (torch.randn(C, k, generator=g) * 0.5).to(dtype)
+    dy = torch.randn(B, T, C, generator=g).to(dtype)
+    xd, wd = x.to(dev).requires_grad_(), w.to(dev).requires_grad_()
+    causal_dwconv(xd, wd).backward(dy.to(dev))
+    dx, dw = oa.causal_dwconv_grads(x.float().numpy(), w.float().numpy(), dy.float().numpy())
+    got_dx = xd.grad.float().cpu().numpy()
+    if dtype == torch.float32:
+        assert np.abs(got_dx - dx).max() <= 1e-5 * max(1.0, np.abs(dx).max())
+    else:
+        close(got_dx, dx)
+    assert wd.grad.dtype == dtype
+    got_dw = wd.grad.float().cpu().numpy()
+    tol = 1e-4 if dtype == torch.float32 else 1e-2  # the 16-bit weight grad is rounded on return
+    assert np.abs(got_dw - dw).max() <= tol * max(1.0, np.abs(dw).max())
+
+
+def test_dwconv_backward_strided_and_deterministic(dev):
+    g = torch.Generator().manual_seed(21)
+    big = torch.randn(2, 500, 96, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(32, 4, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    dy = torch.randn(2, 500, 32, generator=g).to(torch.bfloat16).to(dev)
+    from titans_core.kernels.conv import dwconv_causal_bwd
+    x = big[:, :, 32:64]
+    dx1, dw1 = dwconv_causal_bwd(dy, x, w)
+    dx2, dw2 = dwconv_causal_bwd(dy, x, w)
+    assert torch.equal(dx1, dx2) and torch.equal(dw1, dw2) and dw1.dtype == torch.float32
+    want_dx, want_dw = oa.causal_dwconv_grads(x.float().cpu().numpy(), w.float().cpu().numpy(),
+                                              dy.float().cpu().numpy())
+    close(dx1.float().cpu().numpy(), want_dx)
+    assert np.abs(dw1.cpu().numpy() - want_dw).max() <= 1e-4 * np.abs(want_dw).max()
+
+
+def _bsa_grads_fp64(m, x, dy):
+    """fp64 CPU autograd of BlockSparseAttention's function on the module's own weights:
+    projection, the three causal depthwise convolutions (torch conv1d), masked attention
+    with the block-window mask, output projection."""
+    ps = {n: p.detach().double().cpu().requires_grad_() for n, p in m.named_parameters()}
+    xd = x.detach().double().cpu().requires_grad_()
+    B, T, D = x.shape
+    H, dh = m.n_heads, D // m.n_heads
+    qkv = xd @ ps["qkv_proj.weight"].T
+    parts = []
+    for t, name in zip(qkv.chunk(3, dim=-1), "qkv"):
+        w = ps[f"conv_{name}.weight"]
+        k = w.shape[-1]
+        t = torch.nn.functional.conv1d(t.transpose(1, 2), w, padding=k - 1, groups=D)[..., :T]
+        parts.append(t.transpose(1, 2).reshape(B, T, H, dh).transpose(1, 2))
+    mask = om.blockwin_mask(T, m.window_size, m.block_size, m.n_persistent, m.causal)
+    add = torch.zeros(T, T, dtype=torch.float64).masked_fill(~torch.from_numpy(mask), float("-inf"))
+    o = torch.nn.functional.scaled_dot_product_attention(*parts, attn_mask=add)
+    y = o.transpose(1, 2).reshape(B, T, D) @ ps["out_proj.weight"].T
+    y.backward(dy.double().cpu())
+    return xd.grad.numpy(), {n: p.grad.numpy() for n, p in ps.items()}
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_module_training_step_bf16(dev, causal):
+    """BlockSparseAttention (d=128, 2 heads, w=128, block 64, Np=16) in bf16: gradients of
+    x and of every parameter against fp64 autograd of the same function."""
+    g = torch.Generator().manual_seed(22)
+    m = tc.BlockSparseAttention(128, 2, window_size=128, block_size=64, n_persistent=16,
+                                causal=causal)
+    with torch.no_grad():
+        m.qkv_proj.weight.copy_(torch.randn(384, 128, generator=g) * 0.06)
+        m.out_proj.weight.copy_(torch.randn(128, 128, generator=g) * 0.06)
+        for c in (m.conv_q, m.conv_k, m.conv_v):
+            c.weight.copy_(torch.randn(128, 1, 4, generator=g) * 0.4)
+    m = m.to(dev, torch.bfloat16).train()
+    x = torch.randn(2, 300, 128, generator=g).to(torch.bfloat16)
+    dy = torch.randn(2, 300, 128, generator=g).to(torch.bfloat16)
+    xd = x.to(dev).requires_grad_()
+    m(xd).backward(dy.to(dev))
+    want_x, want = _bsa_grads_fp64(m, x, dy)
+    scaled_close(xd.grad.float().cpu().numpy(), want_x, atol=2e-2, rtol=2e-2, what="x")
+    for n, p in m.named_parameters():
+        scaled_close(p.grad.float().cpu().numpy(), want[n], atol=2e-2, rtol=2e-2, what=n)

@@ -49,6 +49,21 @@ def test_grads_single_allowed_key():
     assert np.allclose(dv, do) and np.abs(dq).max() < 1e-12 and np.abs(dk).max() < 1e-12
 
 
+@pytest.mark.parametrize("B,T,C,k", [(2, 1, 3, 4), (2, 7, 5, 4), (1, 30, 6, 1), (3, 20, 4, 8)])
+def test_conv_grads_against_torch_autograd(B, T, C, k):
+    """The written-out conv backward against autograd of torch's grouped conv1d (fp64)."""
+    rng = np.random.default_rng(7)
+    x, dout = rng.standard_normal((B, T, C)), rng.standard_normal((B, T, C))
+    w = rng.standard_normal((C, k))
+    dx, dw = oa.causal_dwconv_grads(x, w, dout)
+    xt = torch.from_numpy(x).requires_grad_()
+    wt = torch.from_numpy(w[:, None, :]).requires_grad_()
+    y = torch.nn.functional.conv1d(xt.transpose(1, 2), wt, padding=k - 1, groups=C)[..., :T]
+    y.transpose(1, 2).backward(torch.from_numpy(dout))
+    assert np.allclose(dx, xt.grad.numpy(), rtol=1e-12, atol=1e-12)
+    assert np.allclose(dw, wt.grad.numpy()[:, 0, :], rtol=1e-12, atol=1e-12)
+
+
 def test_single_allowed_key_returns_that_value():
     # Np = 0, w = 0: every row sees only itself.
     rng = np.random.default_rng(1)

@@ -20,7 +20,9 @@ matmul with ``torch.cat`` of the persistent keys per block. Here the three
 convolutions are one HIP launch on the fused projection
 (``titans_core.kernels.conv``) and the attention is one launch of the
 tile-sparse kernel with the block-window pattern
-(``titans_core.kernels.window_attn``); no CPU or SDPA fallback.
+(``titans_core.kernels.window_attn``); no CPU or SDPA fallback. Both have HIP
+backward kernels (16-bit attention; convolution in every dtype), so the module
+trains.
 """
 from __future__ import annotations
 

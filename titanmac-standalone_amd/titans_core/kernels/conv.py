@@ -10,6 +10,8 @@ layout in one launch (C = 3d when q, k and v come from one fused projection):
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from . import _lib
@@ -42,6 +44,58 @@ def dwconv_causal(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
 @dwconv_causal.register_fake
 def _(x, weight):
     return x.new_empty(x.shape)
+
+
+@torch.library.custom_op("titanmac::dwconv_causal_bwd", mutates_args=())
+def dwconv_causal_bwd(grad_out: torch.Tensor, x: torch.Tensor,
+                      weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(grad_x [B, T, C] in x's dtype, grad_weight [C, k] fp32) of dwconv_causal."""
+    if grad_out.shape != x.shape or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
+        raise ValueError("dwconv_causal_bwd: grad_out must match x [B, T, C] and weight be [C, k]")
+    dev = _lib.require_device(grad_out, x, weight, what="dwconv_causal backward")
+    B, T, C = (int(s) for s in x.shape)
+    k = int(weight.shape[1])
+    g = grad_out.to(x.dtype)
+    if g.stride(2) != 1 or g.stride(0) != T * g.stride(1):
+        g = g.contiguous()
+    if x.stride(2) != 1 or x.stride(0) != T * x.stride(1):
+        x = x.contiguous()
+    w = weight.contiguous()
+    dx = torch.empty((B, T, C), dtype=x.dtype, device=dev)
+    dw = torch.empty((C, k), dtype=torch.float32, device=dev)
+    if B * T * C == 0:
+        return dx, dw.zero_()
+    L = _lib.lib()
+    ws_bytes = ctypes.c_size_t(0)
+    _lib.check(L.tmac_dwconv_causal_bwd_workspace(B, T, C, k, ctypes.byref(ws_bytes)),
+               "tmac_dwconv_causal_bwd_workspace")
+    ws = torch.empty(max(ws_bytes.value, 16), dtype=torch.uint8, device=dev)
+    with torch.cuda.device(dev):
+        rc = L.tmac_dwconv_causal_bwd(_lib.ptr(g), g.stride(1), _lib.ptr(x), x.stride(1),
+                                      _lib.ptr(w), _lib.ptr(dx), C, _lib.ptr(dw), _lib.ptr(ws),
+                                      ws.numel(), B, T, C, k, _lib.dtype_code(x.dtype),
+                                      _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_dwconv_causal_bwd")
+    return dx, dw
+
+
+@dwconv_causal_bwd.register_fake
+def _(grad_out, x, weight):
+    return x.new_empty(x.shape), weight.new_empty(weight.shape, dtype=torch.float32)
+
+
+def _setup(ctx, inputs, output):
+    x, weight = inputs
+    ctx.save_for_backward(x, weight)
+
+
+def _backward(ctx, grad):
+    x, weight = ctx.saved_tensors
+    dx, dw = dwconv_causal_bwd(grad, x, weight)
+    return dx, dw.to(weight.dtype)
+
+
+dwconv_causal.register_autograd(_backward, setup_context=_setup)
 
 
 def causal_dwconv(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
