@@ -287,6 +287,35 @@ int tmac_dwconv_causal_bwd(const void* d_dout, int64_t ld_dout, const void* d_in
                            float* d_dw, void* d_ws, size_t ws_bytes, int B, int T, int C,
                            int ksize, int dtype, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* RMSNorm (device).                                                          */
+/* ------------------------------------------------------------------------- */
+
+/* y[m, :] = x[m, :] · r[m] · scale,  r[m] = 1 / sqrt(mean(x[m, :]²) + eps),
+ * fp32 arithmetic, y in the input dtype. Replaces RMSNorm.forward
+ * (blocks/norms.py:44-62), TitanBlock's two pre-norms
+ * (blocks/titan_block.py:46-47,91,96). x, y: [M, D] with row strides ldx, ldy;
+ * scale: [D] in the same dtype; rstd (nullable): fp32 [M] receives r (what the
+ * backward needs). 1 <= D <= 4096, D and the row strides multiples of 8
+ * (16-bit) or 4 (fp32); pointers 16-byte aligned. dtype: TMAC_F32, TMAC_BF16
+ * or TMAC_F16. */
+int tmac_rmsnorm_fwd(const void* d_x, int64_t ldx, const void* d_scale, void* d_y,
+                     int64_t ldy, float* d_rstd, int M, int D, float eps, int dtype,
+                     void* stream);
+
+/* Bytes of device workspace tmac_rmsnorm_bwd needs for these sizes. */
+int tmac_rmsnorm_bwd_workspace(int M, int D, size_t* ws_bytes);
+
+/* Backward of tmac_rmsnorm_fwd (autograd of blocks/norms.py:58-62):
+ *   dx = r·(dy ⊙ scale) − x · r³ · mean(dy ⊙ scale ⊙ x),
+ *   dscale = Σ_m dy[m, :] ⊙ x[m, :] · r[m]  (fp32 [D], overwritten).
+ * rstd from the forward. dscale is summed per 16 rows into the workspace, then
+ * over those partials in a fixed order, so it is deterministic. */
+int tmac_rmsnorm_bwd(const void* d_dy, int64_t lddy, const void* d_x, int64_t ldx,
+                     const void* d_scale, const float* d_rstd, void* d_dx, int64_t lddx,
+                     float* d_dscale, void* d_ws, size_t ws_bytes, int M, int D, int dtype,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

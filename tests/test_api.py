@@ -182,3 +182,70 @@ def test_block_sparse_attention_refuses_cpu_tensors():
     m = tc.BlockSparseAttention(128, 2, window_size=16, block_size=16, n_persistent=2)
     with pytest.raises(RuntimeError, match="GPU"):
         m(torch.randn(1, 20, 128))
+
+
+def test_block_ell_linear_loads_dense_checkpoint():
+    """A dense nn.Linear state_dict loads into a Block-ELL layer: the pattern stays,
+    the stored blocks are the dense weight's blocks at it."""
+    torch.manual_seed(1)
+    lin = nn.Linear(256, 384)
+    e = BlockELLLinear(256, 384, density=0.5, seed=5)
+    ci = e.col_idx.clone()
+    e.load_state_dict(lin.state_dict())
+    assert torch.equal(e.col_idx, ci) and torch.equal(e.bias, lin.bias)
+    assert torch.equal(e.values, BlockELLLinear.from_linear(lin, col_idx=ci.numpy()).values)
+    with pytest.raises(ValueError, match="does not match"):
+        e.load_state_dict(nn.Linear(128, 384).state_dict())
+
+
+def test_mlp_block_dense_conversions():
+    torch.manual_seed(2)
+    dense = MLPBlock(128, 256)
+    ell = MLPBlock.from_dense(dense, density=0.5, seed=4)
+    assert ell.block_ell and ell.fc1.width == 2 and ell.fc2.width == 1
+    back = ell.to_dense()
+    assert set(back.state_dict()) == set(dense.state_dict())
+    assert torch.equal(back.fc1.weight, ell.fc1.to_dense_weight())
+    # magnitude pruning of the densified block finds exactly the stored blocks again
+    again = MLPBlock.from_dense(back, density=0.5, select="magnitude")
+    assert torch.equal(again.fc1.col_idx, ell.fc1.col_idx)
+    assert torch.equal(again.fc2.values, ell.fc2.values)
+    # and a dense MLP checkpoint loads straight into a Block-ELL MLP (strict)
+    cfg = tc.TitanMACConfig(d_model=128, d_ff=256, mlp_block_ell=True, mlp_density=0.5)
+    m = MLPBlock.from_config(cfg)
+    m.load_state_dict(dense.state_dict())
+    assert torch.equal(m.fc1.to_dense_weight(),
+                       BlockELLLinear.from_linear(dense.fc1, col_idx=m.fc1.col_idx.numpy())
+                       .to_dense_weight())
+
+
+@pytest.mark.parametrize("block_sparse", [True, False])
+def test_titan_block_construction_and_state_dict(block_sparse):
+    cfg = tc.TitanMACConfig(d_model=640, n_heads=10, d_ff=2560, use_block_sparse=block_sparse)
+    b = tc.TitanBlock(cfg)
+    sd = {k: tuple(v.shape) for k, v in b.state_dict().items()}
+    # the reference's keys and shapes (blocks/titan_block.py:46-71)
+    want = {"norm_attn.scale": (640,), "norm_mlp.scale": (640,),
+            "attention.qkv_proj.weight": (1920, 640), "attention.out_proj.weight": (640, 640),
+            "mlp.fc1.weight": (2560, 640), "mlp.fc1.bias": (2560,),
+            "mlp.fc2.weight": (640, 2560), "mlp.fc2.bias": (640,)}
+    if block_sparse:
+        want.update({f"attention.conv_{t}.weight": (640, 1, 4) for t in "qkv"})
+        assert isinstance(b.attention, tc.BlockSparseAttention)
+    else:
+        assert isinstance(b.attention, WindowedAttention)
+    assert sd == want
+    assert b.norm_attn.eps == cfg.norm_eps and torch.equal(b.norm_mlp.scale, torch.ones(640))
+
+
+def test_titan_block_ell_loads_dense_reference_checkpoint():
+    dense = tc.TitanBlock(tc.TitanMACConfig(d_model=128, n_heads=2, d_ff=256))
+    ell = tc.TitanBlock(tc.TitanMACConfig(d_model=128, n_heads=2, d_ff=256, mlp_block_ell=True))
+    ell.load_state_dict(dense.state_dict())
+    assert torch.equal(ell.attention.qkv_proj.weight, dense.attention.qkv_proj.weight)
+    assert isinstance(ell.mlp.fc1, BlockELLLinear)
+
+
+def test_rms_norm_refuses_cpu_tensors():
+    with pytest.raises(RuntimeError, match="GPU"):
+        tc.RMSNorm(64)(torch.randn(2, 64))

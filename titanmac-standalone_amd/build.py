@@ -35,7 +35,8 @@ HIP_FLAGS = [
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
-SOURCES = ["tmac_host.cpp", "bell_kernels.hip", "wattn_kernels.hip", "conv_kernels.hip"]
+SOURCES = ["tmac_host.cpp", "bell_kernels.hip", "wattn_kernels.hip", "conv_kernels.hip",
+           "norm_kernels.hip"]
 
 
 def _hipcc() -> str:

@@ -2,20 +2,21 @@
 
 Drop-in Python API of the reference's hot path over hand-written HIP kernels:
 ``WindowedAttention`` / ``WindowConfig`` / ``build_band_mask`` (attention),
-``MLPBlock`` with Block-ELL linears (``BlockELLLinear``, ``block_ell_mm``) and
+``BlockSparseAttention``, ``MLPBlock`` with Block-ELL linears
+(``BlockELLLinear``, ``block_ell_mm``), ``RMSNorm``, ``TitanBlock`` and
 ``TitanMACConfig``. Importing the package does not load the GPU library; the
 first kernel call does, and raises if libtmac.so is missing.
 """
 from .attn import (BlockSparseAttention, WindowConfig, WindowedAttention, build_band_mask,
                    create_block_sparse_attention)
-from .blocks import MLPBlock
+from .blocks import MLPBlock, RMSNorm, TitanBlock
 from .config import TITANS_VARIANTS, TitanMACConfig
-from .kernels import (BlockELLLinear, BlockELLPattern, block_ell_mm, causal_dwconv,
+from .kernels import (BlockELLLinear, BlockELLPattern, block_ell_mm, causal_dwconv, rms_norm,
                       windowed_attention)
 
 __version__ = "0.1.0"
 
 __all__ = ["TitanMACConfig", "TITANS_VARIANTS", "WindowedAttention", "WindowConfig",
            "build_band_mask", "BlockSparseAttention", "create_block_sparse_attention", "MLPBlock",
-           "BlockELLLinear", "BlockELLPattern", "block_ell_mm", "causal_dwconv",
-           "windowed_attention"]
+           "RMSNorm", "TitanBlock", "BlockELLLinear", "BlockELLPattern", "block_ell_mm",
+           "causal_dwconv", "rms_norm", "windowed_attention"]

@@ -1,4 +1,6 @@
-"""Transformer blocks of the TitanMAC hot path."""
+"""Transformer blocks of the TitanMAC hot path (reference: blocks/)."""
 from .mlp import MLPBlock
+from .norms import RMSNorm
+from .titan_block import TitanBlock
 
-__all__ = ["MLPBlock"]
+__all__ = ["MLPBlock", "RMSNorm", "TitanBlock"]

@@ -1,7 +1,8 @@
 """HIP kernels of the TitanMAC sparse hot path (libtmac.so, gfx950), with their torch ops."""
 from .block_ell import BlockELLLinear, BlockELLPattern, block_ell_mm
 from .conv import causal_dwconv
-from .window_attn import tile_kinds, windowed_attention, work_list
+from .norm import rms_norm
+from .window_attn import tile_kinds, windowed_attention, work_list, work_list_kv
 
-__all__ = ["BlockELLLinear", "BlockELLPattern", "block_ell_mm", "causal_dwconv",
-           "windowed_attention", "tile_kinds", "work_list"]
+__all__ = ["BlockELLLinear", "BlockELLPattern", "block_ell_mm", "causal_dwconv", "rms_norm",
+           "windowed_attention", "tile_kinds", "work_list", "work_list_kv"]

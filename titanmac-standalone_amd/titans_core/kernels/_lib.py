@@ -56,6 +56,9 @@ SIGNATURES = {
     "tmac_dwconv_causal_bwd_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
     "tmac_dwconv_causal_bwd": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _i,
                                _i, _vp],
+    "tmac_rmsnorm_fwd": [_vp, _i64, _vp, _vp, _i64, _vp, _i, _i, ctypes.c_float, _i, _vp],
+    "tmac_rmsnorm_bwd_workspace": [_i, _i, ctypes.POINTER(_sz)],
+    "tmac_rmsnorm_bwd": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _vp],
 }
 
 

@@ -345,6 +345,21 @@ class BlockELLLinear(nn.Module):
             nn.init.uniform_(self.bias, -bound, bound)
 
     def _load_from_state_dict(self, state_dict, prefix, *args, **kwargs):
+        wkey = prefix + "weight"
+        if wkey in state_dict and prefix + "values" not in state_dict:
+            # A dense nn.Linear checkpoint (weight [out, in]): keep the Block-ELL pattern
+            # (this module's, or the checkpoint's col_idx when it has one) and take the
+            # weight's blocks at it; the rest of the dense weight is pruned.
+            W = state_dict.pop(wkey)
+            if tuple(W.shape) != (self.out_features, self.in_features):
+                raise ValueError(f"{wkey}: dense weight {tuple(W.shape)} does not match "
+                                 f"[{self.out_features}, {self.in_features}]")
+            ci = state_dict.get(prefix + "col_idx", self.col_idx).to(torch.int64).cpu()
+            n_brow, n_bcol = self.in_features // BLOCK, self.out_features // BLOCK
+            blocks = W.detach().t().reshape(n_brow, BLOCK, n_bcol, BLOCK).permute(0, 2, 1, 3)
+            rows = torch.arange(n_brow)[:, None].expand(-1, ci.shape[1])
+            state_dict[prefix + "values"] = blocks[rows, ci.to(W.device)].contiguous()
+            state_dict.setdefault(prefix + "col_idx", ci.to(torch.int32))
         key = prefix + "col_idx"
         if key in state_dict:
             ci = state_dict[key]
