@@ -13,14 +13,17 @@ The same run also times, as secondary figures:
     denominator of `attn_speedup_vs_dense`);
   - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
     masked bf16 backward (five bmm over the full S x S);
-  - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40).
+  - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40);
+  - the causal depthwise conv of BlockSparseAttention (B=8, T=4096, 1920 channels,
+    4 taps) and TitanBlock's RMSNorm (32768 x 640), forward and backward, in GB/s
+    of compulsory HBM traffic.
 Inputs are drawn on the CPU from fixed seeds and copied to HBM before timing.
 Kernel time is measured with HIP events on the launch stream (torch's current
 stream) around exactly K back-to-back launches after W warm-up launches.
 The CPU baseline runs the oracle's dense restatement of the reference path
 (X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only.
 
-Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, copy (a
+Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, conv, norm, copy (a
 plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
 """
 from __future__ import annotations
@@ -229,6 +232,80 @@ def dense_attention_bwd_baseline(att, bwd, steps: int, stream):
     return timed(dense_bwd, max(2, steps // 10), 2, stream)
 
 
+CONV = dict(B=8, T=4096, C=1920, k=4, seed=5)   # BlockSparseAttention q/k/v conv at config 3's shape
+NORM = dict(M=32768, D=640, seed=6)               # TitanBlock RMSNorm over config 3's tokens
+
+
+def setup_conv(dev):
+    """Causal depthwise conv (fused q/k/v channels) forward and backward, bf16."""
+    import ctypes
+    c = CONV
+    B, T, C, k = c["B"], c["T"], c["C"], c["k"]
+    x = gen((B, T, C), c["seed"]).to(dev)
+    w = gen((C, k), c["seed"] + 1, 0.5).to(dev)
+    dy = gen((B, T, C), c["seed"] + 2).to(dev)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    dw = torch.empty(C, k, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    n = ctypes.c_size_t(0)
+    _lib.check(L.tmac_dwconv_causal_bwd_workspace(B, T, C, k, ctypes.byref(n)), "workspace")
+    ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_ptr(dev)
+
+    def fwd():
+        rc = L.tmac_dwconv_causal(_lib.ptr(x), C, _lib.ptr(w), _lib.ptr(y), C, B, T, C, k,
+                                  _lib.BF16, stream)
+        if rc:
+            _lib.check(rc, "tmac_dwconv_causal")
+
+    def bwd():
+        rc = L.tmac_dwconv_causal_bwd(_lib.ptr(dy), C, _lib.ptr(x), C, _lib.ptr(w), _lib.ptr(dx),
+                                      C, _lib.ptr(dw), _lib.ptr(ws), ws.numel(), B, T, C, k,
+                                      _lib.BF16, stream)
+        if rc:
+            _lib.check(rc, "tmac_dwconv_causal_bwd")
+
+    act = B * T * C * 2
+    return dict(fwd=fwd, bwd=bwd, fwd_bytes=2 * act, bwd_bytes=3 * act,
+                keep=(x, w, dy, y, dx, dw, ws))
+
+
+def setup_norm(dev):
+    """RMSNorm forward and backward, bf16 [M, D]."""
+    import ctypes
+    c = NORM
+    M, D = c["M"], c["D"]
+    x = gen((M, D), c["seed"]).to(dev)
+    sc = gen((D,), c["seed"] + 1).to(dev)
+    dy = gen((M, D), c["seed"] + 2).to(dev)
+    y, dx = torch.empty_like(x), torch.empty_like(x)
+    rstd = torch.empty(M, dtype=torch.float32, device=dev)
+    dsc = torch.empty(D, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    n = ctypes.c_size_t(0)
+    _lib.check(L.tmac_rmsnorm_bwd_workspace(M, D, ctypes.byref(n)), "workspace")
+    ws = torch.empty(n.value, dtype=torch.uint8, device=dev)
+    stream = _lib.stream_ptr(dev)
+
+    def fwd():
+        rc = L.tmac_rmsnorm_fwd(_lib.ptr(x), D, _lib.ptr(sc), _lib.ptr(y), D, _lib.ptr(rstd), M, D,
+                                1e-5, _lib.BF16, stream)
+        if rc:
+            _lib.check(rc, "tmac_rmsnorm_fwd")
+
+    def bwd():
+        rc = L.tmac_rmsnorm_bwd(_lib.ptr(dy), D, _lib.ptr(x), D, _lib.ptr(sc), _lib.ptr(rstd),
+                                _lib.ptr(dx), D, _lib.ptr(dsc), _lib.ptr(ws), ws.numel(), M, D,
+                                _lib.BF16, stream)
+        if rc:
+            _lib.check(rc, "tmac_rmsnorm_bwd")
+
+    fwd()
+    act = M * D * 2
+    return dict(fwd=fwd, bwd=bwd, fwd_bytes=2 * act + 4 * M, bwd_bytes=3 * act + 4 * M,
+                keep=(x, sc, dy, y, dx, rstd, dsc, ws))
+
+
 def setup_dx_sddmm(dev):
     c = CFG4
     pat = BlockELLPattern.sample(c["seed"], c["n_brow"], c["n_bcol"], c["width"])
@@ -344,7 +421,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "copy"])
+    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "conv",
+                                                     "norm", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the hot path's kernels run on one MI355X and this "
@@ -395,6 +473,14 @@ def main() -> int:
             ms = timed(bw["sddmm"], K, W, stream)
             out["sddmm"] = dict(ms=ms, tflops=bw["flops"] / ms / 1e9, gbs=bw["sd_bytes"] / ms / 1e6)
 
+    for mode, setup in (("conv", setup_conv), ("norm", setup_norm)):
+        if args.mode in ("all", mode):
+            wl = setup(dev)
+            f_ms = timed(wl["fwd"], K, W, stream)
+            b_ms = timed(wl["bwd"], K, W, stream)
+            out[mode] = dict(fwd_ms=f_ms, fwd_gbs=wl["fwd_bytes"] / f_ms / 1e6, bwd_ms=b_ms,
+                             bwd_gbs=wl["bwd_bytes"] / b_ms / 1e6)
+
     if args.mode != "all":
         print(json.dumps({"mode": args.mode, **out}))
         return 0
@@ -443,6 +529,14 @@ def main() -> int:
             "bell_sddmm_cfg4_ms": round(out["sddmm"]["ms"], 5),
             "bell_sddmm_cfg4_tflops": round(out["sddmm"]["tflops"], 3),
             "bell_sddmm_cfg4_hbm_gbs_compulsory": round(out["sddmm"]["gbs"], 1),
+            "dwconv_fwd_ms": round(out["conv"]["fwd_ms"], 5),
+            "dwconv_fwd_hbm_gbs_compulsory": round(out["conv"]["fwd_gbs"], 1),
+            "dwconv_bwd_ms": round(out["conv"]["bwd_ms"], 5),
+            "dwconv_bwd_hbm_gbs_compulsory": round(out["conv"]["bwd_gbs"], 1),
+            "rmsnorm_fwd_ms": round(out["norm"]["fwd_ms"], 5),
+            "rmsnorm_fwd_hbm_gbs_compulsory": round(out["norm"]["fwd_gbs"], 1),
+            "rmsnorm_bwd_ms": round(out["norm"]["bwd_ms"], 5),
+            "rmsnorm_bwd_hbm_gbs_compulsory": round(out["norm"]["bwd_gbs"], 1),
         },
     }
     if not args.no_cpu:

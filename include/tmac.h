@@ -309,7 +309,7 @@ int tmac_rmsnorm_bwd_workspace(int M, int D, size_t* ws_bytes);
 /* Backward of tmac_rmsnorm_fwd (autograd of blocks/norms.py:58-62):
  *   dx = r·(dy ⊙ scale) − x · r³ · mean(dy ⊙ scale ⊙ x),
  *   dscale = Σ_m dy[m, :] ⊙ x[m, :] · r[m]  (fp32 [D], overwritten).
- * rstd from the forward. dscale is summed per 16 rows into the workspace, then
+ * rstd from the forward. dscale is summed per 64 rows into the workspace, then
  * over those partials in a fixed order, so it is deterministic. */
 int tmac_rmsnorm_bwd(const void* d_dy, int64_t lddy, const void* d_x, int64_t ldx,
                      const void* d_scale, const float* d_rstd, void* d_dx, int64_t lddx,

@@ -10,10 +10,11 @@
 // so no transposes are needed.
 //
 // Memory-bound stencil: each thread owns one 16-byte vector of channels and a
-// chunk of 64 consecutive positions, keeps the last k input rows in registers
-// (fp32) and writes each output row once; consecutive threads read consecutive
-// 16-byte pieces of a row, so every row is read with full coalescing. The
-// halo (k-1 rows before the chunk) is the only re-read.
+// chunk of 64 consecutive positions, keeps a window of input rows in registers
+// (fp32), loads the rows in groups of 4 before using them (four loads in
+// flight per thread) and writes each output row once; consecutive threads read
+// consecutive 16-byte pieces of a row, so every row is read with full
+// coalescing. The halo (k-1 rows before the chunk) is the only re-read.
 
 #include "tmac_device.h"
 
@@ -22,6 +23,7 @@ using namespace tmac;
 namespace {
 
 constexpr int kChunk = 64;  // positions per thread
+constexpr int kGroup = 4;   // rows loaded together before use (memory-level parallelism)
 
 template <int DT>
 struct Vec;
@@ -67,6 +69,17 @@ struct Vec<TMAC_BF16> : Vec16<TMAC_BF16> {};
 template <>
 struct Vec<TMAC_F16> : Vec16<TMAC_F16> {};
 
+// Row `row` of a [rows, ld] buffer when `ok`, else zeros, without a branch: the
+// load always reads a valid row (row 0 when not ok), so a group of these stays
+// in flight together instead of each waiting behind its own branch.
+template <int DT, int NN>
+__device__ __forceinline__ void load_or_zero(const uint8_t* base, int64_t row_bytes, int row,
+                                             bool ok, float (&v)[NN]) {
+  Vec<DT>::load(base + static_cast<int64_t>(ok ? row : 0) * row_bytes, v);
+#pragma unroll
+  for (int e = 0; e < NN; ++e) v[e] = ok ? v[e] : 0.f;
+}
+
 template <int DT, int KS>
 __global__ __launch_bounds__(256) void dwconv_causal_kernel(const uint8_t* __restrict__ in,
                                                             int64_t ld_in, const uint8_t* __restrict__ w,
@@ -75,10 +88,12 @@ __global__ __launch_bounds__(256) void dwconv_causal_kernel(const uint8_t* __res
   using V = Vec<DT>;
   constexpr int N = V::N;
   constexpr int E = DT == TMAC_F32 ? 4 : 2;  // bytes per element
+  constexpr int W = KS - 1 + kGroup;         // window rows
   const int vc = blockIdx.y * 256 + threadIdx.x;
   if (vc * N >= C) return;
   const int b = blockIdx.x / n_chunks;
   const int t0 = (blockIdx.x - b * n_chunks) * kChunk;
+  const int t1 = min(t0 + kChunk, T);
   const int c0 = vc * N;
 
   // Taps of this thread's channels: wt[j][i] = w[c0 + i][j] (weights are
@@ -97,33 +112,37 @@ __global__ __launch_bounds__(256) void dwconv_causal_kernel(const uint8_t* __res
 
   const uint8_t* ib = in + (static_cast<int64_t>(b) * T) * ld_in * E + static_cast<int64_t>(c0) * E;
   uint8_t* ob = out + (static_cast<int64_t>(b) * T) * ld_out * E + static_cast<int64_t>(c0) * E;
-  // ring[j] holds input row t - (KS-1) + j for the row t being produced.
-  float ring[KS][N];
+  // win[i] holds input row t - (KS-1) + i for the group of rows t .. t + kGroup - 1.
+  float win[W][N];
+  const int64_t rb_in = ld_in * E;
 #pragma unroll
-  for (int j = 0; j < KS - 1; ++j) {
-    const int t = t0 - (KS - 1) + j;
-    if (t >= 0)
-      V::load(ib + static_cast<int64_t>(t) * ld_in * E, ring[j]);
-    else
-#pragma unroll
-      for (int i = 0; i < N; ++i) ring[j][i] = 0.f;
+  for (int i = 0; i < KS - 1; ++i) {
+    const int t = t0 - (KS - 1) + i;
+    load_or_zero<DT>(ib, rb_in, t, t >= 0, win[i]);
   }
-  const int t1 = min(t0 + kChunk, T);
-  for (int t = t0; t < t1; ++t) {
-    V::load(ib + static_cast<int64_t>(t) * ld_in * E, ring[KS - 1]);
-    float o[N];
+  for (int t = t0; t < t1; t += kGroup) {
+    // the group's kGroup input rows are loaded before any is used
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      float acc = 0.f;
+    for (int u = 0; u < kGroup; ++u) load_or_zero<DT>(ib, rb_in, t + u, t + u < t1, win[KS - 1 + u]);
 #pragma unroll
-      for (int j = 0; j < KS; ++j) acc = fmaf(wt[j][i], ring[j][i], acc);
-      o[i] = acc;
+    for (int u = 0; u < kGroup; ++u) {
+      if (t + u < t1) {
+        float o[N];
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int j = 0; j < KS; ++j) acc = fmaf(wt[j][e], win[u + j][e], acc);
+          o[e] = acc;
+        }
+        V::store(ob + static_cast<int64_t>(t + u) * ld_out * E, o);
+      }
     }
-    V::store(ob + static_cast<int64_t>(t) * ld_out * E, o);
+    // move down, lowest slot first (the slots overlap when KS - 1 > kGroup)
 #pragma unroll
-    for (int j = 0; j < KS - 1; ++j)
+    for (int i = 0; i < KS - 1; ++i)
 #pragma unroll
-      for (int i = 0; i < N; ++i) ring[j][i] = ring[j + 1][i];
+      for (int e = 0; e < N; ++e) win[i][e] = win[kGroup + i][e];
   }
 }
 
@@ -166,11 +185,11 @@ int launch_dwconv(const void* d_in, int64_t ld_in, const void* d_w, void* d_out,
 //   d_in[b, t, c] = Σ_j w[c, j] · d_out[b, t + (k-1) - j, c]   (d_out[b, >= T, c] = 0)
 //   dw[c, j]     = Σ_{b, t} d_out[b, t, c] · in[b, t - (k-1) + j, c]
 // Each thread owns one 16-byte vector of channels and a chunk of 64 positions,
-// walks the chunk from its end with register rings of the k d_out rows
-// starting at t and of the k input rows ending at t, writes each d_in row once
-// and its chunk's partial dw (fp32 [N channels][k]) to one workspace row.
-// dwconv_wgrad_reduce_kernel then sums the partials of every (c, j) in chunk
-// order, so dw is deterministic.
+// walks the chunk from its end in groups of 4 rows with register windows of
+// the d_out rows from t on and the input rows up to t, writes each d_in row
+// once and its chunk's partial dw (fp32, tap-major) to one workspace row.
+// column_sum_kernel then sums the partials of every (c, j) in a fixed order,
+// so dw is deterministic.
 template <int DT, int KS>
 __global__ __launch_bounds__(256) void dwconv_causal_bwd_kernel(
     const uint8_t* __restrict__ dout, int64_t ld_dout, const uint8_t* __restrict__ in,
@@ -179,6 +198,7 @@ __global__ __launch_bounds__(256) void dwconv_causal_bwd_kernel(
   using V = Vec<DT>;
   constexpr int N = V::N;
   constexpr int E = DT == TMAC_F32 ? 4 : 2;
+  constexpr int W = KS - 1 + kGroup;
   const int vc = blockIdx.y * 256 + threadIdx.x;
   if (vc * N >= C) return;
   const int b = blockIdx.x / n_chunks;
@@ -204,74 +224,66 @@ __global__ __launch_bounds__(256) void dwconv_causal_bwd_kernel(
   const uint8_t* ib = in + row0 * ld_in * E + static_cast<int64_t>(c0) * E;
   uint8_t* db = din + row0 * ld_din * E + static_cast<int64_t>(c0) * E;
 
-  // g[j] = d_out row t + j (g[0] loaded per step); x[j] = input row t - (KS-1) + j;
-  // set up for t = t1 - 1.
-  float g[KS][N], x[KS][N], dw[KS][N];
+  // Groups of kGroup rows t0 + gU .. t0 + gU + kGroup - 1, walked from the top.
+  // For the group with first row tb: gw[i] = d_out row tb + i and
+  // xw[i] = input row tb - (KS-1) + i, i < W. The KS-1 rows one group shares
+  // with the next lower one move from the bottom of the windows to the top.
+  float gw[W][N], xw[W][N], dw[KS][N];
+  const int n_groups = (t1 - t0 + kGroup - 1) / kGroup;
+  int tb = t0 + (n_groups - 1) * kGroup;
+  const int64_t rb_g = ld_dout * E, rb_in = ld_in * E;
 #pragma unroll
-  for (int j = 0; j < KS; ++j) {
-    const int tg = t1 - 1 + j;
-    if (j > 0 && tg < T)
-      V::load(gb + static_cast<int64_t>(tg) * ld_dout * E, g[j]);
-    else
-#pragma unroll
-      for (int i = 0; i < N; ++i) g[j][i] = 0.f;
-    const int tx = t1 - KS + j;
-    if (tx >= 0)
-      V::load(ib + static_cast<int64_t>(tx) * ld_in * E, x[j]);
-    else
-#pragma unroll
-      for (int i = 0; i < N; ++i) x[j][i] = 0.f;
-#pragma unroll
-    for (int i = 0; i < N; ++i) dw[j][i] = 0.f;
+  for (int i = kGroup; i < W; ++i) {
+    const int tg = tb + i, tx = tb - (KS - 1) + i;
+    load_or_zero<DT>(gb, rb_g, tg, tg < T, gw[i]);
+    load_or_zero<DT>(ib, rb_in, tx, tx >= 0 && tx < t1, xw[i]);
   }
-  for (int t = t1 - 1; t >= t0; --t) {
-    V::load(gb + static_cast<int64_t>(t) * ld_dout * E, g[0]);
-    float o[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) {
-      float acc = 0.f;
+  for (int j = 0; j < KS; ++j)
 #pragma unroll
-      for (int j = 0; j < KS; ++j) {
-        acc = fmaf(wt[j][i], g[KS - 1 - j][i], acc);
-        dw[j][i] = fmaf(g[0][i], x[j][i], dw[j][i]);
-      }
-      o[i] = acc;
+    for (int e = 0; e < N; ++e) dw[j][e] = 0.f;
+  for (; tb >= t0; tb -= kGroup) {
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int tg = tb + u, tx = tb - (KS - 1) + u;  // d_out rows in [t1, T) are the next chunk's
+      load_or_zero<DT>(gb, rb_g, tg, tg < T, gw[u]);
+      load_or_zero<DT>(ib, rb_in, tx, tx >= 0 && tx < t1, xw[u]);
     }
-    V::store(db + static_cast<int64_t>(t) * ld_din * E, o);
-    // step to t - 1: d_out rows move up one slot, input rows down one slot and
-    // input row t - KS enters at the bottom
 #pragma unroll
-    for (int j = KS - 1; j > 0; --j)
+    for (int u = 0; u < kGroup; ++u) {
+      if (tb + u < t1) {
+        float o[N];
 #pragma unroll
-      for (int i = 0; i < N; ++i) g[j][i] = g[j - 1][i];
+        for (int e = 0; e < N; ++e) {
+          float acc = 0.f;
 #pragma unroll
-    for (int j = KS - 1; j > 0; --j)
+          for (int j = 0; j < KS; ++j) {
+            acc = fmaf(wt[j][e], gw[u + KS - 1 - j][e], acc);
+            dw[j][e] = fmaf(gw[u][e], xw[u + j][e], dw[j][e]);
+          }
+          o[e] = acc;
+        }
+        V::store(db + static_cast<int64_t>(tb + u) * ld_din * E, o);
+      }
+    }
+    // move up, highest slot first (the slots overlap when KS - 1 > kGroup)
 #pragma unroll
-      for (int i = 0; i < N; ++i) x[j][i] = x[j - 1][i];
-    const int tx = t - KS;
-    if (tx >= 0 && t > t0)
-      V::load(ib + static_cast<int64_t>(tx) * ld_in * E, x[0]);
-    else
+    for (int i = KS - 2; i >= 0; --i)
 #pragma unroll
-      for (int i = 0; i < N; ++i) x[0][i] = 0.f;
+      for (int e = 0; e < N; ++e) {
+        gw[kGroup + i][e] = gw[i][e];
+        xw[kGroup + i][e] = xw[i][e];
+      }
   }
-  // partial[(b * n_chunks + chunk)][c][j], contiguous N*KS floats per thread
-  float* pp = partial + (static_cast<int64_t>(blockIdx.x) * C + c0) * KS;
+  // partial[(b * n_chunks + chunk)][j][c]: for each tap, consecutive threads
+  // write consecutive 16-byte pieces (coalesced); the reduction transposes to [c][j].
+  float* pp = partial + static_cast<int64_t>(blockIdx.x) * C * KS + c0;
 #pragma unroll
-  for (int i = 0; i < N; ++i)
+  for (int j = 0; j < KS; ++j)
 #pragma unroll
-    for (int j = 0; j < KS; ++j) pp[i * KS + j] = dw[j][i];
-}
-
-// dw[e] = Σ_p partial[p][e] over p = 0..P-1 in order, e = c * KS + j; fp32.
-__global__ __launch_bounds__(256) void dwconv_wgrad_reduce_kernel(const float* __restrict__ partial,
-                                                                  float* __restrict__ dw,
-                                                                  int64_t n_elem, int P) {
-  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= n_elem) return;
-  float acc = 0.f;
-  for (int p = 0; p < P; ++p) acc += partial[static_cast<int64_t>(p) * n_elem + e];
-  dw[e] = acc;
+    for (int i = 0; i < N; i += 4)
+      *reinterpret_cast<f32x4*>(pp + static_cast<int64_t>(j) * C + i) =
+          f32x4{dw[j][i], dw[j][i + 1], dw[j][i + 2], dw[j][i + 3]};
 }
 
 template <int DT>
@@ -308,8 +320,8 @@ int launch_dwconv_bwd(const void* d_dout, int64_t ld_dout, const void* d_in, int
   }
 #undef TMAC_DWCONV_BWD_CASE
   const int64_t n_elem = static_cast<int64_t>(C) * ks;
-  hipLaunchKernelGGL(dwconv_wgrad_reduce_kernel, dim3(static_cast<unsigned>((n_elem + 255) / 256)),
-                     dim3(256), 0, s, ws, d_dw, n_elem, static_cast<int>(gx));
+  hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((n_elem + 63) / 64)), dim3(256), 0,
+                     s, ws, d_dw, n_elem, static_cast<int>(gx), static_cast<int64_t>(C));
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }

@@ -7,8 +7,8 @@
 // vectors of the row (8 16-bit or 4 fp32 elements) in registers, fp32
 // arithmetic, rows of up to 4096 elements. The backward
 //   dx = r·(g ⊙ scale) − x · r³ · mean(g ⊙ scale ⊙ x),   dscale = Σ_m g ⊙ x · r
-// writes each wave's partial dscale row to a workspace and sums the rows in a
-// fixed order, so dscale is deterministic.
+// writes each workgroup's partial dscale row (64 rows of x) to a workspace and
+// sums the partial rows in a fixed order, so dscale is deterministic.
 
 #include "tmac_device.h"
 
@@ -16,7 +16,7 @@ using namespace tmac;
 
 namespace {
 
-constexpr int kRowsPerWave = 16;  // backward: rows per wave, one dscale partial per wave
+constexpr int kRowsPerWave = 16;  // backward: rows per wave; 64 rows per dscale partial
 
 template <int DT>
 struct Vec;
@@ -112,8 +112,10 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_kernel(const uint8_t* __restr
   }
 }
 
-// Backward: wave w of the grid owns rows [16w, 16w + 16); partial[w][:] = its
-// rows' Σ g ⊙ x · r.
+// Backward: workgroup b owns rows [64b, 64b + 64), wave w of it rows
+// 64b + 16w .. +16, walked with the next row's loads issued before the current
+// row's arithmetic. The four waves' Σ g ⊙ x · r are added through LDS in wave
+// order into partial[b][:]. Dynamic LDS: 3 * D floats.
 template <int DT, int NV>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
     const uint8_t* __restrict__ g, int64_t ldg, const uint8_t* __restrict__ x, int64_t ldx,
@@ -122,12 +124,12 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
   using V = Vec<DT>;
   constexpr int N = V::N;
   constexpr int E = DT == TMAC_F32 ? 4 : 2;
-  const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+  extern __shared__ float red[];  // [3][D]: waves 1..3
+  const int w = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int n_vec = D / N;
-  const int r0 = wave * kRowsPerWave;
-  if (r0 >= M) return;
-  const int r1 = min(r0 + kRowsPerWave, M);
+  const int r0 = blockIdx.x * (4 * kRowsPerWave) + w * kRowsPerWave;
+  const int r1 = min(r0 + kRowsPerWave, M);  // r0 >= r1: no rows, but the wave still joins the barrier
   float sc[NV][N], ds[NV][N];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -140,18 +142,30 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
 #pragma unroll
       for (int e = 0; e < N; ++e) sc[i][e] = 0.f;
   }
-  for (int row = r0; row < r1; ++row) {
-    const float r = rstd[row];
+  float gv[NV][N], xv[NV][N];
+  auto load_row = [&](int row, float (&gg)[NV][N], float (&xx)[NV][N])
+      __attribute__((always_inline)) {
     const uint8_t* gr = g + static_cast<int64_t>(row) * ldg * E;
     const uint8_t* xr = x + static_cast<int64_t>(row) * ldx * E;
-    float gv[NV][N], xv[NV][N];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (c < n_vec) {
+        V::load(gr + static_cast<int64_t>(c) * N * E, gg[i]);
+        V::load(xr + static_cast<int64_t>(c) * N * E, xx[i]);
+      }
+    }
+  };
+  if (r0 < r1) load_row(r0, gv, xv);
+  for (int row = r0; row < r1; ++row) {
+    float gn[NV][N], xn[NV][N];
+    if (row + 1 < r1) load_row(row + 1, gn, xn);
+    const float r = rstd[row];
     float dot = 0.f;  // Σ g ⊙ scale ⊙ x
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       const int c = lane + 64 * i;
       if (c < n_vec) {
-        V::load(gr + static_cast<int64_t>(c) * N * E, gv[i]);
-        V::load(xr + static_cast<int64_t>(c) * N * E, xv[i]);
 #pragma unroll
         for (int e = 0; e < N; ++e) {
           dot = fmaf(gv[i][e] * sc[i][e], xv[i][e], dot);
@@ -172,26 +186,37 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(
         V::store(dr + static_cast<int64_t>(c) * N * E, o);
       }
     }
-  }
-  float* pr = partial + static_cast<int64_t>(wave) * D;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int c = lane + 64 * i;
-    if (c < n_vec)
+    for (int i = 0; i < NV; ++i)
 #pragma unroll
-      for (int e = 0; e < N; ++e) pr[c * N + e] = ds[i][e];
+      for (int e = 0; e < N; ++e) {
+        gv[i][e] = gn[i][e];
+        xv[i][e] = xn[i][e];
+      }
   }
-}
-
-// dscale[d] = Σ_p partial[p][d], p = 0..P-1 in order.
-__global__ __launch_bounds__(256) void rmsnorm_dscale_reduce_kernel(const float* __restrict__ partial,
-                                                                    float* __restrict__ dscale,
-                                                                    int D, int P) {
-  const int d = blockIdx.x * 256 + threadIdx.x;
-  if (d >= D) return;
-  float acc = 0.f;
-  for (int p = 0; p < P; ++p) acc += partial[static_cast<int64_t>(p) * D + d];
-  dscale[d] = acc;
+  if (w > 0) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (c < n_vec)
+#pragma unroll
+        for (int e = 0; e < N; ++e) red[(w - 1) * D + c * N + e] = ds[i][e];
+    }
+  }
+  __syncthreads();
+  if (w == 0) {
+    float* pr = partial + static_cast<int64_t>(blockIdx.x) * D;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int c = lane + 64 * i;
+      if (c < n_vec)
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          const int d = c * N + e;
+          pr[d] = ((ds[i][e] + red[d]) + red[D + d]) + red[2 * D + d];
+        }
+    }
+  }
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -245,14 +270,15 @@ void launch_bwd(const void* g, int64_t ldg, const void* x, int64_t ldx, const vo
                 const float* rstd, void* dx, int64_t lddx, float* dscale, float* ws, int M, int D,
                 hipStream_t s) {
   const int nv = nv_for(D / Vec<DT>::N);
-  const int n_waves = (M + kRowsPerWave - 1) / kRowsPerWave;
-  const dim3 grid(static_cast<unsigned>((n_waves + 3) / 4));
+  const int n_blocks = (M + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave);
+  const dim3 grid(static_cast<unsigned>(n_blocks));
+  const size_t shmem = 3 * static_cast<size_t>(D) * sizeof(float);
   const auto* gp = static_cast<const uint8_t*>(g);
   const auto* xp = static_cast<const uint8_t*>(x);
   const auto* sp = static_cast<const uint8_t*>(scale);
   auto* dp = static_cast<uint8_t*>(dx);
 #define TMAC_RMS_BWD(NVV)                                                                          \
-  hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, NVV>), grid, dim3(256), 0, s, gp, ldg, xp, ldx, sp,  \
+  hipLaunchKernelGGL((rmsnorm_bwd_kernel<DT, NVV>), grid, dim3(256), shmem, s, gp, ldg, xp, ldx, sp, \
                      rstd, dp, lddx, ws, M, D)
   switch (nv) {
     case 1: TMAC_RMS_BWD(1); break;
@@ -269,8 +295,8 @@ void launch_bwd(const void* g, int64_t ldg, const void* x, int64_t ldx, const vo
       break;
   }
 #undef TMAC_RMS_BWD
-  hipLaunchKernelGGL(rmsnorm_dscale_reduce_kernel, dim3(static_cast<unsigned>((D + 255) / 256)),
-                     dim3(256), 0, s, ws, dscale, D, n_waves);
+  hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((D + 63) / 64)), dim3(256), 0, s,
+                     ws, dscale, static_cast<int64_t>(D), n_blocks, int64_t{0});
 }
 
 }  // namespace
@@ -300,7 +326,7 @@ extern "C" int tmac_rmsnorm_fwd(const void* d_x, int64_t ldx, const void* d_scal
 extern "C" int tmac_rmsnorm_bwd_workspace(int M, int D, size_t* ws_bytes) {
   if (!ws_bytes) return TMAC_ERR_NULL;
   if (M <= 0 || D <= 0) return TMAC_ERR_SHAPE;
-  *ws_bytes = static_cast<size_t>((M + kRowsPerWave - 1) / kRowsPerWave) * D * sizeof(float);
+  *ws_bytes = static_cast<size_t>((M + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave)) * D * sizeof(float);
   return TMAC_OK;
 }
 

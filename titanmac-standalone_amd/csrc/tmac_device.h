@@ -150,6 +150,46 @@ __device__ __forceinline__ bool work_item(const WorkMap& m, const int32_t* __res
   return true;
 }
 
+// out[o(e)] = Σ_{p < P} part[p * n + e] for e < n (fp32 partial sums of a
+// weight gradient), o(e) = e, or with inner > 0 the transpose of an
+// [n / inner, inner] row-major column index: o(e) = (e % inner) * (n / inner)
+// + e / inner. Workgroup = 64 consecutive columns x 4 waves; wave w sums
+// rows p ≡ w (mod 4) into 8 independent accumulators (rows p ≡ w + 4j
+// (mod 32)), so each lane keeps 8 loads in flight, and the 32 partial sums of
+// a column are added through LDS in a fixed order: deterministic for given
+// (n, P). Launch with grid ceil(n / 64), 256 threads.
+static __global__ __launch_bounds__(256) void column_sum_kernel(const float* __restrict__ part,
+                                                                float* __restrict__ out,
+                                                                int64_t n, int P, int64_t inner) {
+  __shared__ float red[4][8][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 64 + lane;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  if (e < n) {
+    int p = w;
+    for (; p + 28 < P; p += 32) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] += part[static_cast<int64_t>(p + 4 * j) * n + e];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (p + 4 * j < P) acc[j] += part[static_cast<int64_t>(p + 4 * j) * n + e];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[w][j][lane] = acc[j];
+  __syncthreads();
+  if (w == 0 && e < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) t += red[ww][j][lane];
+    out[inner > 0 ? (e % inner) * (n / inner) + e / inner : e] = t;
+  }
+}
+
 __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
 }
