@@ -233,7 +233,8 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
  * row_ptr/entries/order/n_lead: as for tmac_wattn_fwd;
  * col_ptr/entries_kv: tmac_wattn_schedule_kv with k_block = 128,
  * sub_cols = 32, order_kv/n_lead_kv: tmac_wattn_launch_order of col_ptr
- * (device copies). dtype: TMAC_BF16 or TMAC_F16; dh = 64. */
+ * (device copies). dtype: TMAC_BF16 / TMAC_F16 (MFMA kernels) or TMAC_F32
+ * (FMA kernels, for fp32 modules); dh = 64. */
 int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
                    const void* d_V, const int64_t v_strides[3],

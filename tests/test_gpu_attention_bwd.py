@@ -66,6 +66,19 @@ def test_backward_parity_16bit(dev, dtype, B, H, S, w, Np, causal, pattern, bs):
         close(got.float().cpu(), ref, what=f"d{name}")
 
 
+@pytest.mark.parametrize("B,H,S,w,Np,causal,pattern,bs", GRID[::2] + [GRID[11]])
+def test_backward_parity_fp32(dev, B, H, S, w, Np, causal, pattern, bs):
+    """fp32 path (FMA kernels): within 1e-4 of the largest gradient entry."""
+    q, k, v, do = tensors((B, H, S, 64), torch.float32, seed=5 * S + w)
+    _, dq, dk, dv = run_bwd(dev, q, k, v, do, w, Np, causal, pattern, bs)
+    mask = om.make_mask(S, w, Np, causal, pattern, bs)
+    want = oa.masked_attention_grads(*(t.numpy() for t in (q, k, v, do)), mask)
+    for got, ref, name in zip((dq, dk, dv), want, "qkv"):
+        assert got.dtype == torch.float32
+        err = np.abs(got.cpu().numpy() - ref).max()
+        assert err <= 1e-4 * max(1.0, np.abs(ref).max()), f"d{name}: {err}"
+
+
 def test_lse_matches_oracle(dev):
     B, H, S, w, Np = 2, 3, 300, 100, 5
     q, k, v = tensors((B, H, S, 64), torch.bfloat16, seed=11, n=3)
@@ -137,6 +150,24 @@ def _module_grads_fp64(m, x, dy, mask, conv=False):
     y = o.transpose(1, 2).reshape(B, T, D) @ w_out.T
     y.backward(dy.double().cpu())
     return xd.grad.numpy(), w_qkv.grad.numpy(), w_out.grad.numpy()
+
+
+def test_windowed_attention_module_training_step_fp32(dev):
+    """The fp32 module (the reference trains in fp32 unless AMP is on): gradients of x and
+    both projections within 1e-4 of the largest entry of fp64 autograd."""
+    cfg = tc.WindowConfig(window_size=64, num_heads=2, head_dim=64, n_persistent=8)
+    m = tc.WindowedAttention(cfg).to(dev).train()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(2, 200, 128, generator=g)
+    dy = torch.randn(2, 200, 128, generator=g)
+    xd = x.to(dev).requires_grad_()
+    m(xd).backward(dy.to(dev))
+    want = _module_grads_fp64(m, x, dy, om.band_mask(200, 64, 8))
+    got = (xd.grad, m.qkv_proj.weight.grad, m.out_proj.weight.grad)
+    for a, b, name in zip(got, want, ("x", "w_qkv", "w_out")):
+        err = np.abs(a.cpu().numpy() - b).max()
+        assert err <= 1e-4 * max(1.0, np.abs(b).max()), f"{name}: {err}"
 
 
 def test_windowed_attention_module_training_step_bf16(dev):

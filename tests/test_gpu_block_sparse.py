@@ -228,3 +228,26 @@ def test_module_training_step_bf16(dev, causal):
     scaled_close(xd.grad.float().cpu().numpy(), want_x, atol=2e-2, rtol=2e-2, what="x")
     for n, p in m.named_parameters():
         scaled_close(p.grad.float().cpu().numpy(), want[n], atol=2e-2, rtol=2e-2, what=n)
+
+
+def test_module_training_step_fp32(dev):
+    """fp32 BlockSparseAttention (the reference trains in fp32 unless AMP is on): x and
+    parameter gradients within 1e-4 of the largest entry of fp64 autograd."""
+    g = torch.Generator().manual_seed(23)
+    m = tc.BlockSparseAttention(128, 2, window_size=96, block_size=32, n_persistent=8)
+    with torch.no_grad():
+        m.qkv_proj.weight.copy_(torch.randn(384, 128, generator=g) * 0.06)
+        m.out_proj.weight.copy_(torch.randn(128, 128, generator=g) * 0.06)
+        for c in (m.conv_q, m.conv_k, m.conv_v):
+            c.weight.copy_(torch.randn(128, 1, 4, generator=g) * 0.4)
+    m = m.to(dev).train()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    x = torch.randn(2, 150, 128, generator=g)
+    dy = torch.randn(2, 150, 128, generator=g)
+    xd = x.to(dev).requires_grad_()
+    m(xd).backward(dy.to(dev))
+    want_x, want = _bsa_grads_fp64(m, x, dy)
+    assert np.abs(xd.grad.cpu().numpy() - want_x).max() <= 1e-4 * max(1.0, np.abs(want_x).max())
+    for n, p in m.named_parameters():
+        err = np.abs(p.grad.cpu().numpy() - want[n]).max()
+        assert err <= 1e-4 * max(1.0, np.abs(want[n]).max()), f"{n}: {err}"

@@ -221,8 +221,10 @@ def test_wattn_bwd_argument_errors(lib):
             FAKE, FAKE, FAKE, 1, 1, None]
     a = list(base); a[21] = 128
     assert lib.tmac_wattn_bwd(*a) == -2           # head_dim must be 64
-    a = list(base); a[36] = 0
-    assert lib.tmac_wattn_bwd(*a) == -4           # fp32 backward is not an MFMA path
+    a = list(base); a[36] = 9
+    assert lib.tmac_wattn_bwd(*a) == -4           # unknown dtype
+    a = list(base); a[36] = 0; a[1] = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1922)
+    assert lib.tmac_wattn_bwd(*a) == -5           # fp32: strides in whole 16-byte vectors
     a = list(base); a[23] = 4096
     assert lib.tmac_wattn_bwd(*a) == -8           # n_persistent >= S (band)
     a = list(base); a[35] = -1

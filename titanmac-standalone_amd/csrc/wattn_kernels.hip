@@ -659,6 +659,225 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   store_row64<DT>(dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss, dqt, scale, h);
 }
 
+// fp32 backward (FMA path, for fp32 modules). Δ[b, h, q] = Σ_d dO · O, eight
+// lanes per row.
+__global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
+    const float* __restrict__ O, const float* __restrict__ dO, float* __restrict__ delta,
+    int64_t osb, int64_t osh, int64_t oss, int64_t gsb, int64_t gsh, int64_t gss, int H, int S,
+    int64_t n_rows) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 32 + (threadIdx.x >> 3);
+  const int ch = threadIdx.x & 7;
+  float acc = 0.f;
+  if (row < n_rows) {
+    const int64_t bh = row / S;
+    const int q = static_cast<int>(row - bh * S);
+    const int b = static_cast<int>(bh / H), hd = static_cast<int>(bh - static_cast<int64_t>(b) * H);
+    const float* op = O + b * osb + hd * osh + static_cast<int64_t>(q) * oss + 8 * ch;
+    const float* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(q) * gss + 8 * ch;
+#pragma unroll
+    for (int i = 0; i < 8; i += 4) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(op + i);
+      const f32x4 g = *reinterpret_cast<const f32x4*>(gp + i);
+      acc = fmaf(o.x, g.x, fmaf(o.y, g.y, fmaf(o.z, g.z, fmaf(o.w, g.w, acc))));
+    }
+  }
+  acc += __shfl_xor(acc, 1);
+  acc += __shfl_xor(acc, 2);
+  acc += __shfl_xor(acc, 4);
+  if (row < n_rows && ch == 0) delta[row] = acc;
+}
+
+// fp32 dQ: one query row per thread (128 per workgroup, the forward's work
+// list); K and V tiles staged in LDS and read as broadcasts.
+__global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
+    int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
+    int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
+    float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
+  __shared__ __attribute__((aligned(16))) float kt_lds[64 * 64];
+  __shared__ __attribute__((aligned(16))) float vt_lds[64 * 64];
+
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+  const int tid = threadIdx.x;
+  const int q_row = qb * 128 + tid;
+  const int qc = min(q_row, S - 1);
+  const int sub = tid >> 5;
+
+  float q[64], g[64], dq[64];
+  {
+    const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss;
+    const float* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss;
+#pragma unroll
+    for (int d = 0; d < 64; d += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(qp + d);
+      const f32x4 w = *reinterpret_cast<const f32x4*>(gp + d);
+      q[d] = v.x * scale_log2;
+      q[d + 1] = v.y * scale_log2;
+      q[d + 2] = v.z * scale_log2;
+      q[d + 3] = v.w * scale_log2;
+      g[d] = w.x;
+      g[d + 1] = w.y;
+      g[d + 2] = w.z;
+      g[d + 3] = w.w;
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 64; ++d) dq[d] = 0.f;
+  const float l2 = lse[static_cast<int64_t>(bh) * S + qc] * kLog2e;
+  const float dl = delta[static_cast<int64_t>(bh) * S + qc];
+
+  const float* Kbh = K + b * ksb + hd * ksh;
+  const float* Vbh = V + b * vsb + hd * vsh;
+  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int kt = ent & 0xffff;
+    __syncthreads();
+    for (int c = tid; c < 64 * 16; c += 128) {
+      const int row = c >> 4, col = (c & 15) * 4;
+      const int key = min(kt * 64 + row, S - 1);
+      *reinterpret_cast<f32x4*>(kt_lds + row * 64 + col) =
+          *reinterpret_cast<const f32x4*>(Kbh + key * kss + col);
+      *reinterpret_cast<f32x4*>(vt_lds + row * 64 + col) =
+          *reinterpret_cast<const f32x4*>(Vbh + key * vss + col);
+    }
+    __syncthreads();
+    const int kind = (ent >> (16 + 2 * sub)) & 3;
+    if (kind == 0) continue;
+    for (int j = 0; j < 64; ++j) {
+      float sj = 0.f, dp = 0.f;
+#pragma unroll
+      for (int d = 0; d < 64; ++d) {
+        sj = fmaf(q[d], kt_lds[j * 64 + d], sj);
+        dp = fmaf(g[d], vt_lds[j * 64 + d], dp);
+      }
+      float pj = __builtin_amdgcn_exp2f(sj - l2);
+      if (kind == 2 && !allowed(mp, q_row, kt * 64 + j)) pj = 0.f;
+      const float ds = pj * (dp - dl);
+#pragma unroll
+      for (int d = 0; d < 64; ++d) dq[d] = fmaf(ds, kt_lds[j * 64 + d], dq[d]);
+    }
+  }
+  if (q_row >= S) return;
+  float* dp_out = dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss;
+#pragma unroll
+  for (int d = 0; d < 64; d += 4)
+    *reinterpret_cast<f32x4*>(dp_out + d) =
+        f32x4{dq[d] * scale, dq[d + 1] * scale, dq[d + 2] * scale, dq[d + 3] * scale};
+}
+
+// fp32 dK, dV: two lanes per key (lane and lane + 32 hold head dims 0..31 and
+// 32..63), 32 keys per wave, 128 per workgroup (the key-major work list); Q,
+// dO, LSE and Δ of each listed 64-query tile staged in LDS.
+__global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dK, float* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
+    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
+    int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
+    int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
+  __shared__ __attribute__((aligned(16))) float q_lds[64 * 64];
+  __shared__ __attribute__((aligned(16))) float g_lds[64 * 64];
+  __shared__ float l2_lds[64], dl_lds[64];
+
+  int bh, kb;
+  if (!work_item(wm, order, bh, kb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int half = lane >> 5;
+  const int key = kb * 128 + wave * 32 + (lane & 31);
+  const int kc = min(key, S - 1);
+
+  float k[32], v[32], dk[32], dv[32];
+  {
+    const float* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + 32 * half;
+    const float* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + 32 * half;
+#pragma unroll
+    for (int d = 0; d < 32; d += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(kp + d);
+      const f32x4 c = *reinterpret_cast<const f32x4*>(vp + d);
+      k[d] = a.x;
+      k[d + 1] = a.y;
+      k[d + 2] = a.z;
+      k[d + 3] = a.w;
+      v[d] = c.x;
+      v[d + 1] = c.y;
+      v[d + 2] = c.z;
+      v[d + 3] = c.w;
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < 32; ++d) {
+    dk[d] = 0.f;
+    dv[d] = 0.f;
+  }
+  const float* Qbh = Q + b * qsb + hd * qsh;
+  const float* Gbh = dO + b * gsb + hd * gsh;
+  const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
+  const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
+  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int qt = ent & 0xffff;
+    __syncthreads();
+    for (int c = tid; c < 64 * 16; c += 256) {
+      const int row = c >> 4, col = (c & 15) * 4;
+      const int qr = min(qt * 64 + row, S - 1);
+      *reinterpret_cast<f32x4*>(q_lds + row * 64 + col) =
+          *reinterpret_cast<const f32x4*>(Qbh + qr * qss + col);
+      *reinterpret_cast<f32x4*>(g_lds + row * 64 + col) =
+          *reinterpret_cast<const f32x4*>(Gbh + qr * gss + col);
+    }
+    if (tid < 64) {
+      const int qr = min(qt * 64 + tid, S - 1);
+      l2_lds[tid] = lse_bh[qr] * kLog2e;
+      dl_lds[tid] = dl_bh[qr];
+    }
+    __syncthreads();
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    if (kind == 0) continue;
+    for (int i = 0; i < 64; ++i) {
+      const float* qi = q_lds + i * 64 + 32 * half;
+      const float* gi = g_lds + i * 64 + 32 * half;
+      float sp = 0.f, dpp = 0.f;
+#pragma unroll
+      for (int d = 0; d < 32; ++d) {
+        sp = fmaf(qi[d], k[d], sp);
+        dpp = fmaf(gi[d], v[d], dpp);
+      }
+      sp += __shfl_xor(sp, 32);
+      dpp += __shfl_xor(dpp, 32);
+      float pi = __builtin_amdgcn_exp2f(sp * scale_log2 - l2_lds[i]);
+      if (kind == 2 && !allowed(mp, qt * 64 + i, key)) pi = 0.f;
+      const float ds = pi * (dpp - dl_lds[i]);
+#pragma unroll
+      for (int d = 0; d < 32; ++d) {
+        dv[d] = fmaf(pi, gi[d], dv[d]);
+        dk[d] = fmaf(ds, qi[d], dk[d]);
+      }
+    }
+  }
+  if (key >= S) return;
+  float* dkp = dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss + 32 * half;
+  float* dvp = dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss + 32 * half;
+#pragma unroll
+  for (int d = 0; d < 32; d += 4) {
+    *reinterpret_cast<f32x4*>(dkp + d) =
+        f32x4{dk[d] * scale, dk[d + 1] * scale, dk[d + 2] * scale, dk[d + 3] * scale};
+    *reinterpret_cast<f32x4*>(dvp + d) = f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]};
+  }
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Launch map and grid size for n_bh heads x n_blk blocks with the n_lead
@@ -762,12 +981,13 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
   if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
   if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
   if (!(scale > 0.f)) return TMAC_ERR_VALUE;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16-byte vector
   const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides,
                            do_strides, dq_strides, dk_strides, dv_strides};
   for (const int64_t* st : all)
     for (int i = 0; i < 3; ++i)
-      if (st[i] < 0 || st[i] % 8) return TMAC_ERR_ALIGN;
+      if (st[i] < 0 || st[i] % vec) return TMAC_ERR_ALIGN;
   const void* ptrs[8] = {d_Q, d_K, d_V, d_O, d_dO, d_dQ, d_dK, d_dV};
   for (const void* p : ptrs)
     if (!aligned16(p)) return TMAC_ERR_ALIGN;
@@ -806,10 +1026,28 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
                        vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H, mp, scale, scale_log2, \
                        d_row_ptr, d_entries, d_order, wm_q);                                         \
   } while (0)
-  if (dtype == TMAC_BF16)
+  if (dtype == TMAC_F32) {
+    const auto* Qf = static_cast<const float*>(d_Q);
+    const auto* Kf = static_cast<const float*>(d_K);
+    const auto* Vf = static_cast<const float*>(d_V);
+    const auto* Of = static_cast<const float*>(d_O);
+    const auto* Gf = static_cast<const float*>(d_dO);
+    hipLaunchKernelGGL(wattn_bwd_delta_f32_kernel, dim3(dgrid), dim3(256), 0, s, Of, Gf, d_delta,
+                       os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);
+    hipLaunchKernelGGL(wattn_bwd_kv_f32_kernel, dim3(grid_kv), dim3(256), 0, s, Qf, Kf, Vf, Gf,
+                       d_lse, d_delta, static_cast<float*>(d_dK), static_cast<float*>(d_dV),
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
+                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], H, mp, scale,
+                       scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv);
+    hipLaunchKernelGGL(wattn_bwd_q_f32_kernel, dim3(grid_q), dim3(128), 0, s, Qf, Kf, Vf, Gf, d_lse,
+                       d_delta, static_cast<float*>(d_dQ), qs[0], qs[1], qs[2], ks[0], ks[1],
+                       ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H,
+                       mp, scale, scale_log2, d_row_ptr, d_entries, d_order, wm_q);
+  } else if (dtype == TMAC_BF16) {
     TMAC_WATTN_BWD(TMAC_BF16);
-  else
+  } else {
     TMAC_WATTN_BWD(TMAC_F16);
+  }
 #undef TMAC_WATTN_BWD
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);

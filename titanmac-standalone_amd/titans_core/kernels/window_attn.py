@@ -206,9 +206,6 @@ def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
     grad_out and out [B, S, H, dh] and lse [B, H, S] of window_attn_fwd."""
     _check_qkv(q, k, v)
     B, H, S, dh = (int(s) for s in q.shape)
-    if q.dtype not in (torch.bfloat16, torch.float16):
-        raise NotImplementedError(
-            f"windowed attention backward runs in bfloat16/float16 (MFMA kernels); got {q.dtype}")
     if out.shape != (B, S, H, dh) or grad_out.shape != (B, S, H, dh):
         raise ValueError("out and grad_out must be [B, S, H, dh] as window_attn_fwd returns")
     if lse.shape != (B, H, S) or lse.dtype != torch.float32:
