@@ -203,3 +203,34 @@ def test_titan_block_training_step_bf16(dev, name):
         else:
             ref = want[n]
         close(prm.grad.float().cpu().numpy(), ref, atol=3e-2, rtol=3e-2, what=n)
+
+
+@pytest.mark.parametrize("amp_dtype", [torch.float16, torch.bfloat16])
+def test_titan_block_autocast_training_step(dev, amp_dtype):
+    """fp32 TitanBlock (block-sparse attention, Block-ELL MLP) under torch.autocast, as the
+    reference's AMP training step runs it: gradients against fp64 autograd."""
+    cfg = tc.TitanMACConfig(d_model=128, n_heads=2, d_ff=512, window_size=96, n_persistent=8,
+                            block_size=64, use_block_sparse=True, mlp_block_ell=True,
+                            mlp_density=0.5)
+    b = _make_block(cfg, 11, dev, torch.float32).train()
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, 200, 128, generator=g)
+    dy = torch.randn(2, 200, 128, generator=g)
+    xd = x.to(dev).requires_grad_()
+    with torch.autocast("cuda", dtype=amp_dtype):
+        y = b(xd)
+    y.float().backward(dy.to(dev))
+    assert all(p.grad is not None and p.grad.dtype == torch.float32 for p in b.parameters())
+    want_x, want = _block_grads_fp64(b, x, dy)
+    close(xd.grad.cpu().numpy(), want_x, atol=3e-2, rtol=3e-2, what="x")
+    for n, prm in b.named_parameters():
+        if n.endswith("values"):
+            lin = b.mlp.fc1 if "fc1" in n else b.mlp.fc2
+            ci = lin.col_idx.long().cpu()
+            dW = torch.from_numpy(want[n.replace("values", "weight")]).t()
+            nb_r, nb_c = lin.in_features // 64, lin.out_features // 64
+            blocks = dW.reshape(nb_r, 64, nb_c, 64).permute(0, 2, 1, 3)
+            ref = blocks[torch.arange(nb_r)[:, None].expand(-1, ci.shape[1]), ci].numpy()
+        else:
+            ref = want[n]
+        close(prm.grad.cpu().numpy(), ref, atol=3e-2, rtol=3e-2, what=n)

@@ -268,10 +268,19 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
 
     activation: None or "gelu" (erf form, as nn.GELU()). The GELU is fused into
     the kernel's store when no gradient is required; otherwise it is applied as
-    a separate op so autograd can differentiate it.
+    a separate op so autograd can differentiate it. The kernels compute in
+    bfloat16 / float16 (fp32 accumulation); under torch.autocast the inputs are
+    cast to the autocast dtype first, as for nn.Linear.
     """
     if activation not in (None, "gelu"):
         raise ValueError(f"unsupported activation {activation!r}")
+    if values.is_cuda and torch.is_autocast_enabled("cuda"):
+        # Inside torch.autocast the product runs in the autocast dtype, as nn.Linear's
+        # matmul does (x, weight and bias cast; the result in that dtype).
+        dt = torch.get_autocast_dtype("cuda")
+        if dt in (torch.bfloat16, torch.float16):
+            x, values = x.to(dt), values.to(dt)
+            bias = bias.to(dt) if bias is not None else None
     idx = pattern.device_index(values.device)
     fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
         x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
