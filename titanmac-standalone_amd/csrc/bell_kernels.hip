@@ -84,24 +84,6 @@ __device__ __forceinline__ void dma16(const uint16_t* src, uint16_t* lds_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds_base), 16, 0, 0);
 }
 
-// Work order of the gather GEMM: groups of kGM m-tiles; within a group, chunks of
-// kCC output blocks; within a chunk, m-tile-major. The workgroups resident on one
-// XCD at a time then share kGM activation slabs, and each weight block they read
-// serves kGM m-tiles from that XCD's L2 instead of being fetched once per m-tile.
-constexpr int kGM = 4, kCC = 16;
-
-__device__ __forceinline__ void gemm_work(int logical, int n_mtiles, int n_out, int& mtile,
-                                          int& oi) {
-  const int g = logical / (kGM * n_out);
-  const int rem = logical - g * kGM * n_out;
-  const int gm = min(kGM, n_mtiles - g * kGM);
-  const int chunk = rem / (gm * kCC);
-  const int rem2 = rem - chunk * gm * kCC;
-  const int cc = min(kCC, n_out - chunk * kCC);
-  mtile = g * kGM + rem2 / cc;
-  oi = chunk * kCC + rem2 % cc;
-}
-
 template <int DT, bool FWD>
 __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
@@ -122,8 +104,8 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 
   const int logical = xcd_logical_id(per_xcd);
   if (logical >= n_mtiles * n_out) return;
-  int mtile, oi;
-  gemm_work(logical, n_mtiles, n_out, mtile, oi);
+  const int mtile = logical / n_out;
+  const int oi = logical - mtile * n_out;
   const int ob = FWD ? order[oi] : oi;
   const int e0 = FWD ? t_ptr[ob] : ob * width;
   const int e1 = FWD ? t_ptr[ob + 1] : e0 + width;
