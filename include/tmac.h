@@ -182,6 +182,16 @@ int tmac_wattn_schedule_kv(int S, int window, int n_persistent, int causal,
                            int32_t* h_col_ptr, int32_t* h_entries, int capacity,
                            int* n_entries);
 
+/* The mask as the attention kernels evaluate it on partial tiles: for each
+ * query row i, h_rows[3i..3i+2] = (np, lo, hi) such that i attends to key j
+ * iff j < np or lo <= j <= hi; for each key j, h_cols[3j..3j+2] = (np, lo, hi)
+ * such that query i attends to j iff i < np or lo <= i <= hi (the transpose,
+ * used by the backward's dK/dV kernel). Same masks and errors as
+ * tmac_wattn_tile_kinds; h_rows and h_cols hold 3*S entries each. */
+int tmac_wattn_mask_spans(int S, int window, int n_persistent, int causal,
+                          int pattern, int block_size, int32_t* h_rows,
+                          int32_t* h_cols);
+
 /* Launch order of a work list (tmac_wattn_schedule's row_ptr or
  * tmac_wattn_schedule_kv's col_ptr, n_blocks + 1 entries): h_order[0..n_blocks)
  * lists the blocks by list length, longest first (ties by block index), and

@@ -133,6 +133,31 @@ def test_work_list_kv_shape_errors(lib):
                                           ctypes.byref(n)) == -2
 
 
+SPAN_CASES = CASES + [(300, 5000, 7, False, "band", 64), (300, 10**9, 7, True, "blockwin", 48),
+                      (129, 0, 0, False, "blockwin", 1), (65, 3, 65, True, "blockwin", 8),
+                      (1, 0, 0, True, "band", 64), (200, 63, 5, False, "blockwin", 200)]
+
+
+@pytest.mark.parametrize("S,w,Np,causal,pattern,bs", SPAN_CASES)
+def test_mask_spans_bit_exact(lib, S, w, Np, causal, pattern, bs):
+    """The per-row and per-key intervals the kernels test on partial tiles reproduce
+    the oracle mask and its transpose exactly."""
+    rows = np.zeros(3 * S, dtype=np.int32)
+    cols = np.zeros(3 * S, dtype=np.int32)
+    code = 0 if pattern == "band" else 1
+    assert lib.tmac_wattn_mask_spans(S, w, Np, int(causal), code, bs, rows.ctypes.data,
+                                     cols.ctypes.data) == 0
+    m = om.make_mask(S, w, Np, causal, pattern, bs)
+    idx = np.arange(S)
+
+    def expand(sp):
+        np_, lo, hi = sp.reshape(S, 3).T
+        return (idx[None, :] < np_[:, None]) | ((idx[None, :] >= lo[:, None]) & (idx[None, :] <= hi[:, None]))
+
+    assert np.array_equal(expand(rows), m)
+    assert np.array_equal(expand(cols), m.T)
+
+
 def test_tile_map_golden():
     assert np.array_equal(tile_kinds(4096, 512, 16), np.load(GOLDEN / "wattn_tiles_cfg3.npy"))
     g = np.load(GOLDEN / "wattn_worklist_cfg3.npz")

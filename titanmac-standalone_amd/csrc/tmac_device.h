@@ -118,6 +118,88 @@ __device__ __forceinline__ int xcd_logical_id(int per_xcd) {
   return (b & 7) * per_xcd + (b >> 3);
 }
 
+// Mask of the windowed attention. window is clamped to S by the host (any
+// window >= S gives the same mask), so index arithmetic stays in int range.
+struct MaskParams {
+  int S, window, Np, causal, pattern, bs;
+};
+
+// A set of indices x in [0, S): x < np, or lo <= x <= hi.
+struct Span {
+  int np, lo, hi;
+};
+
+__host__ __device__ inline bool span_has(const Span& s, int x) {
+  return (x < s.np) | ((x >= s.lo) & (x <= s.hi));
+}
+
+// Keys that query row i attends to.
+// Band (attn/windowed_attention.py:97-152): persistent rows (i < Np) see the
+// persistent keys only; sequence rows see the persistent keys and the
+// sequence keys j with i - w <= j <= i (causal) or |i - j| <= w.
+// Block window (attn/block_sparse_attention.py:277-334), r = i - Np,
+// b0 = bs * floor(r / bs): persistent rows see every key; sequence rows see
+// the persistent keys and sequence keys c = j - Np in [max(0, b0 - w), r]
+// (causal) or [max(0, b0 - w), min(b0 + bs, S - Np) - 1].
+// Rows i >= S (tile padding) see nothing.
+__host__ __device__ inline Span mask_row_span(const MaskParams& p, int i) {
+  Span s{0, 1, 0};
+  if (i >= p.S) return s;
+  s.np = p.Np;
+  if (i < p.Np) {
+    if (p.pattern == TMAC_PATTERN_BLOCKWIN) {
+      s.lo = 0;
+      s.hi = p.S - 1;
+    }
+    return s;
+  }
+  if (p.pattern == TMAC_PATTERN_BAND) {
+    s.lo = i - p.window > p.Np ? i - p.window : p.Np;
+    s.hi = p.causal ? i : (i + p.window < p.S - 1 ? i + p.window : p.S - 1);
+  } else {
+    const int r = i - p.Np, b0 = (r / p.bs) * p.bs;
+    s.lo = p.Np + (b0 - p.window > 0 ? b0 - p.window : 0);
+    const int end = b0 + p.bs < p.S - p.Np ? b0 + p.bs : p.S - p.Np;
+    s.hi = p.Np + (p.causal ? r : end - 1);
+  }
+  return s;
+}
+
+// Query rows that attend to key j: the transpose of mask_row_span.
+// Band: a persistent key is seen by every row; a sequence key j by the sequence
+// rows i with j <= i <= j + w (causal) or |i - j| <= w.
+// Block window: every key is seen by the persistent rows; a persistent key by
+// every row; a sequence key c = j - Np by the sequence rows r = i - Np with
+// c <= r (causal) or floor(c / bs) * bs <= r (not causal), and
+// floor(r / bs) <= floor((c + w) / bs).
+__host__ __device__ inline Span mask_col_span(const MaskParams& p, int j) {
+  Span s{0, 1, 0};
+  if (j >= p.S) return s;
+  if (p.pattern == TMAC_PATTERN_BAND) {
+    if (j < p.Np) {
+      s.lo = 0;
+      s.hi = p.S - 1;
+    } else {
+      const int a = p.causal ? j : j - p.window;
+      s.lo = a > p.Np ? a : p.Np;
+      s.hi = j + p.window < p.S - 1 ? j + p.window : p.S - 1;
+    }
+    return s;
+  }
+  s.np = p.Np;
+  if (j < p.Np) {
+    s.lo = p.Np;
+    s.hi = p.S - 1;
+    return s;
+  }
+  const int c = j - p.Np;
+  const int r_lo = p.causal ? c : (c / p.bs) * p.bs;
+  const int r_hi = ((c + p.window) / p.bs + 1) * p.bs - 1;
+  s.lo = p.Np + r_lo;
+  s.hi = p.Np + r_hi < p.S - 1 ? p.Np + r_hi : p.S - 1;
+  return s;
+}
+
 // Launch map of a per-(b, h) block work list whose lists differ in length.
 // order[0..n_blk) names the blocks heaviest (longest list) first. Workgroup ids
 // [0, n_bh * n_lead) take the n_lead heaviest blocks of every (b, h), so they

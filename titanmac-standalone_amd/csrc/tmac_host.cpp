@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "../../include/tmac.h"
+#include "tmac_device.h"
 
 extern "C" int tmac_abi_version(void) { return TMAC_ABI_VERSION; }
 
@@ -320,5 +321,24 @@ extern "C" int tmac_wattn_launch_order(const int32_t* h_ptr, int n_blocks, int32
   int lead = 0;
   while (lead < n_blocks && len[h_order[lead]] * n_blocks >= 2 * total && total > 0) ++lead;
   *n_lead = lead;
+  return TMAC_OK;
+}
+
+extern "C" int tmac_wattn_mask_spans(int S, int window, int n_persistent, int causal, int pattern,
+                                     int block_size, int32_t* h_rows, int32_t* h_cols) {
+  if (!h_rows || !h_cols) return TMAC_ERR_NULL;
+  int st = check_mask_args(S, window, n_persistent, pattern, block_size);
+  if (st != TMAC_OK) return st;
+  const tmac::MaskParams mp{S, std::min(window, S), n_persistent, causal ? 1 : 0, pattern,
+                            block_size};
+  for (int i = 0; i < S; ++i) {
+    const tmac::Span r = tmac::mask_row_span(mp, i), c = tmac::mask_col_span(mp, i);
+    h_rows[3 * i] = r.np;
+    h_rows[3 * i + 1] = r.lo;
+    h_rows[3 * i + 2] = r.hi;
+    h_cols[3 * i] = c.np;
+    h_cols[3 * i + 1] = c.lo;
+    h_cols[3 * i + 2] = c.hi;
+  }
   return TMAC_OK;
 }

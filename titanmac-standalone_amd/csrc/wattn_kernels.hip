@@ -36,26 +36,6 @@ using namespace tmac;
 
 namespace {
 
-struct MaskParams {
-  int S, window, Np, causal, pattern, bs;
-};
-
-// The effective mask, element by element (see tmac_wattn_tile_kinds for the
-// reference citations of each clause).
-__device__ __forceinline__ bool allowed(const MaskParams& p, int i, int j) {
-  if (i >= p.S || j >= p.S) return false;
-  if (i < p.Np) return p.pattern == TMAC_PATTERN_BLOCKWIN || j < p.Np;
-  if (j < p.Np) return true;
-  if (p.pattern == TMAC_PATTERN_BAND) {
-    if (j < i - p.window) return false;
-    return p.causal ? j <= i : j <= i + p.window;
-  }
-  const int r = i - p.Np, c = j - p.Np;
-  const int b0 = (r / p.bs) * p.bs;
-  if (c < b0 - p.window) return false;
-  return p.causal ? c <= r : c < min(b0 + p.bs, p.S - p.Np);
-}
-
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -80,6 +60,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int q_row = qb * 128 + wave * 32 + l32;  // this lane's query row
+  const Span span = mask_row_span(mp, q_row);    // its allowed keys (partial tiles only)
 
   const uint16_t* Kbh = K + b * ksb + hd * ksh;
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
@@ -144,30 +125,32 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
           const u32x4 a = lds16(kt_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
           st[kh] = Mfma<DT>::run(a, qf[kk], st[kh]);
         }
-      // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4.
+      // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
+      // scores; the running max m_run is kept unscaled too, scale_log2 > 0).
+      if (kind == 2) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+            st[kh][j] = span_has(span, key) ? st[kh][j] : -INFINITY;
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          float x = st[kh][j] * scale_log2;
-          if (kind == 2) {
-            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-            if (!allowed(mp, q_row, key)) x = -INFINITY;
-          }
-          st[kh][j] = x;
-          mx = fmaxf(mx, x);
-        }
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kh][j]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;  // row fully masked so far
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new * scale_log2;  // row fully masked so far
+      const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
       float rs = 0.f;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          const float pj = __builtin_amdgcn_exp2f(st[kh][j] - m_use);
+          const float pj = __builtin_amdgcn_exp2f(fmaf(st[kh][j], scale_log2, -m_use));
           st[kh][j] = pj;
           rs += pj;
         }
@@ -222,7 +205,8 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
       *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * jg + 4 * h) = packed;
     }
   if (lse && h == 0)
-    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + __log2f(l_run)) * kLn2;
+    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] =
+        (m_run * scale_log2 + __log2f(l_run)) * kLn2;
 }
 
 // fp32 path: one query row per thread, 128 rows per workgroup (2 waves).
@@ -243,6 +227,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   const int tid = threadIdx.x;
   const int q_row = qb * 128 + tid;
   const int sub = tid >> 5;  // 32-row slice of this thread
+  const Span span = mask_row_span(mp, q_row);
 
   float q[64], o[64];
   {
@@ -286,7 +271,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
       float acc = 0.f;
 #pragma unroll
       for (int d = 0; d < 64; ++d) acc = fmaf(q[d], kt_lds[j * 64 + d], acc);
-      if (kind == 2 && !allowed(mp, q_row, kt * 64 + j)) acc = -INFINITY;
+      if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
       s[j] = acc;
       mx = fmaxf(mx, acc);
     }
@@ -418,6 +403,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int key = kb * 128 + wave * 32 + l32;  // this lane's key
+  const Span span = mask_col_span(mp, key);     // the queries that see it (partial tiles only)
 
   u32x4 kf[4], vf[4];
   {
@@ -495,12 +481,17 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
           dp = Mfma<DT>::run(ga, vf[kk], dp);
         }
         // s[j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4.
+        if (kind == 2) {
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int ql = 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
+            s[j] = span_has(span, qt * 64 + ql) ? s[j] : -INFINITY;
+          }
+        }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
           const int ql = 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
-          const float l2 = stat[buf][0][ql];
-          float pj = (l2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s[j] * scale_log2 - l2);
-          if (kind == 2 && !allowed(mp, qt * 64 + ql, key)) pj = 0.f;
+          const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], scale_log2, -stat[buf][0][ql]));
           s[j] = pj;
           dp[j] = pj * (dp[j] - stat[buf][1][ql]);
         }
@@ -557,6 +548,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int q_row = qb * 128 + wave * 32 + l32;
+  const Span span = mask_row_span(mp, q_row);
 
   u32x4 qf[4], gf[4];
   {
@@ -627,15 +619,20 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
         }
       }
       // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4.
+      if (kind == 2) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+            s[kh][j] = span_has(span, key) ? s[kh][j] : -INFINITY;
+          }
+      }
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-          float pj = (l2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(s[kh][j] * scale_log2 - l2);
-          if (kind == 2) {
-            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-            if (!allowed(mp, q_row, key)) pj = 0.f;
-          }
+          const float pj = __builtin_amdgcn_exp2f(fmaf(s[kh][j], scale_log2, -l2));
           dp[kh][j] = pj * (dp[kh][j] - dl);
         }
       // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
@@ -708,6 +705,7 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
   const int q_row = qb * 128 + tid;
   const int qc = min(q_row, S - 1);
   const int sub = tid >> 5;
+  const Span span = mask_row_span(mp, q_row);
 
   float q[64], g[64], dq[64];
   {
@@ -758,7 +756,7 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
         dp = fmaf(g[d], vt_lds[j * 64 + d], dp);
       }
       float pj = __builtin_amdgcn_exp2f(sj - l2);
-      if (kind == 2 && !allowed(mp, q_row, kt * 64 + j)) pj = 0.f;
+      if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
       const float ds = pj * (dp - dl);
 #pragma unroll
       for (int d = 0; d < 64; ++d) dq[d] = fmaf(ds, kt_lds[j * 64 + d], dq[d]);
@@ -797,6 +795,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
   const int half = lane >> 5;
   const int key = kb * 128 + wave * 32 + (lane & 31);
   const int kc = min(key, S - 1);
+  const Span span = mask_col_span(mp, key);
 
   float k[32], v[32], dk[32], dv[32];
   {
@@ -858,7 +857,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
       sp += __shfl_xor(sp, 32);
       dpp += __shfl_xor(dpp, 32);
       float pi = __builtin_amdgcn_exp2f(sp * scale_log2 - l2_lds[i]);
-      if (kind == 2 && !allowed(mp, qt * 64 + i, key)) pi = 0.f;
+      if (kind == 2 && !span_has(span, qt * 64 + i)) pi = 0.f;
       const float ds = pi * (dpp - dl_lds[i]);
 #pragma unroll
       for (int d = 0; d < 32; ++d) {
@@ -926,7 +925,7 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
   if (n_lead < 0 || n_lead > n_qb) return TMAC_ERR_VALUE;
   unsigned grid = 0;
   const WorkMap wm = make_work_map(B * H, n_qb, n_lead, &grid);
-  const MaskParams mp{S, window, n_persistent, causal ? 1 : 0, pattern, block_size};
+  const MaskParams mp{S, min(window, S), n_persistent, causal ? 1 : 0, pattern, block_size};
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t* qs = q_strides;
@@ -998,7 +997,7 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
   unsigned grid_q = 0, grid_kv = 0;
   const WorkMap wm_q = make_work_map(B * H, n_qb, n_lead, &grid_q);
   const WorkMap wm_kv = make_work_map(B * H, n_qb, n_lead_kv, &grid_kv);
-  const MaskParams mp{S, window, n_persistent, causal ? 1 : 0, pattern, block_size};
+  const MaskParams mp{S, min(window, S), n_persistent, causal ? 1 : 0, pattern, block_size};
   const float scale_log2 = scale * kLog2e;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* Q = static_cast<const uint16_t*>(d_Q);

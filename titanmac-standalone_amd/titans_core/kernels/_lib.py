@@ -44,6 +44,7 @@ SIGNATURES = {
     "tmac_wattn_tile_kinds": [_i, _i, _i, _i, _i, _i, _i, _i, _vp],
     "tmac_wattn_schedule": [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _i, ctypes.POINTER(_i)],
     "tmac_wattn_launch_order": [_vp, _i, _vp, ctypes.POINTER(_i)],
+    "tmac_wattn_mask_spans": [_i, _i, _i, _i, _i, _i, _vp, _vp],
     "tmac_wattn_fwd": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
                        _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
                        _i, _vp],
