@@ -276,10 +276,8 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
           for (int t = 0; t < 4; ++t) v[t] = gelu_erf(v[t]);
         }
         u32x2 packed;
-        packed.x = static_cast<uint32_t>(Mfma<DT>::from_f32(v[0])) |
-                   (static_cast<uint32_t>(Mfma<DT>::from_f32(v[1])) << 16);
-        packed.y = static_cast<uint32_t>(Mfma<DT>::from_f32(v[2])) |
-                   (static_cast<uint32_t>(Mfma<DT>::from_f32(v[3])) << 16);
+        packed.x = Mfma<DT>::pack2(v[0], v[1]);
+        packed.y = Mfma<DT>::pack2(v[2], v[3]);
         *reinterpret_cast<u32x2*>(stage + (32 * mi + l32) * kPitch + n_loc) = packed;
       }
   __syncthreads();
@@ -414,10 +412,8 @@ __global__ __launch_bounds__(256) void bell_sddmm_reduce_kernel(const float* __r
     *reinterpret_cast<f32x4*>(static_cast<float*>(out) + i4) = s;
   } else {
     u32x2 packed;
-    packed.x = static_cast<uint32_t>(Mfma<OUT>::from_f32(s.x)) |
-               (static_cast<uint32_t>(Mfma<OUT>::from_f32(s.y)) << 16);
-    packed.y = static_cast<uint32_t>(Mfma<OUT>::from_f32(s.z)) |
-               (static_cast<uint32_t>(Mfma<OUT>::from_f32(s.w)) << 16);
+    packed.x = Mfma<OUT>::pack2(s.x, s.y);
+    packed.y = Mfma<OUT>::pack2(s.z, s.w);
     *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(out) + i4) = packed;
   }
 }

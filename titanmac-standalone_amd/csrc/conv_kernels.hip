@@ -59,8 +59,7 @@ struct Vec16 {
     uint32_t w[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      w[i] = static_cast<uint32_t>(Mfma<DT16>::from_f32(v[2 * i])) |
-             (static_cast<uint32_t>(Mfma<DT16>::from_f32(v[2 * i + 1])) << 16);
+      w[i] = Mfma<DT16>::pack2(v[2 * i], v[2 * i + 1]);
     *reinterpret_cast<u32x4*>(p) = u32x4{w[0], w[1], w[2], w[3]};
   }
 };

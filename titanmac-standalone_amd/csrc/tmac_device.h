@@ -52,6 +52,12 @@ struct Mfma<TMAC_BF16> {
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return __uint_as_float(static_cast<uint32_t>(x) << 16);
   }
+  // lo | hi << 16, both rounded to nearest even: one v_cvt_pk_bf16_f32.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+  }
 };
 
 template <>
@@ -65,6 +71,12 @@ struct Mfma<TMAC_F16> {
   }
   static __device__ __forceinline__ float to_f32(uint16_t x) {
     return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  // lo | hi << 16, both rounded to nearest even.
+  static __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
   }
 };
 

@@ -169,8 +169,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
         uint32_t w[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
-          w[t] = static_cast<uint32_t>(Mfma<DT>::from_f32(st[kh][j0 + 2 * t])) |
-                 (static_cast<uint32_t>(Mfma<DT>::from_f32(st[kh][j0 + 2 * t + 1])) << 16);
+          w[t] = Mfma<DT>::pack2(st[kh][j0 + 2 * t], st[kh][j0 + 2 * t + 1]);
         pb[ks] = u32x4{w[0], w[1], w[2], w[3]};
       }
       // Vᵀ as the A operand in the same key order: rows 16ks + 4h + 0..3, then
@@ -198,10 +197,8 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       u32x2 packed;
-      packed.x = static_cast<uint32_t>(Mfma<DT>::from_f32(ot[dt][4 * jg] * inv_l)) |
-                 (static_cast<uint32_t>(Mfma<DT>::from_f32(ot[dt][4 * jg + 1] * inv_l)) << 16);
-      packed.y = static_cast<uint32_t>(Mfma<DT>::from_f32(ot[dt][4 * jg + 2] * inv_l)) |
-                 (static_cast<uint32_t>(Mfma<DT>::from_f32(ot[dt][4 * jg + 3] * inv_l)) << 16);
+      packed.x = Mfma<DT>::pack2(ot[dt][4 * jg] * inv_l, ot[dt][4 * jg + 1] * inv_l);
+      packed.y = Mfma<DT>::pack2(ot[dt][4 * jg + 2] * inv_l, ot[dt][4 * jg + 3] * inv_l);
       *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * jg + 4 * h) = packed;
     }
   if (lse && h == 0)
@@ -348,8 +345,7 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& v, int j0) {
   uint32_t w[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
-    w[t] = static_cast<uint32_t>(Mfma<DT>::from_f32(v[j0 + 2 * t])) |
-           (static_cast<uint32_t>(Mfma<DT>::from_f32(v[j0 + 2 * t + 1])) << 16);
+    w[t] = Mfma<DT>::pack2(v[j0 + 2 * t], v[j0 + 2 * t + 1]);
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
@@ -364,10 +360,8 @@ __device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 (&acc)[
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       u32x2 packed;
-      packed.x = static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg] * mul)) |
-                 (static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 1] * mul)) << 16);
-      packed.y = static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 2] * mul)) |
-                 (static_cast<uint32_t>(Mfma<DT>::from_f32(acc[dt][4 * jg + 3] * mul)) << 16);
+      packed.x = Mfma<DT>::pack2(acc[dt][4 * jg] * mul, acc[dt][4 * jg + 1] * mul);
+      packed.y = Mfma<DT>::pack2(acc[dt][4 * jg + 2] * mul, acc[dt][4 * jg + 3] * mul);
       *reinterpret_cast<u32x2*>(rowp + 32 * dt + 8 * jg + 4 * h) = packed;
     }
 }
