@@ -75,18 +75,31 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
 
   const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
 
-  // K/V tile staging: 2 x 512 chunks of 16 bytes, 4 per thread.
+  // K/V tile staging: 2 x 512 chunks of 16 bytes, 4 per thread (rows tid/8 and
+  // tid/8 + 32 of the K and V tiles). Offsets within a tile are fixed per thread;
+  // only the last tile of a sequence whose length is not a multiple of 64 needs
+  // its rows clamped.
   u32x4 pre[4];
-  auto gload = [&](int kt) {
+  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
+  const int64_t koff0 = r0 * kss + c8, koff1 = (r0 + 32) * kss + c8;
+  const int64_t voff0 = r0 * vss + c8, voff1 = (r0 + 32) * vss + c8;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    if (kt * 64 + 64 <= S) {
+      const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
+      const uint16_t* vb = Vbh + static_cast<int64_t>(kt) * 64 * vss;
+      pre[0] = ldg16(kb + koff0);
+      pre[1] = ldg16(kb + koff1);
+      pre[2] = ldg16(vb + voff0);
+      pre[3] = ldg16(vb + voff1);
+    } else {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      const int key = min(kt * 64 + row, S - 1);  // rows past S: valid memory, always masked
-      const uint16_t* src = (p < 2 ? Kbh + key * kss : Vbh + key * vss) + (tid & 7) * 8;
-      pre[p] = ldg16(src);
+      for (int p = 0; p < 4; ++p) {
+        const int key = min(kt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
+        pre[p] = ldg16((p < 2 ? Kbh + key * kss : Vbh + key * vss) + c8);
+      }
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int row = (tid >> 3) + 32 * (p & 1);
@@ -97,7 +110,13 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
   f32x16 ot[2];
   ot[0] = f32x16{};
   ot[1] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  // Online softmax with a lazily moved reference: P = exp2(S·c − m_ref) with c =
+  // scale·log2e, and m_ref (scaled units) moves, rescaling O and the row sum, only
+  // when a tile's row maximum exceeds it by more than kTau. P then stays <= 2^kTau,
+  // which neither the 16-bit P operand (relative rounding) nor the fp32 sums mind,
+  // and the 32 accumulator multiplies run only on the rare tiles that move it.
+  constexpr float kTau = 8.f;
+  float m_ref = -INFINITY, l_run = 0.f;
 
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
@@ -126,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
           st[kh] = Mfma<DT>::run(a, qf[kk], st[kh]);
         }
       // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
-      // scores; the running max m_run is kept unscaled too, scale_log2 > 0).
+      // scores; scale_log2 > 0, so the row maximum commutes with the scaling).
       if (kind == 2) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
@@ -141,10 +160,18 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kh][j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new * scale_log2;  // row fully masked so far
-      const float alpha = __builtin_amdgcn_exp2f(m_run * scale_log2 - m_use);
+      mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+      const bool move = mx > m_ref + kTau;  // false while the row is fully masked
+      if (__builtin_amdgcn_ballot_w64(move)) {
+        // lanes that keep their reference scale by 1 (also when it is still -inf)
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mx) : 1.f;  // 0 from -inf
+        const float m_new = move ? mx : m_ref;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < 2; ++dt) ot[dt] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
       float rs = 0.f;
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
@@ -155,10 +182,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
           rs += pj;
         }
       rs += __shfl_xor(rs, 32);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) ot[dt] *= alpha;
+      l_run += rs;
 
       // Pᵀ as the B operand, 16 keys per MFMA: k-step ks covers keys
       // 16ks..16ks+15 and lane t-th value is key 16ks + 8(t/4) + 4h + t%4.
@@ -202,8 +226,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
       *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * jg + 4 * h) = packed;
     }
   if (lse && h == 0)
-    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] =
-        (m_run * scale_log2 + __log2f(l_run)) * kLn2;
+    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
 }
 
 // fp32 path: one query row per thread, 128 rows per workgroup (2 waves).
