@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
     const int32_t* __restrict__ order, WorkMap wm) {
   // [buffer][Q, dO] 64x64 tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
-  __shared__ float stat[2][2][64];
+  __shared__ __attribute__((aligned(16))) float stat[2][2][64];
 
   int bh, kb;
   if (!work_item(wm, order, bh, kb)) return;
@@ -442,20 +442,30 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
 
   u32x4 pre[4];
   float st_pre = 0.f;
-  auto gload = [&](int qt) {
+  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
+  const int64_t qoff0 = r0 * qss + c8, qoff1 = (r0 + 32) * qss + c8;
+  const int64_t goff0 = r0 * gss + c8, goff1 = (r0 + 32) * gss + c8;
+  auto gload = [&](int qt) __attribute__((always_inline)) {
+    if (qt * 64 + 64 <= S) {
+      const uint16_t* qb = Qbh + static_cast<int64_t>(qt) * 64 * qss;
+      const uint16_t* gb = Gbh + static_cast<int64_t>(qt) * 64 * gss;
+      pre[0] = ldg16(qb + qoff0);
+      pre[1] = ldg16(qb + qoff1);
+      pre[2] = ldg16(gb + goff0);
+      pre[3] = ldg16(gb + goff1);
+    } else {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      const int qr = min(qt * 64 + row, S - 1);  // rows past S: valid memory, always masked
-      const uint16_t* src = (p < 2 ? Qbh + qr * qss : Gbh + qr * gss) + (tid & 7) * 8;
-      pre[p] = ldg16(src);
+      for (int p = 0; p < 4; ++p) {
+        const int qr = min(qt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
+        pre[p] = ldg16((p < 2 ? Qbh + qr * qss : Gbh + qr * gss) + c8);
+      }
     }
     if (tid < 128) {
       const int qr = min(qt * 64 + (tid & 63), S - 1);
       st_pre = tid < 64 ? lse_bh[qr] * kLog2e : dl_bh[qr];
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int row = (tid >> 3) + 32 * (p & 1);
@@ -505,12 +515,19 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
             s[j] = span_has(span, qt * 64 + ql) ? s[j] : -INFINITY;
           }
         }
+        // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e and Δ as one 16-byte read each
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int ql = 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
-          const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], scale_log2, -stat[buf][0][ql]));
-          s[j] = pj;
-          dp[j] = pj * (dp[j] - stat[buf][1][ql]);
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat[buf][0][32 * qh + 8 * g + 4 * h]);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][32 * qh + 8 * g + 4 * h]);
+          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int j = 4 * g + t;
+            const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], scale_log2, -lv[t]));
+            s[j] = pj;
+            dp[j] = pj * (dp[j] - dv4[t]);
+          }
         }
         // dVᵀ[d][key] += Σ_q dO[q][d] P[q][key]; dKᵀ[d][key] += Σ_q Q[q][d] dS[q][key].
 #pragma unroll
@@ -585,16 +602,26 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
 
   u32x4 pre[4];
-  auto gload = [&](int kt) {
+  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
+  const int64_t koff0 = r0 * kss + c8, koff1 = (r0 + 32) * kss + c8;
+  const int64_t voff0 = r0 * vss + c8, voff1 = (r0 + 32) * vss + c8;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    if (kt * 64 + 64 <= S) {
+      const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
+      const uint16_t* vb = Vbh + static_cast<int64_t>(kt) * 64 * vss;
+      pre[0] = ldg16(kb + koff0);
+      pre[1] = ldg16(kb + koff1);
+      pre[2] = ldg16(vb + voff0);
+      pre[3] = ldg16(vb + voff1);
+    } else {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      const int kr = min(kt * 64 + row, S - 1);
-      const uint16_t* src = (p < 2 ? Kbh + kr * kss : Vbh + kr * vss) + (tid & 7) * 8;
-      pre[p] = ldg16(src);
+      for (int p = 0; p < 4; ++p) {
+        const int kr = min(kt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
+        pre[p] = ldg16((p < 2 ? Kbh + kr * kss : Vbh + kr * vss) + c8);
+      }
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int row = (tid >> 3) + 32 * (p & 1);
