@@ -10,7 +10,9 @@ The same run also times, as secondary figures:
   - windowed attention forward of config 3 (B=8, H=10, S=4096, dh=64, w=512,
     Np=16, bf16) in tokens/s, against the dense masked SDPA and the dense
     bmm -> softmax -> bmm path on the same GPU (the faster one is the
-    denominator of `attn_speedup_vs_dense`);
+    denominator of `attn_speedup_vs_dense`); also at the model-shaped S=4112
+    (4096 tokens + 16 persistent) and with BlockSparseAttention's block-window
+    mask (block 64);
   - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
     masked bf16 backward (five bmm over the full S x S);
   - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40);
@@ -118,22 +120,27 @@ def setup_spmm(dev):
                 keep=(X, V, Y, idx))
 
 
-def setup_attn(dev):
-    c = CFG3
+def setup_attn(dev, S=None, pattern=None, block_size=64):
+    """Windowed attention forward at config 3's shape (S overridable; the pattern
+    defaults to the band of WindowedAttention)."""
+    c = dict(CFG3)
+    if S is not None:
+        c["S"] = S
+    pattern = _lib.PATTERN_BAND if pattern is None else pattern
     shape = (c["B"], c["S"], 3, c["H"], c["dh"])  # fused qkv projection output layout
     qkv = gen(shape, c["seed"]).to(dev)
     q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))  # [B, H, S, dh] views
     out = torch.empty(c["B"], c["S"], c["H"], c["dh"], dtype=torch.bfloat16, device=dev)
     o_view = out.permute(0, 2, 1, 3)
     row_ptr, entries, order, n_lead = _device_work_list(c["S"], c["window"], c["n_persistent"],
-                                                        True, _lib.PATTERN_BAND, 64, dev)
+                                                        True, pattern, block_size, dev)
     import ctypes
     st = lambda t: (ctypes.c_int64 * 3)(t.stride(0), t.stride(1), t.stride(2))  # noqa: E731
     L = _lib.lib()
     stream = _lib.stream_ptr(dev)
     args = (_lib.ptr(q), st(q), _lib.ptr(k), st(k), _lib.ptr(v), st(v), _lib.ptr(out), st(o_view),
             None, c["B"], c["H"], c["S"], c["dh"], c["window"], c["n_persistent"], 1,
-            _lib.PATTERN_BAND, 64, float(1.0 / np.sqrt(c["dh"])), _lib.ptr(row_ptr),
+            pattern, block_size, float(1.0 / np.sqrt(c["dh"])), _lib.ptr(row_ptr),
             _lib.ptr(entries), _lib.ptr(order), n_lead, _lib.BF16, stream)
 
     def launch():
@@ -141,7 +148,15 @@ def setup_attn(dev):
         if rc:
             _lib.check(rc, "tmac_wattn_fwd")
 
-    pairs = band_pairs(c["S"], c["window"], c["n_persistent"])
+    if pattern == _lib.PATTERN_BAND:
+        pairs = band_pairs(c["S"], c["window"], c["n_persistent"])
+    else:  # allowed pairs from the host's per-row intervals
+        rows = np.zeros(3 * c["S"], dtype=np.int32)
+        cols = np.zeros(3 * c["S"], dtype=np.int32)
+        _lib.check(L.tmac_wattn_mask_spans(c["S"], c["window"], c["n_persistent"], 1, pattern,
+                                           block_size, rows.ctypes.data, cols.ctypes.data), "spans")
+        np_, lo, hi = rows.reshape(-1, 3).T.astype(np.int64)
+        pairs = int(np.sum(np_ + np.maximum(0, hi - np.maximum(lo, np_) + 1)))
     bh = c["B"] * c["H"]
     flops = 4 * c["dh"] * pairs * bh
     bytes_ = 4 * bh * c["S"] * c["dh"] * 2
@@ -446,6 +461,13 @@ def main() -> int:
                            tflops=att["flops"] / ms / 1e9, gbs=att["bytes"] / ms / 1e6)
         if args.mode == "all":
             out["attn"].update(dense_attention_baseline(att, K, W, stream))
+            for key, kw in (("s4112", dict(S=4112)),
+                            ("blockwin", dict(pattern=_lib.PATTERN_BLOCKWIN))):
+                extra = setup_attn(dev, **kw)
+                ms_x = timed(extra["launch"], K, W, stream)
+                out["attn"][key] = dict(ms=ms_x, tokens_per_s=extra["tokens"] / ms_x * 1e3,
+                                        tflops=extra["flops"] / ms_x / 1e9)
+                del extra
     if args.mode in ("all", "attn_bwd"):
         bwd = setup_attn_bwd(dev, att)
         ms = timed(bwd["launch"], K, W, stream)
@@ -506,6 +528,10 @@ def main() -> int:
             "dense_masked_sdpa_ms": round(a["sdpa_masked_ms"], 4),
             "dense_bmm_softmax_bmm_ms": round(a["bmm_softmax_bmm_ms"], 4),
             "attn_speedup_vs_dense": round(dense_ms / a["ms"], 2),
+            "windowed_attn_fwd_s4112_ms": round(a["s4112"]["ms"], 5),
+            "windowed_attn_fwd_s4112_tokens_per_s": round(a["s4112"]["tokens_per_s"], 1),
+            "blocksparse_attn_fwd_blockwin_ms": round(a["blockwin"]["ms"], 5),
+            "blocksparse_attn_fwd_blockwin_tflops_algorithmic": round(a["blockwin"]["tflops"], 3),
             "windowed_attn_bwd_ms": round(out["attn_bwd"]["ms"], 5),
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
