@@ -212,7 +212,8 @@ int tmac_wattn_launch_order(const int32_t* h_ptr, int n_blocks, int32_t* h_order
  * conversion (:311-315).
  * Q, K, V, O: [B, H, S, dh] addressed by strides (batch, head, seq) in
  * elements, last dimension contiguous, so the chunked views of the fused qkv
- * projection (:295-304) are taken without a copy. dh must be 64.
+ * projection (:295-304) are taken without a copy. dh: 32, 64 or 128
+ * (d_model / n_heads of the reference's configs).
  * lse (nullable): fp32 [B, H, S], natural-log log-sum-exp of each row.
  * row_ptr/entries: device copies of tmac_wattn_schedule's output built with
  * q_block = 128, sub_rows = 32; order/n_lead: device copy of
@@ -244,7 +245,7 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
  * col_ptr/entries_kv: tmac_wattn_schedule_kv with k_block = 128,
  * sub_cols = 32, order_kv/n_lead_kv: tmac_wattn_launch_order of col_ptr
  * (device copies). dtype: TMAC_BF16 / TMAC_F16 (MFMA kernels) or TMAC_F32
- * (FMA kernels, for fp32 modules); dh = 64. */
+ * (FMA kernels, for fp32 modules); dh: 32, 64 or 128. */
 int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
                    const void* d_V, const int64_t v_strides[3],

@@ -86,8 +86,8 @@ def test_value_errors(dev):
     with pytest.raises(ValueError):
         windowed_attention(q, q, q, -1, 0)
     with pytest.raises(ValueError):
-        windowed_attention(torch.zeros(1, 1, 16, 32, device=dev, dtype=torch.bfloat16),
-                           *[torch.zeros(1, 1, 16, 32, device=dev, dtype=torch.bfloat16)] * 2, 4, 0)
+        windowed_attention(torch.zeros(1, 1, 16, 48, device=dev, dtype=torch.bfloat16),
+                           *[torch.zeros(1, 1, 16, 48, device=dev, dtype=torch.bfloat16)] * 2, 4, 0)
 
 
 def test_config1_module_fp32(dev):

@@ -221,8 +221,9 @@ def test_wattn_fwd_argument_errors(lib):
     st = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1920)
     base = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, None, 8, 10, 4096, 64, 512, 16, 1, 0, 64, 0.125,
             FAKE, FAKE, FAKE, 0, 1, None]
-    a = list(base); a[12] = 32
-    assert lib.tmac_wattn_fwd(*a) == -2           # head_dim must be 64
+    for dh in (0, 16, 48, 96, 256):
+        a = list(base); a[12] = dh
+        assert lib.tmac_wattn_fwd(*a) == -2       # head_dim must be 32, 64 or 128
     a = list(base); a[14] = 4096
     assert lib.tmac_wattn_fwd(*a) == -8           # n_persistent >= S
     a = list(base); a[13] = -1
@@ -244,8 +245,9 @@ def test_wattn_bwd_argument_errors(lib):
     base = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, FAKE, FAKE, st, FAKE, st,
             FAKE, st, 8, 10, 4096, 64, 512, 16, 1, 0, 64, 0.125, FAKE, FAKE, FAKE, 1,
             FAKE, FAKE, FAKE, 1, 1, None]
-    a = list(base); a[21] = 128
-    assert lib.tmac_wattn_bwd(*a) == -2           # head_dim must be 64
+    for dh in (0, 16, 48, 96, 256):
+        a = list(base); a[21] = dh
+        assert lib.tmac_wattn_bwd(*a) == -2       # head_dim must be 32, 64 or 128
     a = list(base); a[36] = 9
     assert lib.tmac_wattn_bwd(*a) == -4           # unknown dtype
     a = list(base); a[36] = 0; a[1] = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1922)

@@ -95,12 +95,13 @@ __device__ __forceinline__ u32x4 lds_read_tr8(const uint16_t* tile, int r0, int 
 }
 
 // Same as lds_read_tr8 but the two 4-row groups are independent
-// (rows r0..r0+3 and r1..r1+3).
+// (rows r0..r0+3 and r1..r1+3), in a tile of row pitch P elements.
+template <int P = kPitch>
 __device__ __forceinline__ u32x4 lds_read_tr4x2(const uint16_t* tile, int r0, int r1, int c0,
                                                 int lane) {
   const int i = lane & 15;
-  const uint16_t* p0 = tile + (r0 + (i >> 2)) * kPitch + c0 + 4 * (i & 3);
-  const uint16_t* p1 = tile + (r1 + (i >> 2)) * kPitch + c0 + 4 * (i & 3);
+  const uint16_t* p0 = tile + (r0 + (i >> 2)) * P + c0 + 4 * (i & 3);
+  const uint16_t* p1 = tile + (r1 + (i >> 2)) * P + c0 + 4 * (i & 3);
   const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p0));
   const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p1));
   const u32x2 l2 = __builtin_bit_cast(u32x2, lo);

@@ -39,7 +39,23 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-template <int DT>
+// 64-row tiles of head dimension D (32, 64 or 128) in LDS: rows padded to
+// D + 8 elements, so the 16-byte row reads of 16 consecutive rows and the
+// transpose reads of 4 rows hit distinct banks. 256 threads stage one tile in
+// D / 32 passes of 16-byte chunks (D / 8 chunks per row, 2048 / D rows a pass).
+template <int D>
+struct Tile {
+  static_assert(D == 32 || D == 64 || D == 128, "head dimension 32, 64 or 128");
+  static constexpr int kP = D + 8;        // row pitch, elements
+  static constexpr int kElems = 64 * kP;  // one tile
+  static constexpr int kCpr = D / 8;      // 16-byte chunks per row
+  static constexpr int kRpp = 256 / kCpr; // rows per staging pass
+  static constexpr int kPasses = D / 32;  // staging passes per tile
+  static constexpr int kKk = D / 16;      // MFMA k-steps over the head dimension
+  static constexpr int kDt = D / 32;      // 32-wide head-dimension tiles of an output
+};
+
+template <int DT, int D>
 __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
@@ -47,8 +63,9 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  // [buffer][K, V] 64x64 tiles.
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+  using T = Tile<D>;
+  // [buffer][K, V] 64 x D tiles.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
 
   int bh, qb;
   if (!work_item(wm, order, bh, qb)) return;
@@ -66,50 +83,57 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
 
   // Q rows as the B operand of Sᵀ = K·Qᵀ: lane holds Q[row][16kk + 8h .. +8].
-  u32x4 qf[4];
+  u32x4 qf[T::kKk];
   {
     const uint16_t* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) qf[kk] = ldg16(qp + 16 * kk);
+    for (int kk = 0; kk < T::kKk; ++kk) qf[kk] = ldg16(qp + 16 * kk);
   }
 
   const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
 
-  // K/V tile staging: 2 x 512 chunks of 16 bytes, 4 per thread (rows tid/8 and
-  // tid/8 + 32 of the K and V tiles). Offsets within a tile are fixed per thread;
-  // only the last tile of a sequence whose length is not a multiple of 64 needs
-  // its rows clamped.
-  u32x4 pre[4];
-  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
-  const int64_t koff0 = r0 * kss + c8, koff1 = (r0 + 32) * kss + c8;
-  const int64_t voff0 = r0 * vss + c8, voff1 = (r0 + 32) * vss + c8;
+  // K/V tile staging: T::kPasses 16-byte chunks of each tile per thread (rows
+  // r0 + pass * T::kRpp, chunk tid % T::kCpr). Offsets within a tile are fixed per
+  // thread; only the last tile of a sequence whose length is not a multiple of 64
+  // needs its rows clamped.
+  u32x4 pre[2 * T::kPasses];
+  const int r0 = tid / T::kCpr, c8 = (tid % T::kCpr) * 8;
+  int64_t koff[T::kPasses], voff[T::kPasses];
+#pragma unroll
+  for (int p = 0; p < T::kPasses; ++p) {
+    koff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * kss + c8;
+    voff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * vss + c8;
+  }
   auto gload = [&](int kt) __attribute__((always_inline)) {
     if (kt * 64 + 64 <= S) {
       const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
       const uint16_t* vb = Vbh + static_cast<int64_t>(kt) * 64 * vss;
-      pre[0] = ldg16(kb + koff0);
-      pre[1] = ldg16(kb + koff1);
-      pre[2] = ldg16(vb + voff0);
-      pre[3] = ldg16(vb + voff1);
+#pragma unroll
+      for (int p = 0; p < T::kPasses; ++p) {
+        pre[p] = ldg16(kb + koff[p]);
+        pre[T::kPasses + p] = ldg16(vb + voff[p]);
+      }
     } else {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int key = min(kt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
-        pre[p] = ldg16((p < 2 ? Kbh + key * kss : Vbh + key * vss) + c8);
+      for (int p = 0; p < T::kPasses; ++p) {
+        const int key = min(kt * 64 + r0 + p * T::kRpp, S - 1);  // rows past S: always masked
+        pre[p] = ldg16(Kbh + key * kss + c8);
+        pre[T::kPasses + p] = ldg16(Vbh + key * vss + c8);
       }
     }
   };
   auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      sts16(smem + (2 * buf + (p >> 1)) * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
+    for (int p = 0; p < T::kPasses; ++p) {
+      const int off = (r0 + p * T::kRpp) * T::kP + c8;
+      sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
+      sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
     }
   };
 
-  f32x16 ot[2];
-  ot[0] = f32x16{};
-  ot[1] = f32x16{};
+  f32x16 ot[T::kDt];
+#pragma unroll
+  for (int dt = 0; dt < T::kDt; ++dt) ot[dt] = f32x16{};
   // Online softmax with a lazily moved reference: P = exp2(S·c − m_ref) with c =
   // scale·log2e, and m_ref (scaled units) moves, rescaling O and the row sum, only
   // when a tile's row maximum exceeds it by more than kTau. P then stays <= 2^kTau,
@@ -132,16 +156,16 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
     if (more) gload(entries[e + 1] & 0xffff);
 
     if (kind != 0) {
-      const uint16_t* kt_lds = smem + (2 * buf) * kTileElems;
-      const uint16_t* vt_lds = smem + (2 * buf + 1) * kTileElems;
+      const uint16_t* kt_lds = smem + (2 * buf) * T::kElems;
+      const uint16_t* vt_lds = smem + (2 * buf + 1) * T::kElems;
       f32x16 st[2];
       st[0] = f32x16{};
       st[1] = f32x16{};
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk)
+      for (int kk = 0; kk < T::kKk; ++kk)
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
-          const u32x4 a = lds16(kt_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
+          const u32x4 a = lds16(kt_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
           st[kh] = Mfma<DT>::run(a, qf[kk], st[kh]);
         }
       // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
@@ -168,7 +192,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
         const float m_new = move ? mx : m_ref;
         l_run *= alpha;
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) ot[dt] *= alpha;
+        for (int dt = 0; dt < T::kDt; ++dt) ot[dt] *= alpha;
         m_ref = m_new;
       }
       const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
@@ -201,9 +225,9 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const u32x4 va = lds_read_tr4x2(vt_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
-                                          32 * dt + 16 * grp, lane);
+        for (int dt = 0; dt < T::kDt; ++dt) {
+          const u32x4 va = lds_read_tr4x2<T::kP>(vt_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
+                                                 32 * dt + 16 * grp, lane);
           ot[dt] = Mfma<DT>::run(va, pb[ks], ot[dt]);
         }
     }
@@ -217,7 +241,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
   uint16_t* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
   // ot[dt][j] = O[q_row][32dt + 8(j/4) + 4h + j%4]: four consecutive dh per j/4.
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < T::kDt; ++dt)
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       u32x2 packed;
@@ -230,6 +254,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
 }
 
 // fp32 path: one query row per thread, 128 rows per workgroup (2 waves).
+template <int D>
 __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
@@ -237,8 +262,8 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  __shared__ __attribute__((aligned(16))) float kt_lds[64 * 64];
-  __shared__ __attribute__((aligned(16))) float vt_lds[64 * 64];
+  __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
+  __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
 
   int bh, qb;
   if (!work_item(wm, order, bh, qb)) return;
@@ -249,11 +274,11 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   const int sub = tid >> 5;  // 32-row slice of this thread
   const Span span = mask_row_span(mp, q_row);
 
-  float q[64], o[64];
+  float q[D], o[D];
   {
     const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss;
 #pragma unroll
-    for (int d = 0; d < 64; d += 4) {
+    for (int d = 0; d < D; d += 4) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(qp + d);
       q[d] = v.x * scale_log2;
       q[d + 1] = v.y * scale_log2;
@@ -262,7 +287,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     }
   }
 #pragma unroll
-  for (int d = 0; d < 64; ++d) o[d] = 0.f;
+  for (int d = 0; d < D; ++d) o[d] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
   const float* Kbh = K + b * ksb + hd * ksh;
@@ -272,13 +297,13 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     const int ent = entries[e];
     const int kt = ent & 0xffff;
     __syncthreads();
-    // 64 rows x 16 chunks of 16 bytes per tile; 8 chunks per thread per tile.
-    for (int c = tid; c < 64 * 16; c += 128) {
-      const int row = c >> 4, col = (c & 15) * 4;
+    // 64 rows x D/4 chunks of 16 bytes per tile.
+    for (int c = tid; c < 64 * (D / 4); c += 128) {
+      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
       const int key = min(kt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(kt_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(kt_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Kbh + key * kss + col);
-      *reinterpret_cast<f32x4*>(vt_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(vt_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Vbh + key * vss + col);
     }
     __syncthreads();
@@ -290,7 +315,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     for (int j = 0; j < 64; ++j) {
       float acc = 0.f;
 #pragma unroll
-      for (int d = 0; d < 64; ++d) acc = fmaf(q[d], kt_lds[j * 64 + d], acc);
+      for (int d = 0; d < D; ++d) acc = fmaf(q[d], kt_lds[j * D + d], acc);
       if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
       s[j] = acc;
       mx = fmaxf(mx, acc);
@@ -300,13 +325,13 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     const float alpha = exp2f(m_run - m_use);
     l_run *= alpha;
 #pragma unroll
-    for (int d = 0; d < 64; ++d) o[d] *= alpha;
+    for (int d = 0; d < D; ++d) o[d] *= alpha;
 #pragma unroll
     for (int j = 0; j < 64; ++j) {
       const float pj = exp2f(s[j] - m_use);
       l_run += pj;
 #pragma unroll
-      for (int d = 0; d < 64; ++d) o[d] = fmaf(pj, vt_lds[j * 64 + d], o[d]);
+      for (int d = 0; d < D; ++d) o[d] = fmaf(pj, vt_lds[j * D + d], o[d]);
     }
     m_run = m_new;
   }
@@ -314,7 +339,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
   float* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
 #pragma unroll
-  for (int d = 0; d < 64; d += 4)
+  for (int d = 0; d < D; d += 4)
     *reinterpret_cast<f32x4*>(op + d) =
         f32x4{o[d] * inv_l, o[d + 1] * inv_l, o[d + 2] * inv_l, o[d + 3] * inv_l};
   if (lse) lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + log2f(l_run)) * kLn2;
@@ -330,14 +355,16 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 // the forward's work list. Both recompute S and dP with MFMAs.
 // ---------------------------------------------------------------------------
 
-// Δ[b, h, q] = Σ_d dO[b, h, q, d] · O[b, h, q, d] in fp32: eight lanes per row.
-template <int DT>
+// Δ[b, h, q] = Σ_d dO[b, h, q, d] · O[b, h, q, d] in fp32: D/8 lanes per row,
+// 2048/D rows per workgroup.
+template <int DT, int D>
 __global__ __launch_bounds__(256) void wattn_bwd_delta_kernel(
     const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO, float* __restrict__ delta,
     int64_t osb, int64_t osh, int64_t oss, int64_t gsb, int64_t gsh, int64_t gss, int H, int S,
     int64_t n_rows) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 32 + (threadIdx.x >> 3);
-  const int ch = threadIdx.x & 7;
+  constexpr int kLpr = D / 8;  // lanes per row
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kLpr) + threadIdx.x / kLpr;
+  const int ch = threadIdx.x % kLpr;
   float acc = 0.f;
   if (row < n_rows) {
     const int64_t bh = row / S;
@@ -354,9 +381,8 @@ __global__ __launch_bounds__(256) void wattn_bwd_delta_kernel(
                  Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] >> 16)), acc);
     }
   }
-  acc += __shfl_xor(acc, 1);
-  acc += __shfl_xor(acc, 2);
-  acc += __shfl_xor(acc, 4);
+#pragma unroll
+  for (int o = 1; o < kLpr; o <<= 1) acc += __shfl_xor(acc, o);
   if (row < n_rows && ch == 0) delta[row] = acc;
 }
 
@@ -373,13 +399,13 @@ __device__ __forceinline__ u32x4 pack8(const f32x16& v, int j0) {
 }
 
 // Stores the transposed accumulators acc[dt] (lane = row `row`, entries
-// 32dt + 8(j/4) + 4h + j%4 of the 64 columns) into row `row` of a 16-bit
+// 32dt + 8(j/4) + 4h + j%4 of the 32*NDT columns) into row `row` of a 16-bit
 // tensor, multiplied by `mul`: four consecutive columns per 8-byte store.
-template <int DT>
-__device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 (&acc)[2], float mul,
-                                            int h) {
+template <int DT, int NDT>
+__device__ __forceinline__ void store_row(uint16_t* rowp, const f32x16 (&acc)[NDT], float mul,
+                                          int h) {
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int jg = 0; jg < 4; ++jg) {
       u32x2 packed;
@@ -396,8 +422,8 @@ __device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 (&acc)[
 // (lane = key, 16 queries per lane), P = exp2(S·c − LSE·log2e) and dS, then
 // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, with dOᵀ and Qᵀ read by transpose reads in the
 // accumulator's permuted query order and P, dS packed straight from registers.
-template <int DT>
-__global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
+template <int DT, int D>
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
     uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
@@ -406,8 +432,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  // [buffer][Q, dO] 64x64 tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+  using T = Tile<D>;
+  // [buffer][Q, dO] 64 x D tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
   __shared__ __attribute__((aligned(16))) float stat[2][2][64];
 
   int bh, kb;
@@ -422,13 +449,13 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
   const int key = kb * 128 + wave * 32 + l32;  // this lane's key
   const Span span = mask_col_span(mp, key);     // the queries that see it (partial tiles only)
 
-  u32x4 kf[4], vf[4];
+  u32x4 kf[T::kKk], vf[T::kKk];
   {
     const int kc = min(key, S - 1);
     const uint16_t* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + 8 * h;
     const uint16_t* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < T::kKk; ++kk) {
       kf[kk] = ldg16(kp + 16 * kk);
       vf[kk] = ldg16(vp + 16 * kk);
     }
@@ -440,24 +467,30 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
 
   const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
 
-  u32x4 pre[4];
+  u32x4 pre[2 * T::kPasses];
   float st_pre = 0.f;
-  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
-  const int64_t qoff0 = r0 * qss + c8, qoff1 = (r0 + 32) * qss + c8;
-  const int64_t goff0 = r0 * gss + c8, goff1 = (r0 + 32) * gss + c8;
+  const int r0 = tid / T::kCpr, c8 = (tid % T::kCpr) * 8;
+  int64_t qoff[T::kPasses], goff[T::kPasses];
+#pragma unroll
+  for (int p = 0; p < T::kPasses; ++p) {
+    qoff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * qss + c8;
+    goff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * gss + c8;
+  }
   auto gload = [&](int qt) __attribute__((always_inline)) {
     if (qt * 64 + 64 <= S) {
       const uint16_t* qb = Qbh + static_cast<int64_t>(qt) * 64 * qss;
       const uint16_t* gb = Gbh + static_cast<int64_t>(qt) * 64 * gss;
-      pre[0] = ldg16(qb + qoff0);
-      pre[1] = ldg16(qb + qoff1);
-      pre[2] = ldg16(gb + goff0);
-      pre[3] = ldg16(gb + goff1);
+#pragma unroll
+      for (int p = 0; p < T::kPasses; ++p) {
+        pre[p] = ldg16(qb + qoff[p]);
+        pre[T::kPasses + p] = ldg16(gb + goff[p]);
+      }
     } else {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int qr = min(qt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
-        pre[p] = ldg16((p < 2 ? Qbh + qr * qss : Gbh + qr * gss) + c8);
+      for (int p = 0; p < T::kPasses; ++p) {
+        const int qr = min(qt * 64 + r0 + p * T::kRpp, S - 1);  // rows past S: always masked
+        pre[p] = ldg16(Qbh + qr * qss + c8);
+        pre[T::kPasses + p] = ldg16(Gbh + qr * gss + c8);
       }
     }
     if (tid < 128) {
@@ -467,16 +500,17 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
   };
   auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      sts16(smem + (2 * buf + (p >> 1)) * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
+    for (int p = 0; p < T::kPasses; ++p) {
+      const int off = (r0 + p * T::kRpp) * T::kP + c8;
+      sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
+      sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
     }
     if (tid < 128) stat[buf][tid >> 6][tid & 63] = st_pre;
   };
 
-  f32x16 dkt[2], dvt[2];
+  f32x16 dkt[T::kDt], dvt[T::kDt];
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
+  for (int dt = 0; dt < T::kDt; ++dt) {
     dkt[dt] = f32x16{};
     dvt[dt] = f32x16{};
   }
@@ -495,15 +529,15 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
     if (more) gload(entries[e + 1] & 0xffff);
 
     if (kind != 0) {
-      const uint16_t* q_lds = smem + (2 * buf) * kTileElems;
-      const uint16_t* g_lds = smem + (2 * buf + 1) * kTileElems;
+      const uint16_t* q_lds = smem + (2 * buf) * T::kElems;
+      const uint16_t* g_lds = smem + (2 * buf + 1) * T::kElems;
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh) {
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const u32x4 qa = lds16(q_lds + (32 * qh + l32) * kPitch + 16 * kk + 8 * h);
-          const u32x4 ga = lds16(g_lds + (32 * qh + l32) * kPitch + 16 * kk + 8 * h);
+        for (int kk = 0; kk < T::kKk; ++kk) {
+          const u32x4 qa = lds16(q_lds + (32 * qh + l32) * T::kP + 16 * kk + 8 * h);
+          const u32x4 ga = lds16(g_lds + (32 * qh + l32) * T::kP + 16 * kk + 8 * h);
           s = Mfma<DT>::run(qa, kf[kk], s);
           dp = Mfma<DT>::run(ga, vf[kk], dp);
         }
@@ -535,10 +569,10 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
           const u32x4 pb = pack8<DT>(s, 8 * ks);
           const u32x4 db = pack8<DT>(dp, 8 * ks);
 #pragma unroll
-          for (int dt = 0; dt < 2; ++dt) {
-            const int r0 = 32 * qh + 16 * ks + 4 * h;
-            const u32x4 ga = lds_read_tr4x2(g_lds, r0, r0 + 8, 32 * dt + 16 * grp, lane);
-            const u32x4 qa = lds_read_tr4x2(q_lds, r0, r0 + 8, 32 * dt + 16 * grp, lane);
+          for (int dt = 0; dt < T::kDt; ++dt) {
+            const int rr = 32 * qh + 16 * ks + 4 * h;
+            const u32x4 ga = lds_read_tr4x2<T::kP>(g_lds, rr, rr + 8, 32 * dt + 16 * grp, lane);
+            const u32x4 qa = lds_read_tr4x2<T::kP>(q_lds, rr, rr + 8, 32 * dt + 16 * grp, lane);
             dvt[dt] = Mfma<DT>::run(ga, pb, dvt[dt]);
             dkt[dt] = Mfma<DT>::run(qa, db, dkt[dt]);
           }
@@ -551,8 +585,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
   }
 
   if (key >= S) return;
-  store_row64<DT>(dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss, dkt, scale, h);
-  store_row64<DT>(dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss, dvt, 1.f, h);
+  store_row<DT, T::kDt>(dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss, dkt, scale, h);
+  store_row<DT, T::kDt>(dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss, dvt, 1.f, h);
 }
 
 // dQ. Workgroup = (b, h, 128 queries) as in the forward; wave w owns queries
@@ -561,8 +595,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_kernel(
 // K and V are staged in LDS; the wave computes Sᵀ, dPᵀ, P and dSᵀ (lane = query,
 // 16 keys per lane), then dQᵀ += Kᵀ·dSᵀ with Kᵀ read by transpose reads in the
 // accumulator's permuted key order.
-template <int DT>
-__global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
+template <int DT, int D>
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
     uint16_t* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
@@ -570,7 +604,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileElems];
+  using T = Tile<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
 
   int bh, qb;
   if (!work_item(wm, order, bh, qb)) return;
@@ -584,13 +619,13 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   const int q_row = qb * 128 + wave * 32 + l32;
   const Span span = mask_row_span(mp, q_row);
 
-  u32x4 qf[4], gf[4];
+  u32x4 qf[T::kKk], gf[T::kKk];
   {
     const int qc = min(q_row, S - 1);
     const uint16_t* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss + 8 * h;
     const uint16_t* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss + 8 * h;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
+    for (int kk = 0; kk < T::kKk; ++kk) {
       qf[kk] = ldg16(qp + 16 * kk);
       gf[kk] = ldg16(gp + 16 * kk);
     }
@@ -601,37 +636,44 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
   const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
 
-  u32x4 pre[4];
-  const int r0 = tid >> 3, c8 = (tid & 7) * 8;
-  const int64_t koff0 = r0 * kss + c8, koff1 = (r0 + 32) * kss + c8;
-  const int64_t voff0 = r0 * vss + c8, voff1 = (r0 + 32) * vss + c8;
+  u32x4 pre[2 * T::kPasses];
+  const int r0 = tid / T::kCpr, c8 = (tid % T::kCpr) * 8;
+  int64_t koff[T::kPasses], voff[T::kPasses];
+#pragma unroll
+  for (int p = 0; p < T::kPasses; ++p) {
+    koff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * kss + c8;
+    voff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * vss + c8;
+  }
   auto gload = [&](int kt) __attribute__((always_inline)) {
     if (kt * 64 + 64 <= S) {
       const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
       const uint16_t* vb = Vbh + static_cast<int64_t>(kt) * 64 * vss;
-      pre[0] = ldg16(kb + koff0);
-      pre[1] = ldg16(kb + koff1);
-      pre[2] = ldg16(vb + voff0);
-      pre[3] = ldg16(vb + voff1);
+#pragma unroll
+      for (int p = 0; p < T::kPasses; ++p) {
+        pre[p] = ldg16(kb + koff[p]);
+        pre[T::kPasses + p] = ldg16(vb + voff[p]);
+      }
     } else {
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const int kr = min(kt * 64 + r0 + 32 * (p & 1), S - 1);  // rows past S: always masked
-        pre[p] = ldg16((p < 2 ? Kbh + kr * kss : Vbh + kr * vss) + c8);
+      for (int p = 0; p < T::kPasses; ++p) {
+        const int kr = min(kt * 64 + r0 + p * T::kRpp, S - 1);  // rows past S: always masked
+        pre[p] = ldg16(Kbh + kr * kss + c8);
+        pre[T::kPasses + p] = ldg16(Vbh + kr * vss + c8);
       }
     }
   };
   auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 32 * (p & 1);
-      sts16(smem + (2 * buf + (p >> 1)) * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
+    for (int p = 0; p < T::kPasses; ++p) {
+      const int off = (r0 + p * T::kRpp) * T::kP + c8;
+      sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
+      sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
     }
   };
 
-  f32x16 dqt[2];
-  dqt[0] = f32x16{};
-  dqt[1] = f32x16{};
+  f32x16 dqt[T::kDt];
+#pragma unroll
+  for (int dt = 0; dt < T::kDt; ++dt) dqt[dt] = f32x16{};
 
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
@@ -647,17 +689,17 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
     if (more) gload(entries[e + 1] & 0xffff);
 
     if (kind != 0) {
-      const uint16_t* k_lds = smem + (2 * buf) * kTileElems;
-      const uint16_t* v_lds = smem + (2 * buf + 1) * kTileElems;
+      const uint16_t* k_lds = smem + (2 * buf) * T::kElems;
+      const uint16_t* v_lds = smem + (2 * buf + 1) * T::kElems;
       f32x16 s[2], dp[2];
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         s[kh] = f32x16{};
         dp[kh] = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const u32x4 ka = lds16(k_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
-          const u32x4 va = lds16(v_lds + (32 * kh + l32) * kPitch + 16 * kk + 8 * h);
+        for (int kk = 0; kk < T::kKk; ++kk) {
+          const u32x4 ka = lds16(k_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
+          const u32x4 va = lds16(v_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
           s[kh] = Mfma<DT>::run(ka, qf[kk], s[kh]);
           dp[kh] = Mfma<DT>::run(va, gf[kk], dp[kh]);
         }
@@ -684,9 +726,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
       for (int ks = 0; ks < 4; ++ks) {
         const u32x4 db = pack8<DT>(dp[ks >> 1], 8 * (ks & 1));
 #pragma unroll
-        for (int dt = 0; dt < 2; ++dt) {
-          const u32x4 ka = lds_read_tr4x2(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
-                                          32 * dt + 16 * grp, lane);
+        for (int dt = 0; dt < T::kDt; ++dt) {
+          const u32x4 ka = lds_read_tr4x2<T::kP>(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
+                                                 32 * dt + 16 * grp, lane);
           dqt[dt] = Mfma<DT>::run(ka, db, dqt[dt]);
         }
       }
@@ -697,17 +739,19 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_kernel(
   }
 
   if (q_row >= S) return;
-  store_row64<DT>(dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss, dqt, scale, h);
+  store_row<DT, T::kDt>(dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss, dqt, scale, h);
 }
 
-// fp32 backward (FMA path, for fp32 modules). Δ[b, h, q] = Σ_d dO · O, eight
-// lanes per row.
+// fp32 backward (FMA path, for fp32 modules). Δ[b, h, q] = Σ_d dO · O, D/8
+// lanes per row (eight elements each).
+template <int D>
 __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
     const float* __restrict__ O, const float* __restrict__ dO, float* __restrict__ delta,
     int64_t osb, int64_t osh, int64_t oss, int64_t gsb, int64_t gsh, int64_t gss, int H, int S,
     int64_t n_rows) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 32 + (threadIdx.x >> 3);
-  const int ch = threadIdx.x & 7;
+  constexpr int kLpr = D / 8;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kLpr) + threadIdx.x / kLpr;
+  const int ch = threadIdx.x % kLpr;
   float acc = 0.f;
   if (row < n_rows) {
     const int64_t bh = row / S;
@@ -722,14 +766,14 @@ __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
       acc = fmaf(o.x, g.x, fmaf(o.y, g.y, fmaf(o.z, g.z, fmaf(o.w, g.w, acc))));
     }
   }
-  acc += __shfl_xor(acc, 1);
-  acc += __shfl_xor(acc, 2);
-  acc += __shfl_xor(acc, 4);
+#pragma unroll
+  for (int o = 1; o < kLpr; o <<= 1) acc += __shfl_xor(acc, o);
   if (row < n_rows && ch == 0) delta[row] = acc;
 }
 
 // fp32 dQ: one query row per thread (128 per workgroup, the forward's work
 // list); K and V tiles staged in LDS and read as broadcasts.
+template <int D>
 __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -738,8 +782,8 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  __shared__ __attribute__((aligned(16))) float kt_lds[64 * 64];
-  __shared__ __attribute__((aligned(16))) float vt_lds[64 * 64];
+  __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
+  __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
 
   int bh, qb;
   if (!work_item(wm, order, bh, qb)) return;
@@ -751,12 +795,12 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
   const int sub = tid >> 5;
   const Span span = mask_row_span(mp, q_row);
 
-  float q[64], g[64], dq[64];
+  float q[D], g[D], dq[D];
   {
     const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss;
     const float* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss;
 #pragma unroll
-    for (int d = 0; d < 64; d += 4) {
+    for (int d = 0; d < D; d += 4) {
       const f32x4 v = *reinterpret_cast<const f32x4*>(qp + d);
       const f32x4 w = *reinterpret_cast<const f32x4*>(gp + d);
       q[d] = v.x * scale_log2;
@@ -770,7 +814,7 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     }
   }
 #pragma unroll
-  for (int d = 0; d < 64; ++d) dq[d] = 0.f;
+  for (int d = 0; d < D; ++d) dq[d] = 0.f;
   const float l2 = lse[static_cast<int64_t>(bh) * S + qc] * kLog2e;
   const float dl = delta[static_cast<int64_t>(bh) * S + qc];
 
@@ -781,12 +825,12 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     const int ent = entries[e];
     const int kt = ent & 0xffff;
     __syncthreads();
-    for (int c = tid; c < 64 * 16; c += 128) {
-      const int row = c >> 4, col = (c & 15) * 4;
+    for (int c = tid; c < 64 * (D / 4); c += 128) {
+      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
       const int key = min(kt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(kt_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(kt_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Kbh + key * kss + col);
-      *reinterpret_cast<f32x4*>(vt_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(vt_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Vbh + key * vss + col);
     }
     __syncthreads();
@@ -795,28 +839,29 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     for (int j = 0; j < 64; ++j) {
       float sj = 0.f, dp = 0.f;
 #pragma unroll
-      for (int d = 0; d < 64; ++d) {
-        sj = fmaf(q[d], kt_lds[j * 64 + d], sj);
-        dp = fmaf(g[d], vt_lds[j * 64 + d], dp);
+      for (int d = 0; d < D; ++d) {
+        sj = fmaf(q[d], kt_lds[j * D + d], sj);
+        dp = fmaf(g[d], vt_lds[j * D + d], dp);
       }
       float pj = __builtin_amdgcn_exp2f(sj - l2);
       if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
       const float ds = pj * (dp - dl);
 #pragma unroll
-      for (int d = 0; d < 64; ++d) dq[d] = fmaf(ds, kt_lds[j * 64 + d], dq[d]);
+      for (int d = 0; d < D; ++d) dq[d] = fmaf(ds, kt_lds[j * D + d], dq[d]);
     }
   }
   if (q_row >= S) return;
   float* dp_out = dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss;
 #pragma unroll
-  for (int d = 0; d < 64; d += 4)
+  for (int d = 0; d < D; d += 4)
     *reinterpret_cast<f32x4*>(dp_out + d) =
         f32x4{dq[d] * scale, dq[d + 1] * scale, dq[d + 2] * scale, dq[d + 3] * scale};
 }
 
-// fp32 dK, dV: two lanes per key (lane and lane + 32 hold head dims 0..31 and
-// 32..63), 32 keys per wave, 128 per workgroup (the key-major work list); Q,
-// dO, LSE and Δ of each listed 64-query tile staged in LDS.
+// fp32 dK, dV: two lanes per key (lane and lane + 32 hold head dims 0..D/2-1
+// and D/2..D-1), 32 keys per wave, 128 per workgroup (the key-major work
+// list); Q, dO, LSE and Δ of each listed 64-query tile staged in LDS.
+template <int D>
 __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -826,8 +871,9 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm) {
-  __shared__ __attribute__((aligned(16))) float q_lds[64 * 64];
-  __shared__ __attribute__((aligned(16))) float g_lds[64 * 64];
+  constexpr int kHd = D / 2;  // head dims per lane
+  __shared__ __attribute__((aligned(16))) float q_lds[64 * D];
+  __shared__ __attribute__((aligned(16))) float g_lds[64 * D];
   __shared__ float l2_lds[64], dl_lds[64];
 
   int bh, kb;
@@ -841,12 +887,12 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
   const int kc = min(key, S - 1);
   const Span span = mask_col_span(mp, key);
 
-  float k[32], v[32], dk[32], dv[32];
+  float k[kHd], v[kHd], dk[kHd], dv[kHd];
   {
-    const float* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + 32 * half;
-    const float* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + 32 * half;
+    const float* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + kHd * half;
+    const float* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + kHd * half;
 #pragma unroll
-    for (int d = 0; d < 32; d += 4) {
+    for (int d = 0; d < kHd; d += 4) {
       const f32x4 a = *reinterpret_cast<const f32x4*>(kp + d);
       const f32x4 c = *reinterpret_cast<const f32x4*>(vp + d);
       k[d] = a.x;
@@ -860,7 +906,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     }
   }
 #pragma unroll
-  for (int d = 0; d < 32; ++d) {
+  for (int d = 0; d < kHd; ++d) {
     dk[d] = 0.f;
     dv[d] = 0.f;
   }
@@ -873,12 +919,12 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     const int ent = entries[e];
     const int qt = ent & 0xffff;
     __syncthreads();
-    for (int c = tid; c < 64 * 16; c += 256) {
-      const int row = c >> 4, col = (c & 15) * 4;
+    for (int c = tid; c < 64 * (D / 4); c += 256) {
+      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
       const int qr = min(qt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(q_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(q_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Qbh + qr * qss + col);
-      *reinterpret_cast<f32x4*>(g_lds + row * 64 + col) =
+      *reinterpret_cast<f32x4*>(g_lds + row * D + col) =
           *reinterpret_cast<const f32x4*>(Gbh + qr * gss + col);
     }
     if (tid < 64) {
@@ -890,11 +936,11 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     if (kind == 0) continue;
     for (int i = 0; i < 64; ++i) {
-      const float* qi = q_lds + i * 64 + 32 * half;
-      const float* gi = g_lds + i * 64 + 32 * half;
+      const float* qi = q_lds + i * D + kHd * half;
+      const float* gi = g_lds + i * D + kHd * half;
       float sp = 0.f, dpp = 0.f;
 #pragma unroll
-      for (int d = 0; d < 32; ++d) {
+      for (int d = 0; d < kHd; ++d) {
         sp = fmaf(qi[d], k[d], sp);
         dpp = fmaf(gi[d], v[d], dpp);
       }
@@ -904,17 +950,17 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
       if (kind == 2 && !span_has(span, qt * 64 + i)) pi = 0.f;
       const float ds = pi * (dpp - dl_lds[i]);
 #pragma unroll
-      for (int d = 0; d < 32; ++d) {
+      for (int d = 0; d < kHd; ++d) {
         dv[d] = fmaf(pi, gi[d], dv[d]);
         dk[d] = fmaf(ds, qi[d], dk[d]);
       }
     }
   }
   if (key >= S) return;
-  float* dkp = dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss + 32 * half;
-  float* dvp = dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss + 32 * half;
+  float* dkp = dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss + kHd * half;
+  float* dvp = dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss + kHd * half;
 #pragma unroll
-  for (int d = 0; d < 32; d += 4) {
+  for (int d = 0; d < kHd; d += 4) {
     *reinterpret_cast<f32x4*>(dkp + d) =
         f32x4{dk[d] * scale, dk[d + 1] * scale, dk[d + 2] * scale, dk[d + 3] * scale};
     *reinterpret_cast<f32x4*>(dvp + d) = f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]};
@@ -936,6 +982,33 @@ inline WorkMap make_work_map(int n_bh, int n_blk, int n_lead, unsigned* grid) {
   return m;
 }
 
+template <int D>
+void launch_wattn_fwd(int dtype, unsigned grid, hipStream_t s, const void* d_Q, const void* d_K,
+                      const void* d_V, void* d_O, float* d_lse, const int64_t* qs,
+                      const int64_t* ks, const int64_t* vs, const int64_t* os, int H,
+                      const MaskParams& mp, float scale_log2, const int32_t* d_row_ptr,
+                      const int32_t* d_entries, const int32_t* d_order, const WorkMap& wm) {
+  if (dtype == TMAC_F32) {
+    hipLaunchKernelGGL((wattn_fwd_f32_kernel<D>), dim3(grid), dim3(128), 0, s,
+                       static_cast<const float*>(d_Q), static_cast<const float*>(d_K),
+                       static_cast<const float*>(d_V), static_cast<float*>(d_O), d_lse, qs[0],
+                       qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2],
+                       H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+  } else if (dtype == TMAC_BF16) {
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16, D>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
+                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
+                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+  } else {
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16, D>), dim3(grid), dim3(256), 0, s,
+                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
+                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
+                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+  }
+}
+
 }  // namespace
 
 extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const void* d_K,
@@ -949,7 +1022,7 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
       !d_row_ptr || !d_entries || !d_order)
     return TMAC_ERR_NULL;
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
-  if (dh != 64) return TMAC_ERR_SHAPE;
+  if (dh != 32 && dh != 64 && dh != 128) return TMAC_ERR_SHAPE;
   if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
   if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
   if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
@@ -976,24 +1049,19 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
   const int64_t* ks = k_strides;
   const int64_t* vs = v_strides;
   const int64_t* os = o_strides;
-  if (dtype == TMAC_F32) {
-    hipLaunchKernelGGL(wattn_fwd_f32_kernel, dim3(grid), dim3(128), 0, s,
-                       static_cast<const float*>(d_Q), static_cast<const float*>(d_K),
-                       static_cast<const float*>(d_V), static_cast<float*>(d_O), d_lse, qs[0],
-                       qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2],
-                       H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
-  } else if (dtype == TMAC_BF16) {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16>), dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
-                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
-  } else {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16>), dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
-                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+  switch (dh) {
+    case 32:
+      launch_wattn_fwd<32>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
+                           scale_log2, d_row_ptr, d_entries, d_order, wm);
+      break;
+    case 64:
+      launch_wattn_fwd<64>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
+                           scale_log2, d_row_ptr, d_entries, d_order, wm);
+      break;
+    default:
+      launch_wattn_fwd<128>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
+                            scale_log2, d_row_ptr, d_entries, d_order, wm);
+      break;
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
@@ -1018,7 +1086,7 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
       !d_entries_kv || !d_order_kv)
     return TMAC_ERR_NULL;
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
-  if (dh != 64) return TMAC_ERR_SHAPE;
+  if (dh != 32 && dh != 64 && dh != 128) return TMAC_ERR_SHAPE;
   if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
   if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
   if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
@@ -1055,19 +1123,34 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
   const int64_t *qs = q_strides, *ks = k_strides, *vs = v_strides, *os = o_strides,
                 *gs = do_strides, *dqs = dq_strides, *dks = dk_strides, *dvs = dv_strides;
   const int64_t n_rows = static_cast<int64_t>(B) * H * S;
-  const unsigned dgrid = static_cast<unsigned>((n_rows + 31) / 32);
-#define TMAC_WATTN_BWD(DTV)                                                                          \
+  // row-sum kernel: 2048/D rows per workgroup
+  const unsigned dgrid = static_cast<unsigned>((n_rows * dh + 2047) / 2048);
+#define TMAC_WATTN_BWD(DTV, DV)                                                                      \
   do {                                                                                               \
-    hipLaunchKernelGGL((wattn_bwd_delta_kernel<DTV>), dim3(dgrid), dim3(256), 0, s, O, G, d_delta,   \
-                       os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);                      \
-    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV>), dim3(grid_kv), dim3(256), 0, s, Q, K, V, G,       \
+    hipLaunchKernelGGL((wattn_bwd_delta_kernel<DTV, DV>), dim3(dgrid), dim3(256), 0, s, O, G,        \
+                       d_delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);             \
+    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV, DV>), dim3(grid_kv), dim3(256), 0, s, Q, K, V, G,   \
                        d_lse, d_delta, dK, dV, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],      \
                        vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],    \
                        dvs[2], H, mp, scale, scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv); \
-    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV>), dim3(grid_q), dim3(256), 0, s, Q, K, V, G,         \
+    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV, DV>), dim3(grid_q), dim3(256), 0, s, Q, K, V, G,     \
                        d_lse, d_delta, dQ, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],   \
                        vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H, mp, scale, scale_log2, \
                        d_row_ptr, d_entries, d_order, wm_q);                                         \
+  } while (0)
+#define TMAC_WATTN_BWD_F32(DV)                                                                       \
+  do {                                                                                               \
+    hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<DV>), dim3(dgrid), dim3(256), 0, s, Of, Gf,       \
+                       d_delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);             \
+    hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<DV>), dim3(grid_kv), dim3(256), 0, s, Qf, Kf, Vf,    \
+                       Gf, d_lse, d_delta, static_cast<float*>(d_dK), static_cast<float*>(d_dV),     \
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],  \
+                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], H, mp, scale,          \
+                       scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv);                      \
+    hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<DV>), dim3(grid_q), dim3(128), 0, s, Qf, Kf, Vf, Gf,  \
+                       d_lse, d_delta, static_cast<float*>(d_dQ), qs[0], qs[1], qs[2], ks[0], ks[1], \
+                       ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H,   \
+                       mp, scale, scale_log2, d_row_ptr, d_entries, d_order, wm_q);                  \
   } while (0)
   if (dtype == TMAC_F32) {
     const auto* Qf = static_cast<const float*>(d_Q);
@@ -1075,23 +1158,29 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
     const auto* Vf = static_cast<const float*>(d_V);
     const auto* Of = static_cast<const float*>(d_O);
     const auto* Gf = static_cast<const float*>(d_dO);
-    hipLaunchKernelGGL(wattn_bwd_delta_f32_kernel, dim3(dgrid), dim3(256), 0, s, Of, Gf, d_delta,
-                       os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);
-    hipLaunchKernelGGL(wattn_bwd_kv_f32_kernel, dim3(grid_kv), dim3(256), 0, s, Qf, Kf, Vf, Gf,
-                       d_lse, d_delta, static_cast<float*>(d_dK), static_cast<float*>(d_dV),
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
-                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], H, mp, scale,
-                       scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv);
-    hipLaunchKernelGGL(wattn_bwd_q_f32_kernel, dim3(grid_q), dim3(128), 0, s, Qf, Kf, Vf, Gf, d_lse,
-                       d_delta, static_cast<float*>(d_dQ), qs[0], qs[1], qs[2], ks[0], ks[1],
-                       ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H,
-                       mp, scale, scale_log2, d_row_ptr, d_entries, d_order, wm_q);
+    if (dh == 32)
+      TMAC_WATTN_BWD_F32(32);
+    else if (dh == 64)
+      TMAC_WATTN_BWD_F32(64);
+    else
+      TMAC_WATTN_BWD_F32(128);
   } else if (dtype == TMAC_BF16) {
-    TMAC_WATTN_BWD(TMAC_BF16);
+    if (dh == 32)
+      TMAC_WATTN_BWD(TMAC_BF16, 32);
+    else if (dh == 64)
+      TMAC_WATTN_BWD(TMAC_BF16, 64);
+    else
+      TMAC_WATTN_BWD(TMAC_BF16, 128);
   } else {
-    TMAC_WATTN_BWD(TMAC_F16);
+    if (dh == 32)
+      TMAC_WATTN_BWD(TMAC_F16, 32);
+    else if (dh == 64)
+      TMAC_WATTN_BWD(TMAC_F16, 64);
+    else
+      TMAC_WATTN_BWD(TMAC_F16, 128);
   }
 #undef TMAC_WATTN_BWD
+#undef TMAC_WATTN_BWD_F32
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }

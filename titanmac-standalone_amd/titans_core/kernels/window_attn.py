@@ -31,6 +31,7 @@ from . import _lib
 
 PATTERNS = {"band": _lib.PATTERN_BAND, "blockwin": _lib.PATTERN_BLOCKWIN}
 Q_BLOCK, SUB_ROWS = 128, 32  # kernel geometry: 128 query rows per workgroup, 32 per wave
+HEAD_DIMS = (32, 64, 128)  # head dimensions the kernels are instantiated for
 
 _sched_lock = threading.Lock()
 _sched_cache: dict = {}
@@ -152,8 +153,9 @@ def _check_qkv(q, k, v):
                          f"{tuple(q.shape)}, {tuple(k.shape)}, {tuple(v.shape)}")
     if not (q.dtype == k.dtype == v.dtype):
         raise TypeError("q, k, v must share one dtype")
-    if int(q.shape[3]) != 64:
-        raise ValueError(f"the attention kernel is built for head_dim 64, got {int(q.shape[3])}")
+    if int(q.shape[3]) not in HEAD_DIMS:
+        raise ValueError(f"the attention kernel is built for head_dim in {HEAD_DIMS}, "
+                         f"got {int(q.shape[3])}")
     for t in (q, k, v):
         if t.stride(3) != 1:
             raise ValueError("q, k, v need a contiguous last (head_dim) dimension")
