@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 2
+#define TMAC_ABI_VERSION 3
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -327,6 +327,62 @@ int tmac_rmsnorm_bwd(const void* d_dy, int64_t lddy, const void* d_x, int64_t ld
                      const void* d_scale, const float* d_rstd, void* d_dx, int64_t lddx,
                      float* d_dscale, void* d_ws, size_t ws_bytes, int M, int D, int dtype,
                      void* stream);
+
+/* ------------------------------------------------------------------------- */
+/* Titans neural memory: update of the memory MLP (device).                   */
+/* ------------------------------------------------------------------------- */
+
+#define TMAC_MEM_MAX_TENSORS 16
+
+/* Clip rule of tmac_mem_update. */
+typedef enum {
+  /* NeuralMemory.update (memory/neural_memory.py:391-409): scale = max_norm/norm
+   * only when norm > max_norm (the clipped gradient is written back into the
+   * gradient tensors, as the reference's in-place mul_ does); the whole update
+   * is skipped when any gradient is NaN or Inf. */
+  TMAC_MEM_CLIP_MEMORY = 0,
+  /* fused_clip_momentum_update (kernels/memory_mlp.py:129-131): scale =
+   * min(1, max_norm / (norm + 1e-8)), never skipped, gradients left as they are. */
+  TMAC_MEM_CLIP_KERNEL = 1
+} tmac_mem_clip_mode;
+
+/* Bytes of device workspace tmac_mem_update needs for these tensor sizes
+ * (8 bytes per workgroup of the launch; at most 16 KB). */
+int tmac_mem_update_workspace(const int64_t* sizes, int n_tensors, size_t* ws_bytes);
+
+/* The Titans memory step over n_tensors (<= TMAC_MEM_MAX_TENSORS) parameter
+ * tensors, elementwise on tensor i's sizes[i] contiguous elements:
+ *   norm = ||g||₂ over all tensors, g' = g · scale(norm, mode),
+ *   S ← η·S − θ·g',  W ← (1 − α)·W + S,  mirror (if given) ← W.
+ * Replaces NeuralMemory.update's flatten / norm / clip / NaN check / momentum /
+ * parameter steps (memory/neural_memory.py:386-434) and the Triton
+ * fused_clip_momentum_update with its norm (kernels/memory_mlp.py:51-154,
+ * 233-252). Two launches on `stream`, no host synchronisation: α (forget gate)
+ * and η (decay gate) are read from device scalars d_alpha, d_eta (fp32).
+ * d_grads/d_moms/d_weights/d_mirrors: host arrays of n_tensors device pointers
+ * (d_mirrors and its entries nullable), all of `dtype` (TMAC_F32/BF16/F16,
+ * fp32 arithmetic). d_norm (nullable): a device fp32 norm to use instead of
+ * computing ||g|| (fused_clip_momentum_update's grad_norm argument); then one
+ * launch and no workspace, and in TMAC_MEM_CLIP_MEMORY mode the skip test is
+ * "norm not finite". d_stats: fp32 [4] receives norm, scale, skipped (0/1),
+ * clipped (0/1). The norm is summed per workgroup and re-added in a fixed
+ * order: deterministic. Calls that share a workspace must not overlap. */
+int tmac_mem_update(void* const* d_grads, void* const* d_moms, void* const* d_weights,
+                    void* const* d_mirrors, const int64_t* sizes, int n_tensors,
+                    const float* d_alpha, const float* d_eta, const float* d_norm, float theta,
+                    float max_norm, int mode, float* d_stats, void* d_ws, size_t ws_bytes,
+                    int dtype, void* stream);
+
+/* dz = dh · σ(z)·(1 + z·(1 − σ(z))) over n contiguous elements: the SiLU
+ * backward of the memory MLP's hand-written gradient (silu_backward,
+ * kernels/memory_mlp.py:28-44, memory/manual_backward.py:26-41). */
+int tmac_silu_bwd(const void* d_dh, const void* d_z, void* d_dz, int64_t n, int dtype,
+                  void* stream);
+
+/* dy = coef · (y − v) over n contiguous elements: the MSE gradient that starts
+ * the memory MLP's backward, coef = 2 / numel (kernels/memory_mlp.py:215-218). */
+int tmac_mse_grad(const void* d_y, const void* d_v, void* d_dy, int64_t n, float coef, int dtype,
+                  void* stream);
 
 #ifdef __cplusplus
 }

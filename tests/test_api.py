@@ -3,6 +3,7 @@ BlockELLLinear construction and state_dicts, build_band_mask, dense <-> ELL
 conversion, meta shapes of the torch ops, and that the hot path refuses CPU
 tensors instead of falling back."""
 import dataclasses
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -249,3 +250,60 @@ def test_titan_block_ell_loads_dense_reference_checkpoint():
 def test_rms_norm_refuses_cpu_tensors():
     with pytest.raises(RuntimeError, match="GPU"):
         tc.RMSNorm(64)(torch.randn(2, 64))
+
+
+MAC_CFG = dict(vocab_size=61, d_model=64, n_heads=1, n_layers=2, d_ff=128, max_seq_len=128,
+               window_size=40, n_persistent=4, block_size=32, use_neural_memory=True,
+               segment_size=48, n_memory_tokens=8)
+
+
+def test_titanmac_state_dict_keys_match_reference_checkpoint():
+    """Every key and shape of the reference's TitanMAC state_dict (the golden checkpoint was
+    written by the reference module itself) and nothing else."""
+    gold = np.load(Path(__file__).parent / "golden" / "mac_golden.npz")
+    want = {k[len("state/"):]: gold[k].shape for k in gold.files if k.startswith("state/")}
+    m = tc.TitanMAC(tc.TitanMACConfig(**MAC_CFG))
+    assert {k: tuple(v.shape) for k, v in m.state_dict().items()} == want
+    m.load_state_dict({k: torch.from_numpy(gold[f"state/{k}"]) for k in want})
+    assert m.lm_head.weight is m.embed_tokens.weight          # tie_weights
+    assert isinstance(m.layers[0].attention, tc.BlockSparseAttention)
+
+
+def test_titanmac_init_and_param_counts():
+    torch.manual_seed(0)
+    cfg = tc.TitanMACConfig(**dict(MAC_CFG, tie_weights=False))
+    m = tc.TitanMAC(cfg)
+    assert abs(float(m.embed_tokens.weight.std()) - 0.02) < 3e-3
+    assert m.memory_proj.weight.shape == (64, 64) and m.gate_proj.bias.shape == (64,)
+    total = sum(p.numel() for p in m.parameters())
+    emb = m.embed_tokens.weight.numel() + m.embed_positions.weight.numel() + m.lm_head.weight.numel()
+    assert m.get_num_params(False) == total and m.get_num_params(True) == total - emb
+    nm = m.neural_memory
+    n = sum(p.numel() for p in nm.memory_mlp.parameters())
+    assert nm.momentum_S.shape == (n,) and nm._flat_param_cache.shape == (n,)
+    assert [o for o, _ in nm._param_offsets] == [0, 64 * 64, 64 * 64 + 64, 2 * 64 * 64 + 64]
+    plain = tc.TitanMAC(tc.TitanMACConfig(**dict(MAC_CFG, use_neural_memory=False)))
+    assert plain.neural_memory is None and plain.memory_proj is None
+    with pytest.raises(ValueError, match="use_neural_memory"):
+        plain.forward_mac(torch.zeros(1, 4, dtype=torch.long))
+    with pytest.raises(NotImplementedError):
+        tc.TitanMAC(tc.TitanMACConfig(**dict(MAC_CFG, use_memory_bank=True)))
+
+
+def test_neural_memory_construction_errors_and_cpu_refusal():
+    nm = tc.NeuralMemory(d_model=32, n_memory_layers=3, theta_lr=0.1)
+    assert len(nm.memory_mlp.linears()) == 3 and nm.theta == 0.1
+    for kw, msg in ((dict(d_model=0), "d_model"), (dict(d_model=8, n_memory_layers=0), "n_memory"),
+                    (dict(d_model=8, theta_lr=0.0), "theta_lr")):
+        with pytest.raises(ValueError, match=msg):
+            tc.NeuralMemory(**kw)
+    with pytest.raises(ValueError, match="3D"):
+        nm.update(torch.zeros(4, 32))
+    with pytest.raises(RuntimeError, match="GPU"):
+        nm.update(torch.zeros(1, 4, 32))
+    # retrieval and the loss are plain torch modules (no HIP op on their path)
+    x = torch.randn(2, 5, 32)
+    assert nm.retrieve(x).shape == (2, 5, 32) and nm.compute_loss(x).dim() == 0
+    from titans_core.kernels import memory_mlp as km
+    with pytest.raises(RuntimeError, match="GPU"):
+        km.silu_backward(torch.zeros(4), torch.zeros(4))

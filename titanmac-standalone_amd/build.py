@@ -36,7 +36,7 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]
 SOURCES = ["tmac_host.cpp", "bell_kernels.hip", "wattn_kernels.hip", "conv_kernels.hip",
-           "norm_kernels.hip"]
+           "norm_kernels.hip", "memory_kernels.hip"]
 
 
 def _hipcc() -> str:

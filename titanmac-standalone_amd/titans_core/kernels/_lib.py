@@ -14,11 +14,13 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
 PATTERN_BAND, PATTERN_BLOCKWIN = 0, 1
+MEM_CLIP_MEMORY, MEM_CLIP_KERNEL = 0, 1
+MEM_MAX_TENSORS = 16
 
 _DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -60,6 +62,11 @@ SIGNATURES = {
     "tmac_rmsnorm_fwd": [_vp, _i64, _vp, _vp, _i64, _vp, _i, _i, ctypes.c_float, _i, _vp],
     "tmac_rmsnorm_bwd_workspace": [_i, _i, ctypes.POINTER(_sz)],
     "tmac_rmsnorm_bwd": [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _vp],
+    "tmac_mem_update_workspace": [_i64p, _i, ctypes.POINTER(_sz)],
+    "tmac_mem_update": [_vp, _vp, _vp, _vp, _i64p, _i, _vp, _vp, _vp, ctypes.c_float,
+                        ctypes.c_float, _i, _vp, _vp, _sz, _i, _vp],
+    "tmac_silu_bwd": [_vp, _vp, _vp, _i64, _i, _vp],
+    "tmac_mse_grad": [_vp, _vp, _vp, _i64, ctypes.c_float, _i, _vp],
 }
 
 
