@@ -18,7 +18,14 @@ The same run also times, as secondary figures:
   - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40);
   - the causal depthwise conv of BlockSparseAttention (B=8, T=4096, 1920 channels,
     4 taps) and TitanBlock's RMSNorm (32768 x 640), forward and backward, in GB/s
-    of compulsory HBM traffic.
+    of compulsory HBM traffic;
+  - config 5: the full TitanMAC forward (MAC variant, 16 layers, d_model 640, 10 heads,
+    window 512, 16 persistent tokens, 32 memory tokens per 512-token segment, Block-ELL
+    MLP at 50%, vocab 50000, random init) on token ids [4, 4096] in bf16, eval, in
+    tokens/s; once with the read-only memory of the default config (segments batched) and
+    once with test-time memory on (segments in order, one memory update each);
+  - the neural-memory update step (norm, clip, momentum, forgetting) over config 5's
+    memory MLP (2 x 640 x 640 + biases, fp32) in GB/s of compulsory traffic.
 Inputs are drawn on the CPU from fixed seeds and copied to HBM before timing.
 Kernel time is measured with HIP events on the launch stream (torch's current
 stream) around exactly K back-to-back launches after W warm-up launches, with a
@@ -26,8 +33,8 @@ device synchronisation on both sides; ms_per_step is that time over K.
 The CPU baseline runs the oracle's dense restatement of the reference path
 (X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only.
 
-Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, conv, norm, copy (a
-plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
+Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, conv, norm, mac,
+mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
 """
 from __future__ import annotations
 
@@ -235,6 +242,65 @@ def dense_attention_bwd_baseline(att, bwd, steps: int, stream):
     return timed(dense_bwd, max(2, steps // 10), 2, stream)
 
 
+CFG5 = dict(B=4, T=4096, vocab_size=50000, d_model=640, n_heads=10, n_layers=16, window_size=512,
+            n_persistent=16, seed=7)
+
+
+def setup_mac(dev, test_time_memory=False):
+    """Config 5: TitanMAC forward (MAC) with the Block-ELL MLP at 50%, bf16, eval."""
+    sys.path.insert(0, str(ROOT / "titanmac-standalone_amd"))
+    import titans_core as tc
+    c = CFG5
+    cfg = tc.TitanMACConfig(vocab_size=c["vocab_size"], d_model=c["d_model"], n_heads=c["n_heads"],
+                            n_layers=c["n_layers"], window_size=c["window_size"],
+                            n_persistent=c["n_persistent"], use_neural_memory=True,
+                            titans_variant="MAC", memory_capacity=256, mlp_block_ell=True,
+                            mlp_density=0.5, enable_test_time_memory=test_time_memory)
+    torch.manual_seed(c["seed"])
+    model = tc.TitanMAC(cfg).to(dev, torch.bfloat16).eval()
+    g = torch.Generator().manual_seed(c["seed"] + 1)
+    ids = torch.randint(0, c["vocab_size"], (c["B"], c["T"]), generator=g).to(dev)
+    res = {}
+
+    def launch():
+        with torch.no_grad():
+            res["out"] = model(ids)
+
+    return dict(launch=launch, tokens=c["B"] * c["T"], keep=(model, ids, res))
+
+
+def setup_memupd(dev):
+    """The neural-memory update step (tmac_mem_update: norm, clip, momentum, forgetting) over
+    config 5's memory MLP parameters, fp32, called through the C ABI with prebuilt arguments."""
+    import ctypes
+    d = CFG5["d_model"]
+    sizes = [d * d, d, d * d, d]
+    g = [gen((n,), 40 + i, 0.001, torch.float32).to(dev) for i, n in enumerate(sizes)]
+    s_ = [gen((n,), 50 + i, 0.01, torch.float32).to(dev) for i, n in enumerate(sizes)]
+    w = [gen((n,), 60 + i, 0.02, torch.float32).to(dev) for i, n in enumerate(sizes)]
+    a = torch.tensor(0.01, device=dev)
+    e = torch.tensor(0.9, device=dev)
+    stats = torch.empty(4, dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    n_t = len(sizes)
+    sz = (ctypes.c_int64 * n_t)(*sizes)
+    wsb = ctypes.c_size_t(0)
+    _lib.check(L.tmac_mem_update_workspace(sz, n_t, ctypes.byref(wsb)), "workspace")
+    ws = torch.empty(wsb.value, dtype=torch.uint8, device=dev)
+    arr = lambda ts: (ctypes.c_void_p * n_t)(*[t.data_ptr() for t in ts])  # noqa: E731
+    args = (arr(g), arr(s_), arr(w), None, sz, n_t, _lib.ptr(a), _lib.ptr(e), None,
+            ctypes.c_float(1e-6), ctypes.c_float(1.0), _lib.MEM_CLIP_MEMORY, _lib.ptr(stats),
+            _lib.ptr(ws), ws.numel(), _lib.F32, _lib.stream_ptr(dev))
+
+    def launch():
+        rc = L.tmac_mem_update(*args)
+        if rc:
+            _lib.check(rc, "tmac_mem_update")
+
+    n = sum(sizes)
+    return dict(launch=launch, params=n, bytes=20 * n, keep=(g, s_, w, a, e, stats, ws, args))
+
+
 CONV = dict(B=8, T=4096, C=1920, k=4, seed=5)   # BlockSparseAttention q/k/v conv at config 3's shape
 NORM = dict(M=32768, D=640, seed=6)               # TitanBlock RMSNorm over config 3's tokens
 
@@ -425,7 +491,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "conv",
-                                                     "norm", "copy"])
+                                                     "norm", "mac", "mac_ttm", "memupd", "copy"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the hot path's kernels run on one MI355X and this "
@@ -491,6 +557,21 @@ def main() -> int:
             out[mode] = dict(fwd_ms=f_ms, fwd_gbs=wl["fwd_bytes"] / f_ms / 1e6, bwd_ms=b_ms,
                              bwd_gbs=wl["bwd_bytes"] / b_ms / 1e6)
 
+    if args.mode in ("all", "memupd"):
+        mu = setup_memupd(dev)
+        ms = timed(mu["launch"], K, W, stream)
+        out["memupd"] = dict(ms=ms, gbs=mu["bytes"] / ms / 1e6, params=mu["params"])
+        del mu
+    # whole-model forwards: a few steps keep the timed region to seconds
+    k5, w5 = max(2, min(K, 10)), max(1, min(W, 3))
+    for key, ttm in (("mac", False), ("mac_ttm", True)):
+        if args.mode in ("all", key):
+            wl = setup_mac(dev, ttm)
+            ms = timed(wl["launch"], k5, w5, stream)
+            out[key] = dict(ms=ms, tokens_per_s=wl["tokens"] / ms * 1e3, steps=k5)
+            del wl
+            torch.cuda.empty_cache()
+
     if args.mode != "all":
         print(json.dumps({"mode": args.mode, **out}))
         return 0
@@ -550,6 +631,13 @@ def main() -> int:
             "rmsnorm_fwd_hbm_gbs_compulsory": round(out["norm"]["fwd_gbs"], 1),
             "rmsnorm_bwd_ms": round(out["norm"]["bwd_ms"], 5),
             "rmsnorm_bwd_hbm_gbs_compulsory": round(out["norm"]["bwd_gbs"], 1),
+            "titanmac_mac_fwd_cfg5_tokens_per_s": round(out["mac"]["tokens_per_s"], 1),
+            "titanmac_mac_fwd_cfg5_ms": round(out["mac"]["ms"], 3),
+            "titanmac_mac_fwd_cfg5_test_time_memory_tokens_per_s": round(
+                out["mac_ttm"]["tokens_per_s"], 1),
+            "titanmac_mac_fwd_cfg5_test_time_memory_ms": round(out["mac_ttm"]["ms"], 3),
+            "neural_memory_update_cfg5_ms": round(out["memupd"]["ms"], 5),
+            "neural_memory_update_cfg5_hbm_gbs_compulsory": round(out["memupd"]["gbs"], 1),
         },
     }
     if not args.no_cpu:

@@ -347,7 +347,7 @@ typedef enum {
 } tmac_mem_clip_mode;
 
 /* Bytes of device workspace tmac_mem_update needs for these tensor sizes
- * (8 bytes per workgroup of the launch; at most 16 KB). */
+ * (8 bytes per workgroup of the launch; at most 4 KB). */
 int tmac_mem_update_workspace(const int64_t* sizes, int n_tensors, size_t* ws_bytes);
 
 /* The Titans memory step over n_tensors (<= TMAC_MEM_MAX_TENSORS) parameter

@@ -57,11 +57,12 @@ def close_rel(got, want, tol, what=""):
 
 # ---------------------------------------------------------------- the HIP update step
 
-SIZES = [[4096, 64, 4096, 64], [1, 3, 5, 1000, 4097], [300000], [7] * 16]
+SIZES = [[4096, 64, 4096, 64], [1, 3, 5, 1000, 4097], [300000], [7] * 16,
+         [640 * 640, 640, 640 * 640, 640]]  # the last: several 4-element chunks per thread
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("sizes", SIZES, ids=["mlp2", "ragged", "large", "sixteen"])
+@pytest.mark.parametrize("sizes", SIZES, ids=["mlp2", "ragged", "large", "sixteen", "cfg5"])
 @pytest.mark.parametrize("mode,gain", [("memory", 0.001), ("memory", 1.0), ("kernel", 0.001),
                                        ("kernel", 1.0)])
 def test_mem_update_matches_oracle(dev, dtype, sizes, mode, gain):

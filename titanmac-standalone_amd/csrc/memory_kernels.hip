@@ -35,7 +35,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kMaxTensors = TMAC_MEM_MAX_TENSORS;
-constexpr int kMaxPartials = 2048;  // bounds the per-workgroup partial re-add
+constexpr int kMaxPartials = 512;  // workgroups (= partials) per launch at most: 2 per CU
 
 struct TensorTable {
   void* g[kMaxTensors];

@@ -135,10 +135,11 @@ class TitanMAC(nn.Module):
     # ------------------------------------------------------------------ MAC
 
     def _mac_segments(self, xs: torch.Tensor, persistent_row: Optional[torch.Tensor],
-                      n_seq: int) -> tuple:
-        """Blocks, memory loss and gated output for a batch of independent segments
-        xs [n·B, L, d] against a read-only memory. Returns (o [n·B, L, d], per-segment MSE
-        sums [n] in fp32, number of elements per segment)."""
+                      n_seq: int, acc: torch.Tensor) -> torch.Tensor:
+        """Blocks and gated output for a batch of independent segments xs [n·B, L, d]
+        (segment-major) against a read-only memory; adds each segment's memory loss
+        F.mse_loss(M(W_K y), W_V y) over its B sequences to ``acc`` in order, as the reference's
+        per-segment loop does. Returns o [n·B, L, d]."""
         nl = self.config.n_memory_tokens
         NB, L, d = xs.shape
         h = self.memory_proj(self.neural_memory.retrieve(xs.mean(dim=1, keepdim=True)))
@@ -148,10 +149,12 @@ class TitanMAC(nn.Module):
         y = self._blocks(torch.cat(parts, dim=1))
         ys = y[:, y.shape[1] - L:]
         nm = self.neural_memory
-        err = (nm.memory_mlp(nm.W_K(ys)) - nm.W_V(ys)).float().pow(2)
-        sums = err.reshape(n_seq, -1).sum(dim=1)
+        pred, target = nm.memory_mlp(nm.W_K(ys)), nm.W_V(ys)
+        B = NB // n_seq
+        for s in range(n_seq):
+            acc.add_(F.mse_loss(pred[s * B:(s + 1) * B], target[s * B:(s + 1) * B]))
         gate = torch.sigmoid(self.gate_proj(nm.retrieve(ys)))
-        return ys * gate, sums, err[0].numel() * (NB // n_seq)
+        return ys * gate
 
     def forward_mac(self, input_ids: torch.Tensor, labels: Optional[torch.Tensor] = None,
                     attention_mask: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
@@ -170,18 +173,15 @@ class TitanMAC(nn.Module):
             # Read-only memory: all full segments in one batch, the remainder in another.
             n_full, tail = divmod(T, seg)
             prow = None if persistent is None else self.persistent_tokens
-            outs, total = [], torch.zeros((), dtype=torch.float32, device=x.device)
+            outs, acc = [], torch.zeros(1, device=x.device, dtype=x.dtype)
             if n_full:
                 xs = x[:, :n_full * seg].reshape(B, n_full, seg, -1).transpose(0, 1)
-                o, sums, cnt = self._mac_segments(xs.reshape(n_full * B, seg, -1), prow, n_full)
+                o = self._mac_segments(xs.reshape(n_full * B, seg, -1), prow, n_full, acc)
                 outs.append(o.reshape(n_full, B, seg, -1).transpose(0, 1).reshape(B, n_full * seg, -1))
-                total = total + (sums / cnt).sum()
             if tail:
-                o, sums, cnt = self._mac_segments(x[:, n_full * seg:], prow, 1)
-                outs.append(o)
-                total = total + (sums / cnt).sum()
+                outs.append(self._mac_segments(x[:, n_full * seg:], prow, 1, acc))
             o = outs[0] if len(outs) == 1 else torch.cat(outs, dim=1)
-            memory_loss = (total / n_segments).to(x.dtype)
+            memory_loss = (acc / n_segments).squeeze()
         else:
             o = torch.empty_like(x)
             acc = torch.zeros(1, device=x.device, dtype=x.dtype)
