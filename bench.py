@@ -7,6 +7,8 @@ headline `value` is the Block-ELL SpMM forward of BASELINE config 2 (X [8192,
 2560] bf16 · W [2560, 10240] Block-ELL, 64x64 blocks, 40 of 160 block-columns
 per block-row), in effective TFLOP/s (multiply-adds on stored blocks only).
 The same run also times, as secondary figures:
+  - the dense bf16 GEMM of the same layer (the reference's nn.Linear, hipBLASLt), for the
+    speed-up of the Block-ELL forward over it;
   - windowed attention forward of config 3 (B=8, H=10, S=4096, dh=64, w=512,
     Np=16, bf16) in tokens/s, against the dense masked SDPA and the dense
     bmm -> softmax -> bmm path on the same GPU (the faster one is the
@@ -440,6 +442,21 @@ def dense_attention_baseline(att, steps: int, warmup: int, stream):
     return res
 
 
+def dense_gemm_baseline(spmm, dev, steps: int, stream) -> float:
+    """ms of the dense bf16 GEMM the reference's MLP runs for the same layer (nn.Linear:
+    X[8192, 2560] @ W[2560, 10240] with the zero blocks stored), hipBLASLt through torch."""
+    sys.path.insert(0, str(ROOT))
+    c = CFG2
+    W = torch.zeros(BS * c["n_brow"], BS * c["n_bcol"], dtype=torch.bfloat16)
+    ci = spmm["pat"].col_idx
+    for r in range(c["n_brow"]):
+        for s_, col in enumerate(ci[r].tolist()):
+            W[BS * r:BS * r + BS, BS * col:BS * col + BS] = spmm["V_cpu"][r, s_]
+    X, Wd = spmm["X_cpu"].to(dev), W.to(dev)
+    Y = torch.empty(X.shape[0], Wd.shape[1], dtype=torch.bfloat16, device=dev)
+    return timed(lambda: torch.mm(X, Wd, out=Y), max(2, steps // 2), 3, stream)
+
+
 def cpu_baseline(spmm) -> dict:
     """The oracle's dense restatement (fp32 numpy X @ to_dense(W)) on the host cores."""
     sys.path.insert(0, str(ROOT))
@@ -519,6 +536,8 @@ def main() -> int:
         ms = timed(spmm["launch"], K, W, stream)
         out["spmm"] = dict(ms=ms, tflops=spmm["flops"] / ms / 1e9, flops=spmm["flops"],
                            bytes=spmm["bytes"])
+        if args.mode == "all":
+            out["spmm"]["dense_ms"] = dense_gemm_baseline(spmm, dev, K, stream)
     if args.mode in ("all", "attn", "attn_bwd"):
         att = setup_attn(dev)
     if args.mode in ("all", "attn"):
@@ -602,6 +621,8 @@ def main() -> int:
                      "unit": "TFLOP/s", "frac": round(s["tflops"] / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic},
         "secondary": {
+            "dense_bf16_gemm_same_layer_ms": round(s["dense_ms"], 4),
+            "spmm_speedup_vs_dense_gemm": round(s["dense_ms"] / s["ms"], 2),
             "windowed_attn_fwd_tokens_per_s": round(a["tokens_per_s"], 1),
             "windowed_attn_fwd_ms": round(a["ms"], 5),
             "windowed_attn_fwd_tflops_algorithmic": round(a["tflops"], 3),

@@ -217,9 +217,15 @@ def ce_loss(logits: np.ndarray, labels: np.ndarray) -> float:
     return float(np.mean(lse - lg[np.arange(len(lb)), lb]))
 
 
-def forward(p: Params, cfg: dict, ids: np.ndarray, update: bool = False):
+def forward(p: Params, cfg: dict, ids: np.ndarray, update: bool = False, record=None,
+            replay=None):
     """TitanMAC.forward dispatch (models/titanmac.py:554-686). Returns (logits, memory_loss,
-    memory) with memory the NeuralMemory after the call (None without neural memory)."""
+    memory) with memory the NeuralMemory after the call (None without neural memory).
+
+    Retrieval is M*(q), a stop-gradient read (memory/neural_memory.py:474-477). For finite
+    differences that must match autograd, pass ``record=[]`` on the unperturbed call to
+    collect every retrieval output in order, and ``replay=`` that list on the perturbed calls
+    to reuse them (the read treated as a constant)."""
     ids = np.asarray(ids)
     B, T = ids.shape
     Np = cfg["n_persistent"]
@@ -230,6 +236,16 @@ def forward(p: Params, cfg: dict, ids: np.ndarray, update: bool = False):
         y = _layers_forward(x, p, cfg)
         return _head(p, y, cfg)[:, Np:], None, None
     mem = NeuralMemory(_sub(p, "neural_memory."), cfg.get("memory_theta_lr", 0.01))
+    if record is not None or replay is not None:
+        read, it = mem.retrieve, iter(replay) if replay is not None else None
+
+        def retrieve(x):
+            if it is not None:
+                return next(it)
+            out = read(x)
+            record.append(out)
+            return out
+        mem.retrieve = retrieve
     variant = cfg.get("titans_variant", "MAC")
     step = mem.update if update else None
     x = _embed(p, ids)

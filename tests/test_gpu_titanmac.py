@@ -311,3 +311,80 @@ def test_titanmac_mac_training_step_runs_on_hip(dev):
     assert len(grads) > 10 and all(torch.isfinite(g).all() for g in grads)
     assert m.layers[0].attention.qkv_proj.weight.grad.abs().sum() > 0
     assert not torch.equal(before, m.neural_memory.memory_mlp.mlp[0].weight)
+
+
+# ---------------------------------------------------------------- training gradients
+
+def _flat_params(m):
+    return [(n, p) for n, p in m.named_parameters()]
+
+
+def _directional_check(dev, m, cfg, ids, groups, seed):
+    """⟨∇L, u⟩ from GPU autograd (fp32) against a central difference of the fp64 oracle
+    along u, for each parameter group; L = CE (+ memory loss). Retrieval outputs are frozen
+    in the oracle (the reference reads the memory under no_grad)."""
+    m.zero_grad()
+    out = m(ids.to(dev), labels=ids.to(dev))
+    out["loss"].backward()
+    base = {k: v.detach().double().cpu().numpy() for k, v in m.state_dict().items()}
+    tied = m.lm_head.weight is m.embed_tokens.weight
+    mem_on = cfg.get("use_neural_memory", False)
+    rec = [] if mem_on else None
+    logits0, ml0, _ = ot.forward(base, cfg, ids.numpy(), record=rec)
+    L0 = ot.ce_loss(logits0, ids.numpy()) + (ml0 if mem_on else 0.0)
+    assert abs(out["loss"].item() - L0) <= 1e-4 * abs(L0)
+    g = torch.Generator().manual_seed(seed)
+    for gname, pick_fn in groups.items():
+        dirs, dot = {}, 0.0
+        for n, prm in _flat_params(m):
+            if not pick_fn(n):
+                continue
+            u = torch.randn(prm.shape, generator=g, dtype=torch.float64)
+            u *= float(prm.detach().double().pow(2).mean().sqrt()) + 1e-2
+            dirs[n] = u.numpy()
+            if prm.grad is not None:
+                dot += float((prm.grad.double().cpu() * u).sum())
+        eps = 1e-5
+        vals = []
+        for sgn in (1.0, -1.0):
+            pp = dict(base)
+            for n, u in dirs.items():
+                pp[n] = base[n] + sgn * eps * u
+            if tied and "embed_tokens.weight" in dirs:
+                pp["lm_head.weight"] = pp["embed_tokens.weight"]
+            lg, ml, _ = ot.forward(pp, cfg, ids.numpy(), replay=rec)
+            vals.append(ot.ce_loss(lg, ids.numpy()) + (ml if mem_on else 0.0))
+        fd = (vals[0] - vals[1]) / (2 * eps)
+        assert abs(dot - fd) <= 2e-3 * max(abs(fd), 1e-3), (gname, dot, fd)
+
+
+GROUPS = {
+    "all": lambda n: True,
+    "blocks": lambda n: n.startswith("layers."),
+    "attention": lambda n: ".attention." in n,
+    "embeddings": lambda n: n.startswith(("embed_", "persistent", "norm.")),
+}
+
+
+def test_titanmac_plain_training_gradients_match_oracle(dev):
+    """The plain forward (no neural memory) in training mode: every parameter's gradient,
+    through embeddings, persistent tokens, block-sparse attention with its convs, RMSNorms,
+    MLPs and the tied head, pinned by directional derivatives of the fp64 oracle."""
+    m = _model(dev, use_neural_memory=False)
+    m.train()
+    cfg = dict(MAC_CFG, use_neural_memory=False)
+    ids = torch.from_numpy(GOLD["input_ids"][:, :70])
+    _directional_check(dev, m, cfg, ids, GROUPS, seed=31)
+
+
+@pytest.mark.parametrize("bsa", [True, False])
+def test_titanmac_mac_gradients_match_oracle(dev, bsa):
+    """MAC with a read-only memory (eval, gradients on: the batched-segment path), loss =
+    CE + memory loss: gradients of blocks, embeddings and the memory's W_K / W_V / MLP /
+    projections, pinned by directional derivatives of the fp64 oracle."""
+    m = _model(dev, "MAC", bsa, False)
+    cfg = dict(MAC_CFG, use_block_sparse=bsa)
+    ids = torch.from_numpy(GOLD["input_ids"])
+    groups = dict(GROUPS, memory=lambda n: n.startswith(("neural_memory.", "memory_proj.",
+                                                          "gate_proj.")))
+    _directional_check(dev, m, cfg, ids, groups, seed=32 + bsa)
