@@ -388,3 +388,45 @@ def test_titanmac_mac_gradients_match_oracle(dev, bsa):
     groups = dict(GROUPS, memory=lambda n: n.startswith(("neural_memory.", "memory_proj.",
                                                           "gate_proj.")))
     _directional_check(dev, m, cfg, ids, groups, seed=32 + bsa)
+
+
+@pytest.mark.parametrize("variant,dtype", [("MAG", torch.bfloat16), ("MAL", torch.bfloat16),
+                                           ("MAC", torch.float16)])
+def test_titanmac_16bit_variants_match_oracle(dev, variant, dtype):
+    """MAG / MAL in bf16 and MAC in fp16, block-sparse attention, Block-ELL MLP, read-only
+    memory, against the fp64 oracle on the same 16-bit weights (the 16-bit bar)."""
+    torch.manual_seed(13)
+    cfg = tc.TitanMACConfig(vocab_size=97, d_model=128, n_heads=2, n_layers=2, d_ff=256,
+                            max_seq_len=256, window_size=64, n_persistent=4, use_neural_memory=True,
+                            titans_variant=variant, segment_size=64, n_memory_tokens=8,
+                            mlp_block_ell=True, mlp_density=0.5)
+    m = tc.TitanMAC(cfg).to(dev, dtype).eval()
+    ids = torch.randint(0, 97, (2, 130), generator=torch.Generator().manual_seed(14))
+    with torch.no_grad():
+        out = m(ids.to(dev))
+    want, wloss, _ = ot.forward(_oracle_params(m), dict(
+        vocab_size=97, d_model=128, n_heads=2, n_layers=2, window_size=64, n_persistent=4,
+        use_neural_memory=True, titans_variant=variant, segment_size=64, n_memory_tokens=8,
+        block_size=64), ids.numpy(), update=False)
+    got = out["logits"].float().cpu().numpy()
+    assert out["logits"].dtype == dtype and got.shape == want.shape
+    sc = max(1.0, np.abs(want).max())
+    err = np.abs(got / sc - want / sc)
+    assert (err <= 2e-2 + 2e-2 * np.abs(want / sc)).all(), err.max()
+    assert abs(out["memory_loss"].float().item() - wloss) <= 5e-2 * abs(wloss)
+
+
+def test_gradient_checkpointing_gives_identical_gradients(dev):
+    """enable_gradient_checkpointing recomputes each block in the backward; with deterministic
+    kernels the gradients are bit-identical to the stored-activation run."""
+    grads = []
+    for ckpt in (False, True):
+        m = _model(dev, use_neural_memory=False).train()
+        if ckpt:
+            m.enable_gradient_checkpointing()
+        ids = torch.from_numpy(GOLD["input_ids"]).to(dev)
+        m(ids, labels=ids)["loss"].backward()
+        grads.append({n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None})
+    assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 10
+    for n in grads[0]:
+        assert torch.equal(grads[0][n], grads[1][n]), n
