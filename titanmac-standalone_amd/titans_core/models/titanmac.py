@@ -180,8 +180,8 @@ class TitanMAC(nn.Module):
                 outs.append(o.reshape(n_full, B, seg, -1).transpose(0, 1).reshape(B, n_full * seg, -1))
             if tail:
                 outs.append(self._mac_segments(x[:, n_full * seg:], prow, 1, acc))
-            o = outs[0] if len(outs) == 1 else torch.cat(outs, dim=1)
-            memory_loss = (acc / n_segments).squeeze()
+            o = x if not outs else (outs[0] if len(outs) == 1 else torch.cat(outs, dim=1))
+            memory_loss = (acc / n_segments).squeeze()  # nan for T = 0, as in the reference
         else:
             o = torch.empty_like(x)
             acc = torch.zeros(1, device=x.device, dtype=x.dtype)
