@@ -111,7 +111,8 @@ def clip_momentum_update(g: np.ndarray, S: np.ndarray, W: np.ndarray, alpha: flo
     norm = float(np.sqrt(np.sum(g * g)))
     if mode == "memory":
         scale = max_norm / norm if norm > max_norm else 1.0
-        gs = g * scale
+        with np.errstate(invalid="ignore"):  # inf * 0 -> nan marks the skip, as in torch
+            gs = g * scale
         if not np.all(np.isfinite(gs)):
             return np.array(S, np.float64), np.array(W, np.float64), gs, norm, True
     else:
