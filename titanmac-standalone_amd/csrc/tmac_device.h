@@ -80,6 +80,20 @@ struct Mfma<TMAC_F16> {
   }
 };
 
+// x combined with the value of lane (lane ^ 32), identical in both lanes: one
+// v_permlane32_swap of x with itself puts x[l] and x[l ^ 32] in the two results
+// (in an order that depends on the half), and max and + are commutative.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_add(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Eight 16-bit values of column (c0 + lane%16 of the 16-lane group) from rows
 // r0..r0+7 of a row-major LDS tile with pitch kPitch, as one MFMA operand:
 // two transpose reads, rows r0..r0+3 then r0+4..r0+7. The caller passes the

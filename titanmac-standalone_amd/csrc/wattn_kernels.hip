@@ -55,8 +55,9 @@ struct Tile {
   static constexpr int kDt = D / 32;      // 32-wide head-dimension tiles of an output
 };
 
+// Four workgroups per CU at D <= 64 (at most 128 VGPRs, 36 KB of LDS each), two at D = 128.
 template <int DT, int D>
-__global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
@@ -73,7 +74,8 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
   const int S = mp.S;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  // The wave index is uniform; saying so keeps the tile kinds and their branches scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int q_row = qb * 128 + wave * 32 + l32;  // this lane's query row
@@ -171,12 +173,16 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
       // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
       // scores; scale_log2 > 0, so the row maximum commutes with the scaling).
       if (kind == 2) {
+        // key - (kt*64 + 4h) is a constant per element, so the span bounds move
+        // to this lane's origin and each test compares a constant with them.
+        const int base = kt * 64 + 4 * h;
+        const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-            st[kh][j] = span_has(span, key) ? st[kh][j] : -INFINITY;
+            const int off = 32 * kh + 8 * (j >> 2) + (j & 3);
+            st[kh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? st[kh][j] : -INFINITY;
           }
       }
       float mx = -INFINITY;
@@ -184,7 +190,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kh][j]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+      mx = xor32_max(mx) * scale_log2;
       const bool move = mx > m_ref + kTau;  // false while the row is fully masked
       if (__builtin_amdgcn_ballot_w64(move)) {
         // lanes that keep their reference scale by 1 (also when it is still -inf)
@@ -196,30 +202,26 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_mfma_kernel(
         m_ref = m_new;
       }
       const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-      float rs = 0.f;
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float pj = __builtin_amdgcn_exp2f(fmaf(st[kh][j], scale_log2, -m_use));
-          st[kh][j] = pj;
-          rs += pj;
-        }
-      rs += __shfl_xor(rs, 32);
-      l_run += rs;
 
       // Pᵀ as the B operand, 16 keys per MFMA: k-step ks covers keys
-      // 16ks..16ks+15 and lane t-th value is key 16ks + 8(t/4) + 4h + t%4.
+      // 16ks..16ks+15 and lane t-th value is key 16ks + 8(t/4) + 4h + t%4. The
+      // row sum stays in fp32, in four chains.
       u32x4 pb[4];
+      float r4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int kh = ks >> 1, j0 = 8 * (ks & 1);
         uint32_t w[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
-          w[t] = Mfma<DT>::pack2(st[kh][j0 + 2 * t], st[kh][j0 + 2 * t + 1]);
+        for (int t = 0; t < 4; ++t) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t], scale_log2, -m_use));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t + 1], scale_log2, -m_use));
+          w[t] = Mfma<DT>::pack2(p0, p1);
+          r4[t] += p0 + p1;
+        }
         pb[ks] = u32x4{w[0], w[1], w[2], w[3]};
       }
+      l_run += xor32_add((r4[0] + r4[1]) + (r4[2] + r4[3]));
       // Vᵀ as the A operand in the same key order: rows 16ks + 4h + 0..3, then
       // 16ks + 8 + 4h + 0..3 of the V tile, column dh = 32dt + lane%32.
 #pragma unroll
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
   const int S = mp.S;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // uniform
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int key = kb * 128 + wave * 32 + l32;  // this lane's key
@@ -541,12 +543,16 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
           s = Mfma<DT>::run(qa, kf[kk], s);
           dp = Mfma<DT>::run(ga, vf[kk], dp);
         }
-        // s[j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4.
+        // s[j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4. The
+        // span bounds move to this lane's origin (qt*64 + 32qh + 4h), so each
+        // test compares a per-element constant with them.
         if (kind == 2) {
+          const int base = qt * 64 + 32 * qh + 4 * h;
+          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int ql = 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
-            s[j] = span_has(span, qt * 64 + ql) ? s[j] : -INFINITY;
+            const int off = 8 * (j >> 2) + (j & 3);
+            s[j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[j] : -INFINITY;
           }
         }
         // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e and Δ as one 16-byte read each
@@ -613,7 +619,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
   const int S = mp.S;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // uniform
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
   const int q_row = qb * 128 + wave * 32 + l32;
@@ -704,14 +710,17 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
           dp[kh] = Mfma<DT>::run(va, gf[kk], dp[kh]);
         }
       }
-      // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4.
+      // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4; the
+      // span bounds move to this lane's origin (kt*64 + 4h).
       if (kind == 2) {
+        const int base = kt * 64 + 4 * h;
+        const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
-            const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-            s[kh][j] = span_has(span, key) ? s[kh][j] : -INFINITY;
+            const int off = 32 * kh + 8 * (j >> 2) + (j & 3);
+            s[kh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[kh][j] : -INFINITY;
           }
       }
 #pragma unroll
