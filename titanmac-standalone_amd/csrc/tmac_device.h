@@ -300,7 +300,22 @@ static __global__ __launch_bounds__(256) void column_sum_kernel(const float* __r
 }
 
 __device__ __forceinline__ float gelu_erf(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+  // erf by Abramowitz & Stegun, Handbook of Mathematical Functions, formula 7.1.26
+  // (Hastings' approximation, |error| <= 1.5e-7 on erf):
+  //   erf(z) = 1 - t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) exp(-z^2), t = 1 / (1 + p z),
+  // for z >= 0, odd in z. Over |x| <= 12 the GELU it gives is within 5e-7 of the
+  // exact one (absolute), far below the 16-bit rounding of the outputs it feeds,
+  // at about a dozen instructions with one reciprocal and one exp2.
+  const float z = x * 0.70710678118654752440f;
+  const float az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, az, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f) * t;
+  const float e = __builtin_amdgcn_exp2f(-(az * az) * 1.4426950408889634f);
+  const float erf_z = copysignf(fmaf(-poly, e, 1.0f), z);
+  return 0.5f * x * (1.0f + erf_z);
 }
 
 }  // namespace tmac
