@@ -171,3 +171,23 @@ def test_cfg4_full_size_dx_sddmm(dev):
     want = ob.sddmm(X.float().numpy(), dY.float().numpy(), pat.col_idx, dtype=np.float32)
     scale = np.abs(want).max()
     close(dV, want, atol=2e-5 * scale, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fused_gelu_over_its_range(dev, dtype):
+    """The fused epilogue's GELU (erf by Abramowitz & Stegun 7.1.26) against the exact erf
+    GELU over [-12, 12], tails included: zero weight blocks, so each output is GELU(bias)."""
+    n_bcol = 64
+    ci = np.arange(n_bcol, dtype=np.int32).reshape(1, n_bcol)  # one block-row, dense
+    pat = kb.BlockELLPattern(ci, n_bcol)
+    N = 64 * n_bcol
+    b = torch.linspace(-12.0, 12.0, N).to(dtype)
+    X = torch.ones(3, 64, dtype=dtype)
+    V = torch.zeros(1, n_bcol, 64, 64, dtype=dtype)
+    with torch.no_grad():
+        y = kb.block_ell_mm(X.to(dev), V.to(dev), pat, b.to(dev), activation="gelu").float().cpu().numpy()
+    want = ob.gelu_erf(b.float().numpy().astype(np.float64))
+    # one 16-bit rounding of the output: half an ulp relative, plus the tiny values near zero
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    err = np.abs(y - want[None, :])
+    assert (err <= eps * np.abs(want)[None, :] + 1e-6).all(), err.max()
