@@ -191,3 +191,49 @@ def test_fused_gelu_over_its_range(dev, dtype):
     eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
     err = np.abs(y - want[None, :])
     assert (err <= eps * np.abs(want)[None, :] + 1e-6).all(), err.max()
+
+
+def test_row_pitch_inputs_and_padded_outputs(dev):
+    """Leading dimensions larger than the feature count. Inputs given as column slices of
+    wider buffers reach the kernels as they are (row pitch > K or N), and through the C ABI
+    Y and dX are written into column slices of wider buffers whose other columns keep their
+    sentinel. Every result equals the contiguous call's bit for bit."""
+    from titans_core.kernels import _lib
+    M, n_brow, n_bcol, width = 300, 4, 6, 3
+    K, N = 64 * n_brow, 64 * n_bcol
+    pat, X, V, dY, b = data(M, n_brow, n_bcol, width, torch.bfloat16, seed=21)
+    idx = pat.device_index(dev)
+    Xd, Vd, dYd, bd = (t.to(dev) for t in (X, V, dY, b))
+    Xw = torch.zeros(M, K + 40, dtype=torch.bfloat16, device=dev)  # pitch 296: 8 columns either side
+    Xw[:, 8:8 + K] = Xd
+    dYw = torch.zeros(M, N + 24, dtype=torch.bfloat16, device=dev)  # pitch 408
+    dYw[:, 16:16 + N] = dYd
+    Xs, dYs = Xw[:, 8:8 + K], dYw[:, 16:16 + N]
+    assert Xs.stride(0) == K + 40 and not Xs.is_contiguous()
+
+    y = kb.block_ell_mm(Xd, Vd, pat, bd, activation="gelu")
+    dx = kb.bell_dx(dYd, Vd, idx["col_idx"], n_bcol)
+    dv = kb.bell_sddmm(Xd, dYd, idx["col_idx"], n_brow, width, torch.float32)
+    assert torch.equal(kb.block_ell_mm(Xs, Vd, pat, bd, activation="gelu"), y)
+    assert torch.equal(kb.bell_dx(dYs, Vd, idx["col_idx"], n_bcol), dx)
+    assert torch.equal(kb.bell_sddmm(Xs, dYs, idx["col_idx"], n_brow, width, torch.float32), dv)
+
+    L = _lib.lib()
+    sentinel = -7.0
+    Yw = torch.full((M, N + 16), sentinel, dtype=torch.bfloat16, device=dev)  # Y at columns 8 .. 8+N
+    dXw = torch.full((M, K + 32), sentinel, dtype=torch.bfloat16, device=dev)  # dX at columns 16 .. 16+K
+    with torch.cuda.device(dev):
+        rc = L.tmac_bell_fwd(_lib.ptr(Xs), K + 40, _lib.ptr(Vd), _lib.ptr(idx["t_ptr"]),
+                             _lib.ptr(idx["t_row"]), _lib.ptr(idx["t_vblk"]), _lib.ptr(idx["order"]),
+                             _lib.ptr(bd), _lib.ptr(Yw[:, 8:]), N + 16, M, n_brow, n_bcol, width,
+                             _lib.BF16, _lib.EPI_GELU, _lib.stream_ptr(dev))
+        assert rc == 0, _lib.lib().tmac_status_string(rc)
+        rc = L.tmac_bell_dx(_lib.ptr(dYs), N + 24, _lib.ptr(Vd), _lib.ptr(idx["col_idx"]),
+                            _lib.ptr(dXw[:, 16:]), K + 32, M, n_brow, n_bcol, width, _lib.BF16,
+                            _lib.stream_ptr(dev))
+        assert rc == 0, _lib.lib().tmac_status_string(rc)
+    torch.cuda.synchronize()
+    assert torch.equal(Yw[:, 8:8 + N], y)
+    assert (Yw[:, :8] == sentinel).all() and (Yw[:, 8 + N:] == sentinel).all()
+    assert torch.equal(dXw[:, 16:16 + K], dx)
+    assert (dXw[:, :16] == sentinel).all() and (dXw[:, 16 + K:] == sentinel).all()

@@ -21,7 +21,7 @@ the transpose of the matching nn.Linear weight block.
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import numpy as np
 import torch
@@ -107,6 +107,21 @@ class BlockELLPattern:
 # torch.library ops
 # ---------------------------------------------------------------------------
 
+def _rows(t: torch.Tensor, features: int) -> Tuple[torch.Tensor, int]:
+    """t as [M, features] rows and their pitch in elements. A row-strided view (a
+    column slice of a wider buffer: unit column stride, pitch a multiple of 8
+    elements, 16-byte aligned start) goes to the kernels as it is; anything else
+    is made contiguous first."""
+    t2 = t.reshape(-1, features)
+    if t2.shape[0] > 0:
+        pitch = t2.stride(0)
+        if ((t2.stride(1) == 1 or features == 1) and pitch >= features and pitch % 8 == 0
+                and t2.data_ptr() % 16 == 0):
+            return t2, pitch
+    t2 = t2.contiguous()
+    return t2, features
+
+
 def _check_values(values: torch.Tensor, what: str) -> None:
     if values.dim() != 4 or values.shape[2:] != (BLOCK, BLOCK):
         raise ValueError(f"{what}: values must be [n_brow, width, 64, 64], got {tuple(values.shape)}")
@@ -128,9 +143,7 @@ def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr
     if x.dtype != values.dtype:
         raise TypeError(f"bell_fwd: x dtype {x.dtype} != values dtype {values.dtype}")
     dev = _lib.require_device(x, values, t_ptr, what="bell_fwd")
-    x2 = x.reshape(-1, K)
-    if not x2.is_contiguous():
-        x2 = x2.contiguous()
+    x2, ldx = _rows(x, K)
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
@@ -140,7 +153,7 @@ def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr
             bias = bias.contiguous()
         with torch.cuda.device(dev):
             rc = _lib.lib().tmac_bell_fwd(
-                _lib.ptr(x2), K, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
+                _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
                 _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, M, n_brow,
                 n_bcol, width, _lib.dtype_code(x.dtype), _lib.EPI_GELU if gelu else _lib.EPI_NONE,
                 _lib.stream_ptr(dev))
@@ -163,17 +176,15 @@ def bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bco
     if dy.shape[-1] != N:
         raise ValueError(f"bell_dx: dy has {dy.shape[-1]} features, W has {N} columns")
     dev = _lib.require_device(dy, values, col_idx, what="bell_dx")
-    dy2 = dy.reshape(-1, N)
-    if not dy2.is_contiguous():
-        dy2 = dy2.contiguous()
-    if dy2.dtype != values.dtype:
-        dy2 = dy2.to(values.dtype)
+    if dy.dtype != values.dtype:
+        dy = dy.to(values.dtype)
+    dy2, lddy = _rows(dy, N)
     M = dy2.shape[0]
     dx = torch.empty((M, K), dtype=values.dtype, device=dev)
     if M > 0:
         with torch.cuda.device(dev):
             rc = _lib.lib().tmac_bell_dx(
-                _lib.ptr(dy2), N, _lib.ptr(values.contiguous()), _lib.ptr(col_idx), _lib.ptr(dx), K,
+                _lib.ptr(dy2), lddy, _lib.ptr(values.contiguous()), _lib.ptr(col_idx), _lib.ptr(dx), K,
                 M, n_brow, n_bcol, width, _lib.dtype_code(values.dtype), _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_bell_dx")
     return dx.reshape(*dy.shape[:-1], K)
@@ -196,10 +207,10 @@ def bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow:
     if N % BLOCK:
         raise ValueError(f"bell_sddmm: dy features {N} not a multiple of 64")
     n_bcol = N // BLOCK
-    x2 = x.reshape(-1, K).contiguous()
-    dy2 = dy.reshape(-1, N).contiguous()
-    if dy2.dtype != x2.dtype:
-        dy2 = dy2.to(x2.dtype)
+    if dy.dtype != x.dtype:
+        dy = dy.to(x.dtype)
+    x2, ldx = _rows(x, K)
+    dy2, lddy = _rows(dy, N)
     if x2.shape[0] != dy2.shape[0]:
         raise ValueError("bell_sddmm: x and dy have different row counts")
     M = x2.shape[0]
@@ -210,7 +221,7 @@ def bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow:
     ws_bytes = _sddmm_workspace_bytes(L, M, n_brow, n_bcol, width)
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
     with torch.cuda.device(dev):
-        rc = L.tmac_bell_sddmm(_lib.ptr(x2), K, _lib.ptr(dy2), N, _lib.ptr(col_idx), _lib.ptr(out),
+        rc = L.tmac_bell_sddmm(_lib.ptr(x2), ldx, _lib.ptr(dy2), lddy, _lib.ptr(col_idx), _lib.ptr(out),
                                _lib.dtype_code(out_dtype), _lib.ptr(ws), ws.numel() * 4, M, n_brow,
                                n_bcol, width, _lib.dtype_code(x2.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_bell_sddmm")
