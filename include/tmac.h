@@ -107,7 +107,8 @@ int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int wi
  * epi = TMAC_EPI_GELU, also the erf GELU between them (blocks/mlp.py:42,61).
  * X, Y row-major with leading dimensions ldx, ldy; bias (nullable) has N
  * entries of the same dtype. dtype: TMAC_BF16 or TMAC_F16.
- * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary.
+ * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary (M <= 64 runs a few-row
+ * kernel that splits each block-column's list over four waves).
  * t_ptr/t_row/t_vblk/order: device copies of tmac_bell_transpose's output. */
 int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
                   const int32_t* d_t_ptr, const int32_t* d_t_row,

@@ -37,7 +37,9 @@ def data(M, n_brow, n_bcol, width, dtype, seed, vscale=0.05):
 SHAPES = [  # M, n_brow, n_bcol, width
     (1, 1, 1, 1), (37, 2, 3, 1), (256, 3, 5, 2), (300, 4, 6, 6), (513, 10, 40, 20), (1000, 5, 7, 3),
     # lists longer than 64 entries (forward: 70 block-rows per column; dX: width 100)
-    (300, 70, 3, 3), (260, 3, 130, 100)]
+    (300, 70, 3, 3), (260, 3, 130, 100),
+    # at most 64 rows: the forward's few-row kernel (four waves splitting each list)
+    (17, 5, 7, 3), (33, 10, 40, 20), (64, 70, 3, 3), (64, 9, 12, 1)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -62,12 +64,13 @@ def test_fwd_dx_sddmm_parity(dev, dtype, M, n_brow, n_bcol, width):
     close(dv.cpu(), want, atol=1e-4 * max(1.0, np.abs(want).max()), rtol=1e-4)
 
 
-def test_empty_columns_get_bias_only(dev):
+@pytest.mark.parametrize("M", [70, 20])
+def test_empty_columns_get_bias_only(dev, M):
     # width 1 of 8: most block-columns have no stored block; Y there is bias (then GELU).
     ci = np.array([[3], [3]], dtype=np.int32)
     pat = kb.BlockELLPattern(ci, 8)
     g = torch.Generator().manual_seed(1)
-    X = torch.randn(70, 128, generator=g).to(torch.bfloat16)
+    X = torch.randn(M, 128, generator=g).to(torch.bfloat16)
     V = (torch.randn(2, 1, 64, 64, generator=g) * 0.1).to(torch.bfloat16)
     b = torch.randn(512, generator=g).to(torch.bfloat16)
     y = kb.block_ell_mm(X.to(dev), V.to(dev), pat, b.to(dev), activation="gelu").float().cpu()
@@ -75,8 +78,9 @@ def test_empty_columns_get_bias_only(dev):
     close(y, ref)
 
 
-def test_output_fully_written_and_deterministic(dev):
-    pat, X, V, dY, _ = data(777, 6, 9, 4, torch.bfloat16, seed=5)
+@pytest.mark.parametrize("M", [777, 50])
+def test_output_fully_written_and_deterministic(dev, M):
+    pat, X, V, dY, _ = data(M, 6, 9, 4, torch.bfloat16, seed=5)
     Xd, Vd, dYd = X.to(dev), V.to(dev), dY.to(dev)
     idx = pat.device_index(dev)
     y1 = kb.block_ell_mm(Xd, Vd, pat)
@@ -193,13 +197,14 @@ def test_fused_gelu_over_its_range(dev, dtype):
     assert (err <= eps * np.abs(want)[None, :] + 1e-6).all(), err.max()
 
 
-def test_row_pitch_inputs_and_padded_outputs(dev):
+@pytest.mark.parametrize("M", [300, 40])
+def test_row_pitch_inputs_and_padded_outputs(dev, M):
     """Leading dimensions larger than the feature count. Inputs given as column slices of
     wider buffers reach the kernels as they are (row pitch > K or N), and through the C ABI
     Y and dX are written into column slices of wider buffers whose other columns keep their
     sentinel. Every result equals the contiguous call's bit for bit."""
     from titans_core.kernels import _lib
-    M, n_brow, n_bcol, width = 300, 4, 6, 3
+    n_brow, n_bcol, width = 4, 6, 3
     K, N = 64 * n_brow, 64 * n_bcol
     pat, X, V, dY, b = data(M, n_brow, n_bcol, width, torch.bfloat16, seed=21)
     idx = pat.device_index(dev)

@@ -29,6 +29,9 @@
 // activations (all output block-columns of a slab, longest list first): the
 // running workgroups of one XCD then share the slab in that XCD's L2.
 //
+// With at most 64 rows the forward runs bell_fwd_small_kernel instead: one
+// workgroup per block-column whose four waves split the column's list.
+//
 // SDDMM: a workgroup owns one block-row r, four of its slots (one per wave)
 // and a contiguous range of M. Per 64-row step it stages X[m, 64r:+64] and the
 // four dY[m, 64c:+64] tiles in LDS and reads both MFMA operands with transpose
@@ -289,6 +292,153 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   }
 }
 
+// Forward for few rows (M <= kSmallM: decoding, small batches). The gather GEMM
+// above gives such a call one 256-row tile per block-column and walks each list
+// one entry at a time, so it pays one memory latency per entry whatever M is.
+// Here one workgroup owns block-column c (all M <= 64 rows) and its four waves
+// split c's list: wave w takes entries w, w + 4, ..., each wave with two LDS
+// stages of its own (64-row activation tile + weight block, both swizzled as
+// above), so up to eight entries' copies are in flight per workgroup and the
+// waves never wait for each other. Each wave accumulates a full 64x64 partial
+// tile; the partials are added through LDS in wave order (deterministic), and
+// wave 0 runs the epilogue. Activation rows past M are clamped onto row M-1.
+constexpr int kSmallM = 64;
+
+template <int DT>
+__global__ __launch_bounds__(256) void bell_fwd_small_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
+    const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ t_row,
+    const int32_t* __restrict__ t_vblk, const uint16_t* __restrict__ bias, int epi,
+    uint16_t* __restrict__ Y, int64_t ldy, int M) {
+  // Per wave and stage: activation tile (64 x 64, xswz) then weight block
+  // (64 x 64, wswz). Separate arrays per stage, so the compiler can tell the
+  // copies into one stage from the reads of the other.
+  __shared__ __attribute__((aligned(16))) uint16_t st0[4][8192];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[4][8192];
+
+  const int ob = blockIdx.x;
+  const int e0 = t_ptr[ob], e1 = t_ptr[ob + 1];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int grp = (lane >> 4) & 1;
+  const int drow = lane >> 3, dpos = lane & 7;
+
+  // Copy addressing as in bell_gemm_kernel: lane L of the instruction for rows
+  // 8j..8j+7 fills chunk position L & 7 of row 8j + L / 8.
+  const uint16_t* xsrc[8];
+  int woff[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 8 * j + drow;
+    const int a = (row >> 1) & 7;
+    xsrc[j] = A + static_cast<int64_t>(min(row, M - 1)) * lda + 8 * (dpos ^ a);
+    woff[j] = row * 64 + 8 * (dpos ^ (((a & 1) << 2) | (a >> 1)));
+  }
+  auto dma_tiles = [&](int e, uint16_t* buf) {
+    const int64_t col = static_cast<int64_t>(t_row[e]) * 64;
+    const uint16_t* wsrc = vals + static_cast<int64_t>(t_vblk[e]) * 4096;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(xsrc[j] + col, buf + 8 * j * 64);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma16(wsrc + woff[j], buf + 4096 + 8 * j * 64);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
+  auto compute = [&](const uint16_t* buf) {
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      u32x4 xa[2], wf[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) xa[mi] = lds16(buf + xswz(32 * mi + l32, 2 * kk + h));
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) wf[ni] = lds_read_tr8_wswz(buf + 4096, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = Mfma<DT>::run(wf[ni], xa[mi], acc[mi][ni]);
+    }
+  };
+
+  // This wave's entries e0 + wave + 4i, two at a time: both copies are issued
+  // before either is computed.
+  uint16_t* b0 = st0[wave];
+  uint16_t* b1 = st1[wave];
+  for (int e = e0 + wave; e < e1; e += 8) {
+    const bool two = e + 4 < e1;
+    dma_tiles(e, b0);
+    if (two) dma_tiles(e + 4, b1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(b0);
+    if (two) compute(b1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // Partial tiles of waves 1..3 through LDS (fp32, lane-major: conflict-free),
+  // added to wave 0's in wave order.
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(&st0[0][0]);  // 3 x 64 x 64 floats = 48 KB
+  if (wave > 0) {
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          red[((wave - 1) * 64 + (mi * 2 + ni) * 16 + j) * 64 + lane] = acc[mi][ni][j];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[mi][ni][j] += red[(w * 64 + (mi * 2 + ni) * 16 + j) * 64 + lane];
+
+  // Epilogue as in bell_gemm_kernel, for wave 0's 64 rows (staging tile in
+  // stage-1 memory, which no wave touches any more).
+  uint16_t* stage = &st1[0][0];
+  const int64_t col0 = static_cast<int64_t>(ob) * 64;
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg) {
+        const int n_loc = 32 * ni + 8 * jg + 4 * h;
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) v[t] = acc[mi][ni][4 * jg + t];
+        if (bias) {
+          const u32x2 b2 = *reinterpret_cast<const u32x2*>(bias + col0 + n_loc);
+          v[0] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x & 0xffff));
+          v[1] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x >> 16));
+          v[2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
+          v[3] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y >> 16));
+        }
+        if (epi == TMAC_EPI_GELU) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) v[t] = gelu_erf(v[t]);
+        }
+        u32x2 packed;
+        packed.x = Mfma<DT>::pack2(v[0], v[1]);
+        packed.y = Mfma<DT>::pack2(v[2], v[3]);
+        *reinterpret_cast<u32x2*>(stage + (32 * mi + l32) * kPitch + n_loc) = packed;
+      }
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int row = it * 8 + (lane >> 3), ch = lane & 7;
+    if (row < M) stg16(Y + static_cast<int64_t>(row) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ dY, int64_t lddy,
@@ -471,6 +621,15 @@ extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
   const auto* V = static_cast<const uint16_t*>(d_vals);
   const auto* b = static_cast<const uint16_t*>(d_bias);
   auto* Y = static_cast<uint16_t*>(d_Y);
+  if (M <= kSmallM) {
+    if (dtype == TMAC_BF16)
+      hipLaunchKernelGGL((bell_fwd_small_kernel<TMAC_BF16>), dim3(n_bcol), dim3(256), 0, s, X, ldx, V,
+                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, M);
+    else
+      hipLaunchKernelGGL((bell_fwd_small_kernel<TMAC_F16>), dim3(n_bcol), dim3(256), 0, s, X, ldx, V,
+                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, M);
+    return launch_status();
+  }
   if (dtype == TMAC_BF16)
     hipLaunchKernelGGL((bell_gemm_kernel<TMAC_BF16, true>), dim3(8 * per_xcd), dim3(256), 0, s, X,
                        ldx, V, d_t_ptr, d_t_row, d_t_vblk, d_order, b, epi, Y, ldy, M, n_bcol, width,
