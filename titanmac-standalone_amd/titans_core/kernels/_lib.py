@@ -7,6 +7,7 @@ raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -119,13 +120,47 @@ def dtype_code(dtype: torch.dtype) -> int:
         raise TypeError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
 
 
-def stream_ptr(device: torch.device) -> ctypes.c_void_p:
-    """The raw hipStream_t of torch's current stream on `device`."""
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+def stream_ptr(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on `device` (the same
+    handle as torch.cuda.current_stream(device).cuda_stream, without building
+    a Stream object on every launch)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
-def ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
-    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+def ptr(t: torch.Tensor | None) -> int:
+    """Device address of t (0 for None), for a c_void_p argument."""
+    return 0 if t is None else t.data_ptr()
+
+
+_NO_GUARD = contextlib.nullcontext()
+
+
+def device_guard(device: torch.device):
+    """torch.cuda.device(device), or nothing when it is already the current device."""
+    if device.index is None or device.index == torch.cuda.current_device():
+        return _NO_GUARD
+    return torch.cuda.device(device)
+
+
+_PLAIN = (torch.Tensor, torch.nn.Parameter)
+
+
+def direct_call(*tensors: torch.Tensor | None) -> bool:
+    """Whether an op may run its implementation directly instead of through the
+    torch.library dispatcher: eager mode (no torch.compile tracing), plain
+    tensors (no fake or wrapper subclasses) and no autograd graph to record.
+    The dispatcher adds several µs of host time per call, more than many of
+    these kernels take on the GPU."""
+    if torch.compiler.is_compiling():
+        return False
+    grad = torch.is_grad_enabled()
+    for t in tensors:
+        if t is None:
+            continue
+        if type(t) not in _PLAIN or (grad and t.requires_grad):
+            return False
+    return True
 
 
 def require_device(*tensors: torch.Tensor, what: str) -> torch.device:

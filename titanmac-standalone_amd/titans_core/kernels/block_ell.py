@@ -129,10 +129,9 @@ def _check_values(values: torch.Tensor, what: str) -> None:
         raise TypeError(f"{what}: the MFMA kernels take bfloat16 or float16, got {values.dtype}")
 
 
-@torch.library.custom_op("titanmac::bell_fwd", mutates_args=())
-def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
-             t_row: torch.Tensor, t_vblk: torch.Tensor, order: torch.Tensor,
-             bias: Optional[torch.Tensor], gelu: bool) -> torch.Tensor:
+def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
+              t_row: torch.Tensor, t_vblk: torch.Tensor, order: torch.Tensor,
+              bias: Optional[torch.Tensor], gelu: bool) -> torch.Tensor:
     """y = (gelu)(x · W + bias) with W in Block-ELL; x [..., 64*n_brow] -> y [..., 64*n_bcol]."""
     _check_values(values, "bell_fwd")
     n_brow, width = int(values.shape[0]), int(values.shape[1])
@@ -151,7 +150,7 @@ def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr
             if bias.shape != (N,) or bias.dtype != x.dtype:
                 raise ValueError(f"bell_fwd: bias must be [{N}] of {x.dtype}")
             bias = bias.contiguous()
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = _lib.lib().tmac_bell_fwd(
                 _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
                 _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, M, n_brow,
@@ -161,14 +160,16 @@ def bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr
     return y.reshape(*x.shape[:-1], N)
 
 
+bell_fwd = torch.library.custom_op("titanmac::bell_fwd", mutates_args=())(_bell_fwd)
+
+
 @bell_fwd.register_fake
 def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu):
     n_bcol = t_ptr.shape[0] - 1
     return x.new_empty((*x.shape[:-1], BLOCK * n_bcol))
 
 
-@torch.library.custom_op("titanmac::bell_dx", mutates_args=())
-def bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bcol: int) -> torch.Tensor:
+def _bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bcol: int) -> torch.Tensor:
     """dX = dY · Wᵀ; dy [..., 64*n_bcol] -> dx [..., 64*n_brow]."""
     _check_values(values, "bell_dx")
     n_brow, width = int(values.shape[0]), int(values.shape[1])
@@ -182,7 +183,7 @@ def bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bco
     M = dy2.shape[0]
     dx = torch.empty((M, K), dtype=values.dtype, device=dev)
     if M > 0:
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = _lib.lib().tmac_bell_dx(
                 _lib.ptr(dy2), lddy, _lib.ptr(values.contiguous()), _lib.ptr(col_idx), _lib.ptr(dx), K,
                 M, n_brow, n_bcol, width, _lib.dtype_code(values.dtype), _lib.stream_ptr(dev))
@@ -190,14 +191,16 @@ def bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bco
     return dx.reshape(*dy.shape[:-1], K)
 
 
+bell_dx = torch.library.custom_op("titanmac::bell_dx", mutates_args=())(_bell_dx)
+
+
 @bell_dx.register_fake
 def _(dy, values, col_idx, n_bcol):
     return dy.new_empty((*dy.shape[:-1], BLOCK * values.shape[0]), dtype=values.dtype)
 
 
-@torch.library.custom_op("titanmac::bell_sddmm", mutates_args=())
-def bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow: int, width: int,
-               out_dtype: torch.dtype) -> torch.Tensor:
+def _bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow: int, width: int,
+                out_dtype: torch.dtype) -> torch.Tensor:
     """dvalues [n_brow, width, 64, 64] = (xᵀ·dy) on the pattern's blocks (deterministic)."""
     K = BLOCK * n_brow
     if x.shape[-1] != K:
@@ -220,12 +223,15 @@ def bell_sddmm(x: torch.Tensor, dy: torch.Tensor, col_idx: torch.Tensor, n_brow:
     L = _lib.lib()
     ws_bytes = _sddmm_workspace_bytes(L, M, n_brow, n_bcol, width)
     ws = torch.empty((ws_bytes + 15) // 16 * 4, dtype=torch.float32, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = L.tmac_bell_sddmm(_lib.ptr(x2), ldx, _lib.ptr(dy2), lddy, _lib.ptr(col_idx), _lib.ptr(out),
                                _lib.dtype_code(out_dtype), _lib.ptr(ws), ws.numel() * 4, M, n_brow,
                                n_bcol, width, _lib.dtype_code(x2.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_bell_sddmm")
     return out
+
+
+bell_sddmm = torch.library.custom_op("titanmac::bell_sddmm", mutates_args=())(_bell_sddmm)
 
 
 @bell_sddmm.register_fake
@@ -261,10 +267,12 @@ def _fwd_backward(ctx, gy):
     x, values, col_idx = ctx.saved_tensors
     n_brow, width = int(values.shape[0]), int(values.shape[1])
     gx = gv = gb = None
+    direct = _lib.direct_call(gy, x, values)
     if ctx.needs_input_grad[0]:
-        gx = bell_dx(gy, values, col_idx, ctx.n_bcol).to(x.dtype)
+        gx = (_bell_dx if direct else bell_dx)(gy, values, col_idx, ctx.n_bcol).to(x.dtype)
     if ctx.needs_input_grad[1]:
-        gv = bell_sddmm(x, gy.to(x.dtype), col_idx, n_brow, width, values.dtype)
+        gv = (_bell_sddmm if direct else bell_sddmm)(x, gy.to(x.dtype), col_idx, n_brow, width,
+                                                     values.dtype)
     if ctx.has_bias and ctx.needs_input_grad[7]:
         gb = gy.reshape(-1, gy.shape[-1]).sum(0)
     return gx, gv, None, None, None, None, None, gb, None
@@ -295,8 +303,9 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
     idx = pattern.device_index(values.device)
     fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
         x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
-    y = bell_fwd(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
-                 idx["order"], bias, fuse)
+    op = _bell_fwd if _lib.direct_call(x, values, bias) else bell_fwd
+    y = op(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"], idx["order"], bias,
+           fuse)
     if activation == "gelu" and not fuse:
         y = torch.nn.functional.gelu(y)
     return y

@@ -17,8 +17,7 @@ import torch
 from . import _lib
 
 
-@torch.library.custom_op("titanmac::dwconv_causal", mutates_args=())
-def dwconv_causal(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def _dwconv_causal(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """x [B, T, C] (rows may be strided, last dimension contiguous), weight [C, k] -> [B, T, C]."""
     if x.dim() != 3 or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
         raise ValueError(f"dwconv_causal: x must be [B, T, C] and weight [C, k]; got "
@@ -33,7 +32,7 @@ def dwconv_causal(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     out = torch.empty((B, T, C), dtype=x.dtype, device=dev)
     if B * T * C == 0:
         return out
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = _lib.lib().tmac_dwconv_causal(_lib.ptr(x), x.stride(1), _lib.ptr(w), _lib.ptr(out), C, B,
                                            T, C, int(w.shape[1]), _lib.dtype_code(x.dtype),
                                            _lib.stream_ptr(dev))
@@ -41,14 +40,16 @@ def dwconv_causal(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     return out
 
 
+dwconv_causal = torch.library.custom_op("titanmac::dwconv_causal", mutates_args=())(_dwconv_causal)
+
+
 @dwconv_causal.register_fake
 def _(x, weight):
     return x.new_empty(x.shape)
 
 
-@torch.library.custom_op("titanmac::dwconv_causal_bwd", mutates_args=())
-def dwconv_causal_bwd(grad_out: torch.Tensor, x: torch.Tensor,
-                      weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def _dwconv_causal_bwd(grad_out: torch.Tensor, x: torch.Tensor,
+                       weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """(grad_x [B, T, C] in x's dtype, grad_weight [C, k] fp32) of dwconv_causal."""
     if grad_out.shape != x.shape or weight.dim() != 2 or weight.shape[0] != x.shape[2]:
         raise ValueError("dwconv_causal_bwd: grad_out must match x [B, T, C] and weight be [C, k]")
@@ -70,13 +71,16 @@ def dwconv_causal_bwd(grad_out: torch.Tensor, x: torch.Tensor,
     _lib.check(L.tmac_dwconv_causal_bwd_workspace(B, T, C, k, ctypes.byref(ws_bytes)),
                "tmac_dwconv_causal_bwd_workspace")
     ws = torch.empty(max(ws_bytes.value, 16), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = L.tmac_dwconv_causal_bwd(_lib.ptr(g), g.stride(1), _lib.ptr(x), x.stride(1),
                                       _lib.ptr(w), _lib.ptr(dx), C, _lib.ptr(dw), _lib.ptr(ws),
                                       ws.numel(), B, T, C, k, _lib.dtype_code(x.dtype),
                                       _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_dwconv_causal_bwd")
     return dx, dw
+
+
+dwconv_causal_bwd = torch.library.custom_op("titanmac::dwconv_causal_bwd", mutates_args=())(_dwconv_causal_bwd)
 
 
 @dwconv_causal_bwd.register_fake
@@ -91,7 +95,8 @@ def _setup(ctx, inputs, output):
 
 def _backward(ctx, grad):
     x, weight = ctx.saved_tensors
-    dx, dw = dwconv_causal_bwd(grad, x, weight)
+    op = _dwconv_causal_bwd if _lib.direct_call(grad, x, weight) else dwconv_causal_bwd
+    dx, dw = op(grad, x, weight)
     return dx, dw.to(weight.dtype)
 
 
@@ -102,4 +107,5 @@ def causal_dwconv(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     """Causal depthwise convolution of x [B, T, C] with weight [C, k] (or nn.Conv1d's [C, 1, k])."""
     if weight.dim() == 3:
         weight = weight.reshape(weight.shape[0], weight.shape[2])
-    return dwconv_causal(x, weight)
+    op = _dwconv_causal if _lib.direct_call(x, weight) else dwconv_causal
+    return op(x, weight)

@@ -45,7 +45,7 @@ def silu_backward(d_h: torch.Tensor, z1: torch.Tensor) -> torch.Tensor:
     dh, z = d_h.contiguous(), z1.to(d_h.dtype).contiguous()
     out = torch.empty_like(dh)
     if out.numel():
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = _lib.lib().tmac_silu_bwd(_lib.ptr(dh), _lib.ptr(z), _lib.ptr(out), out.numel(),
                                           _lib.dtype_code(dh.dtype), _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_silu_bwd")
@@ -61,7 +61,7 @@ def mse_grad(y: torch.Tensor, v: torch.Tensor, coef: Optional[float] = None) -> 
     out = torch.empty_like(yc)
     c = 2.0 / max(y.numel(), 1) if coef is None else float(coef)
     if out.numel():
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = _lib.lib().tmac_mse_grad(_lib.ptr(yc), _lib.ptr(vc), _lib.ptr(out), out.numel(),
                                           ctypes.c_float(c), _lib.dtype_code(y.dtype),
                                           _lib.stream_ptr(dev))
@@ -110,7 +110,7 @@ def mem_update(grads: Sequence[torch.Tensor], momentums: Sequence[torch.Tensor],
         _lib.check(L.tmac_mem_update_workspace(sizes, n, ctypes.byref(wsb)),
                    "tmac_mem_update_workspace")
         ws = torch.empty(max(wsb.value, 16), dtype=torch.uint8, device=dev)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = L.tmac_mem_update(arr(grads), arr(momentums), arr(weights),
                                arr(mirrors) if mirrors is not None else None, sizes, n,
                                _lib.ptr(a), _lib.ptr(e), _lib.ptr(nrm), ctypes.c_float(theta),

@@ -25,9 +25,8 @@ def _rows(x: torch.Tensor):
     return x2
 
 
-@torch.library.custom_op("titanmac::rmsnorm_fwd", mutates_args=())
-def rmsnorm_fwd(x: torch.Tensor, scale: torch.Tensor,
-                eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+def _rmsnorm_fwd(x: torch.Tensor, scale: torch.Tensor,
+                 eps: float) -> tuple[torch.Tensor, torch.Tensor]:
     """(y with x's shape, rstd fp32 [prod(x.shape[:-1])])."""
     if scale.dim() != 1 or scale.shape[0] != x.shape[-1]:
         raise ValueError(f"rmsnorm: scale must be [{x.shape[-1]}], got {tuple(scale.shape)}")
@@ -38,12 +37,15 @@ def rmsnorm_fwd(x: torch.Tensor, scale: torch.Tensor,
     y = torch.empty((M, D), dtype=x.dtype, device=dev)
     rstd = torch.empty((M,), dtype=torch.float32, device=dev)
     if M > 0:
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = _lib.lib().tmac_rmsnorm_fwd(_lib.ptr(x2), x2.stride(0), _lib.ptr(s), _lib.ptr(y), D,
                                              _lib.ptr(rstd), M, D, float(eps),
                                              _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_rmsnorm_fwd")
     return y.view(x.shape), rstd
+
+
+rmsnorm_fwd = torch.library.custom_op("titanmac::rmsnorm_fwd", mutates_args=())(_rmsnorm_fwd)
 
 
 @rmsnorm_fwd.register_fake
@@ -54,9 +56,8 @@ def _(x, scale, eps):
     return x.new_empty(x.shape), x.new_empty((M,), dtype=torch.float32)
 
 
-@torch.library.custom_op("titanmac::rmsnorm_bwd", mutates_args=())
-def rmsnorm_bwd(grad: torch.Tensor, x: torch.Tensor, scale: torch.Tensor,
-                rstd: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def _rmsnorm_bwd(grad: torch.Tensor, x: torch.Tensor, scale: torch.Tensor,
+                 rstd: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """(grad_x with x's shape and dtype, grad_scale fp32 [D])."""
     dev = _lib.require_device(grad, x, scale, rstd, what="rmsnorm backward")
     s = scale.to(x.dtype).contiguous()
@@ -71,13 +72,16 @@ def rmsnorm_bwd(grad: torch.Tensor, x: torch.Tensor, scale: torch.Tensor,
         _lib.check(L.tmac_rmsnorm_bwd_workspace(M, D, ctypes.byref(ws_bytes)),
                    "tmac_rmsnorm_bwd_workspace")
         ws = torch.empty(max(ws_bytes.value, 16), dtype=torch.uint8, device=dev)
-        with torch.cuda.device(dev):
+        with _lib.device_guard(dev):
             rc = L.tmac_rmsnorm_bwd(_lib.ptr(g2), g2.stride(0), _lib.ptr(x2), x2.stride(0),
                                     _lib.ptr(s), _lib.ptr(rstd.contiguous()), _lib.ptr(dx), D,
                                     _lib.ptr(dscale), _lib.ptr(ws), ws.numel(), M, D,
                                     _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_rmsnorm_bwd")
     return dx.view(x.shape), dscale
+
+
+rmsnorm_bwd = torch.library.custom_op("titanmac::rmsnorm_bwd", mutates_args=())(_rmsnorm_bwd)
 
 
 @rmsnorm_bwd.register_fake
@@ -92,7 +96,8 @@ def _setup(ctx, inputs, output):
 
 def _backward(ctx, grad_y, grad_rstd):
     x, scale, rstd = ctx.saved_tensors
-    dx, dscale = rmsnorm_bwd(grad_y, x, scale, rstd)
+    op = _rmsnorm_bwd if _lib.direct_call(grad_y, x, scale) else rmsnorm_bwd
+    dx, dscale = op(grad_y, x, scale, rstd)
     return dx, dscale.to(scale.dtype), None
 
 
@@ -101,4 +106,5 @@ rmsnorm_fwd.register_autograd(_backward, setup_context=_setup)
 
 def rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
     """x / sqrt(mean(x², -1) + eps) * scale over the last dimension."""
-    return rmsnorm_fwd(x, scale, float(eps))[0]
+    op = _rmsnorm_fwd if _lib.direct_call(x, scale) else rmsnorm_fwd
+    return op(x, scale, float(eps))[0]

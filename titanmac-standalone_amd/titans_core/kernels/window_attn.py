@@ -161,10 +161,9 @@ def _check_qkv(q, k, v):
             raise ValueError("q, k, v need a contiguous last (head_dim) dimension")
 
 
-@torch.library.custom_op("titanmac::window_attn_fwd", mutates_args=())
-def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
-                    n_persistent: int, causal: bool, pattern: int, block_size: int,
-                    scale: float, need_lse: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+def _window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
+                     n_persistent: int, causal: bool, pattern: int, block_size: int,
+                     scale: float, need_lse: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
     """Masked attention over q/k/v [B, H, S, dh].
 
     Returns (out, lse): out a contiguous [B, S, H, dh]; lse the fp32 [B, H, S]
@@ -181,7 +180,7 @@ def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_si
     row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
                                                         pattern, block_size, dev)
     o_view = out.permute(0, 2, 1, 3)  # [B, H, S, dh] view
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = _lib.lib().tmac_wattn_fwd(
             _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
             _lib.ptr(out), _strides3(o_view), _lib.ptr(lse) if need_lse else None, B, H, S, dh,
@@ -192,6 +191,9 @@ def window_attn_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_si
     return out, lse
 
 
+window_attn_fwd = torch.library.custom_op("titanmac::window_attn_fwd", mutates_args=())(_window_attn_fwd)
+
+
 @window_attn_fwd.register_fake
 def _(q, k, v, window_size, n_persistent, causal, pattern, block_size, scale, need_lse=False):
     B, H, S, dh = q.shape
@@ -199,11 +201,10 @@ def _(q, k, v, window_size, n_persistent, causal, pattern, block_size, scale, ne
     return q.new_empty((B, S, H, dh)), lse
 
 
-@torch.library.custom_op("titanmac::window_attn_bwd", mutates_args=())
-def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    out: torch.Tensor, lse: torch.Tensor, window_size: int, n_persistent: int,
-                    causal: bool, pattern: int, block_size: int,
-                    scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+def _window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                     out: torch.Tensor, lse: torch.Tensor, window_size: int, n_persistent: int,
+                     causal: bool, pattern: int, block_size: int,
+                     scale: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(dq, dk, dv), each [B, H, S, dh] (transposed views of [B, S, H, dh] buffers), from
     grad_out and out [B, S, H, dh] and lse [B, H, S] of window_attn_fwd."""
     _check_qkv(q, k, v)
@@ -228,7 +229,7 @@ def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
     col_ptr, entries_kv, order_kv, n_lead_kv = _device_work_list_kv(
         S, window_size, n_persistent, causal, pattern, block_size, dev)
     o_view, g_view = out.permute(0, 2, 1, 3), grad_out.permute(0, 2, 1, 3)
-    with torch.cuda.device(dev):
+    with _lib.device_guard(dev):
         rc = _lib.lib().tmac_wattn_bwd(
             _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
             _lib.ptr(out), _strides3(o_view), _lib.ptr(grad_out), _strides3(g_view),
@@ -241,6 +242,9 @@ def window_attn_bwd(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v:
             _lib.dtype_code(q.dtype), _lib.stream_ptr(dev))
     _lib.check(rc, "tmac_wattn_bwd")
     return tuple(views)
+
+
+window_attn_bwd = torch.library.custom_op("titanmac::window_attn_bwd", mutates_args=())(_window_attn_bwd)
 
 
 @window_attn_bwd.register_fake
@@ -263,7 +267,8 @@ def _backward(ctx, grad_out, grad_lse):
         raise RuntimeError("window_attn_fwd was called with need_lse=False; its backward "
                            "needs the log-sum-exp (windowed_attention sets it under autograd)")
     q, k, v, out, lse = ctx.saved_tensors
-    dq, dk, dv = window_attn_bwd(grad_out, q, k, v, out, lse, *ctx.args)
+    op = _window_attn_bwd if _lib.direct_call(grad_out, q, k, v) else window_attn_bwd
+    dq, dk, dv = op(grad_out, q, k, v, out, lse, *ctx.args)
     return dq, dk, dv, None, None, None, None, None, None, None
 
 
@@ -290,6 +295,7 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
         scale = 1.0 / math.sqrt(q.shape[-1])
     need_lse = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
                                             or v.requires_grad)
-    out, _ = window_attn_fwd(q, k, v, int(window_size), int(n_persistent), bool(causal),
-                             code, int(block_size), float(scale), need_lse)
+    op = _window_attn_fwd if _lib.direct_call(q, k, v) else window_attn_fwd
+    out, _ = op(q, k, v, int(window_size), int(n_persistent), bool(causal), code, int(block_size),
+                float(scale), need_lse)
     return out.transpose(1, 2)
