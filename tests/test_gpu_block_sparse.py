@@ -108,6 +108,29 @@ def test_module_bf16_against_oracle(dev):
     close(got, want, atol=3e-2, rtol=2e-2)
 
 
+def test_module_conv_weight_stack_follows_weight_updates(dev):
+    """Without autograd the module keeps its stacked conv weight between calls. An in-place
+    weight update and load_state_dict must both show up in the next output, exactly as a
+    stack rebuilt from scratch gives it."""
+    torch.manual_seed(3)
+    m = tc.BlockSparseAttention(128, 2, window_size=128, block_size=64, n_persistent=16)
+    m = m.to(dev, torch.bfloat16).eval()
+    saved = {k: v.clone() for k, v in m.state_dict().items()}
+    x = torch.randn(2, 300, 128, device=dev).to(torch.bfloat16)
+    with torch.no_grad():
+        y1 = m(x)
+        assert torch.equal(m(x), y1)
+        m.conv_k.weight.mul_(-1.5)
+        y2 = m(x)
+        m.__dict__.pop("_conv_stack", None)
+        y2_fresh = m(x)
+        m.load_state_dict(saved)
+        y3 = m(x)
+    assert not torch.equal(y2, y1)
+    assert torch.equal(y2, y2_fresh)
+    assert torch.equal(y3, y1)
+
+
 def test_blockwin_full_size_with_global_persistent_rows(dev):
     """Config-3 shape (B=8, H=10, S=4096, w=512, Np=16) with the block-window pattern:
     persistent rows attend to all 4096 keys; (b, h) = (0, 0) and (7, 9) in full."""

@@ -63,6 +63,20 @@ class BlockSparseAttention(nn.Module):
         self.dropout = nn.Dropout(dropout) if dropout > 0 else nn.Identity()
         self.scale = 1.0 / math.sqrt(self.d_head)
 
+    def _fused_conv_weight(self, dtype: torch.dtype) -> torch.Tensor:
+        """The three conv weights stacked as [3·d_model, 1, k] in `dtype`. Without a gradient to
+        record, the stack is kept and rebuilt only when a weight changes (new storage or an
+        in-place update: optimizer steps and load_state_dict bump the tensor version)."""
+        ws = (self.conv_q.weight, self.conv_k.weight, self.conv_v.weight)
+        if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+            return torch.cat(ws, dim=0).to(dtype)
+        key = (dtype,) + tuple((w.data_ptr(), w._version) for w in ws)
+        cached = self.__dict__.get("_conv_stack")
+        if cached is None or cached[0] != key:
+            cached = (key, torch.cat(ws, dim=0).to(dtype))
+            self.__dict__["_conv_stack"] = cached
+        return cached[1]
+
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x [B, T, d_model] -> [B, T, d_model]. attn_mask is ignored, as in the reference (:218)."""
         if self.training and self.dropout_p > 0:
@@ -70,8 +84,7 @@ class BlockSparseAttention(nn.Module):
         B, T, D = x.shape
         qkv = self.qkv_proj(x)
         if self.use_conv:
-            w = torch.cat([self.conv_q.weight, self.conv_k.weight, self.conv_v.weight], dim=0)
-            qkv = causal_dwconv(qkv, w.to(qkv.dtype))
+            qkv = causal_dwconv(qkv, self._fused_conv_weight(qkv.dtype))
         q, k, v = qkv.chunk(3, dim=-1)
         q = q.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         k = k.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
