@@ -307,3 +307,35 @@ def test_neural_memory_construction_errors_and_cpu_refusal():
     from titans_core.kernels import memory_mlp as km
     with pytest.raises(RuntimeError, match="GPU"):
         km.silu_backward(torch.zeros(4), torch.zeros(4))
+
+
+def test_direct_call_only_when_nothing_is_recorded():
+    """The op wrappers skip the torch.library dispatcher only in eager mode, for plain
+    tensors, and when no autograd graph has to be recorded for them."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from titans_core.kernels import _lib
+    a = torch.zeros(2)
+    p = nn.Parameter(torch.zeros(2))
+    assert _lib.direct_call(a, None)
+    assert not _lib.direct_call(a, p)  # a parameter that needs a gradient
+    with torch.no_grad():
+        assert _lib.direct_call(a, p)
+    with torch.inference_mode():
+        assert _lib.direct_call(torch.zeros(2), p)
+    p.requires_grad_(False)
+    assert _lib.direct_call(a, p)
+    with FakeTensorMode() as mode:
+        f = mode.from_tensor(a)
+    assert not _lib.direct_call(f)
+
+
+def test_direct_call_defers_to_the_op_under_compile():
+    from titans_core.kernels import _lib
+    seen = []
+
+    def fn(t):
+        seen.append(_lib.direct_call(t))
+        return t + 1
+
+    torch.compile(fn, backend="eager")(torch.zeros(2))
+    assert seen == [False]
