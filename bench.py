@@ -122,11 +122,19 @@ def setup_spmm(dev):
         if rc:
             _lib.check(rc, "tmac_bell_fwd")
 
+    # the same layer on its first 64 rows only (a decoding-sized batch: the few-row kernel)
+    args_m64 = args[:10] + (64,) + args[11:]
+
+    def launch_m64():
+        rc = L.tmac_bell_fwd(*args_m64)
+        if rc:
+            _lib.check(rc, "tmac_bell_fwd")
+
     nnz = c["n_brow"] * c["width"]
     flops = 2 * c["M"] * nnz * BS * BS
     bytes_ = c["M"] * K * 2 + nnz * BS * BS * 2 + (c["n_bcol"] + 1 + 2 * nnz + c["n_bcol"]) * 4 + c["M"] * N * 2
-    return dict(launch=launch, flops=flops, bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu,
-                keep=(X, V, Y, idx))
+    return dict(launch=launch, launch_m64=launch_m64, weight_bytes=nnz * BS * BS * 2, flops=flops,
+                bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu, keep=(X, V, Y, idx))
 
 
 def setup_attn(dev, S=None, pattern=None, block_size=64):
@@ -538,6 +546,8 @@ def main() -> int:
                            bytes=spmm["bytes"])
         if args.mode == "all":
             out["spmm"]["dense_ms"] = dense_gemm_baseline(spmm, dev, K, stream)
+        out["spmm"]["m64_ms"] = timed(spmm["launch_m64"], K, W, stream)
+        out["spmm"]["m64_weight_tbs"] = spmm["weight_bytes"] / out["spmm"]["m64_ms"] / 1e9
     if args.mode in ("all", "attn", "attn_bwd"):
         att = setup_attn(dev)
     if args.mode in ("all", "attn"):
@@ -638,6 +648,8 @@ def main() -> int:
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
             "attn_bwd_speedup_vs_dense": round(out["attn_bwd"]["dense_bwd_ms"] / out["attn_bwd"]["ms"], 2),
+            "bell_fwd_cfg2_m64_us": round(out["spmm"]["m64_ms"] * 1e3, 2),
+            "bell_fwd_cfg2_m64_weight_tbs": round(out["spmm"]["m64_weight_tbs"], 3),
             "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),
             "bell_dx_cfg4_tflops": round(out["dx"]["tflops"], 3),
             "bell_dx_cfg4_hbm_gbs_compulsory": round(out["dx"]["gbs"], 1),
