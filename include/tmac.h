@@ -50,7 +50,8 @@ typedef enum {
   TMAC_ERR_ALIGN = -5,     /* a pointer or stride breaks the 16-byte vector-load alignment */
   TMAC_ERR_WORKSPACE = -6, /* workspace missing or smaller than required */
   TMAC_ERR_CAPACITY = -7,  /* an output array is too small */
-  TMAC_ERR_VALUE = -8      /* an argument value is outside its domain (reference raises ValueError) */
+  TMAC_ERR_VALUE = -8,     /* an argument value is outside its domain (reference raises ValueError) */
+  TMAC_ERR_TOO_LARGE = -9  /* sizes exceed the static scratch of an allocation-free entry point */
 } tmac_status;
 
 typedef enum { TMAC_F32 = 0, TMAC_BF16 = 1, TMAC_F16 = 2 } tmac_dtype;
@@ -263,6 +264,38 @@ int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const int32_t* d_col_ptr, const int32_t* d_entries_kv,
                    const int32_t* d_order_kv, int n_lead_kv,
                    int dtype, void* stream);
+
+/* Rows of the static scratch of tmac_wattn_bwd_noalloc (B*H*S at most). */
+#define TMAC_WATTN_BWD_SCRATCH_ROWS (4 * 1024 * 1024)
+
+/* tmac_wattn_bwd without the delta workspace argument: the fp32 row sums go to a
+ * static device array inside the library (16 MiB per GPU, held until the
+ * process ends), so the call allocates nothing and needs no workspace from the
+ * caller. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving or
+ * training loops, harnesses that forbid hipMalloc). Same arguments, kernels and
+ * results (bit for bit) as tmac_wattn_bwd. Returns TMAC_ERR_TOO_LARGE when
+ * B*H*S > TMAC_WATTN_BWD_SCRATCH_ROWS (nothing launched). Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (concurrent streams,
+ * threads) race and must be serialised by the caller. The scratch's device
+ * address is looked up once per device, on the first call with that device
+ * current. */
+int tmac_wattn_bwd_noalloc(const void* d_Q, const int64_t q_strides[3],
+                           const void* d_K, const int64_t k_strides[3],
+                           const void* d_V, const int64_t v_strides[3],
+                           const void* d_O, const int64_t o_strides[3],
+                           const void* d_dO, const int64_t do_strides[3],
+                           const float* d_lse,
+                           void* d_dQ, const int64_t dq_strides[3],
+                           void* d_dK, const int64_t dk_strides[3],
+                           void* d_dV, const int64_t dv_strides[3],
+                           int B, int H, int S, int dh, int window, int n_persistent,
+                           int causal, int pattern, int block_size, float scale,
+                           const int32_t* d_row_ptr, const int32_t* d_entries,
+                           const int32_t* d_order, int n_lead,
+                           const int32_t* d_col_ptr, const int32_t* d_entries_kv,
+                           const int32_t* d_order_kv, int n_lead_kv,
+                           int dtype, void* stream);
 
 /* ------------------------------------------------------------------------- */
 /* Causal depthwise convolution (device).                                     */

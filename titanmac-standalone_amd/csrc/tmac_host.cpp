@@ -26,6 +26,7 @@ extern "C" const char* tmac_status_string(int code) {
     case TMAC_ERR_WORKSPACE: return "workspace missing or too small";
     case TMAC_ERR_CAPACITY: return "output array too small";
     case TMAC_ERR_VALUE: return "argument value outside its domain";
+    case TMAC_ERR_TOO_LARGE: return "sizes exceed the static scratch of an allocation-free entry point";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -30,6 +30,8 @@
 
 #include <math.h>
 
+#include <mutex>
+
 #include "tmac_device.h"
 
 using namespace tmac;
@@ -1076,19 +1078,21 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }
 
-extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const void* d_K,
-                              const int64_t k_strides[3], const void* d_V,
-                              const int64_t v_strides[3], const void* d_O,
-                              const int64_t o_strides[3], const void* d_dO,
-                              const int64_t do_strides[3], const float* d_lse, float* d_delta,
-                              void* d_dQ, const int64_t dq_strides[3], void* d_dK,
-                              const int64_t dk_strides[3], void* d_dV,
-                              const int64_t dv_strides[3], int B, int H, int S, int dh, int window,
-                              int n_persistent, int causal, int pattern, int block_size,
-                              float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
-                              const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
-                              const int32_t* d_entries_kv, const int32_t* d_order_kv,
-                              int n_lead_kv, int dtype, void* stream) {
+namespace {
+
+// Shared body of tmac_wattn_bwd and tmac_wattn_bwd_noalloc: d_delta is the
+// fp32 [B, H, S] row-sum buffer (the caller's workspace, or the static scratch).
+int wattn_bwd_impl(const void* d_Q, const int64_t q_strides[3], const void* d_K,
+                   const int64_t k_strides[3], const void* d_V, const int64_t v_strides[3],
+                   const void* d_O, const int64_t o_strides[3], const void* d_dO,
+                   const int64_t do_strides[3], const float* d_lse, float* d_delta, void* d_dQ,
+                   const int64_t dq_strides[3], void* d_dK, const int64_t dk_strides[3],
+                   void* d_dV, const int64_t dv_strides[3], int B, int H, int S, int dh,
+                   int window, int n_persistent, int causal, int pattern, int block_size,
+                   float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
+                   const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
+                   const int32_t* d_entries_kv, const int32_t* d_order_kv, int n_lead_kv,
+                   int dtype, void* stream) {
   if (!d_Q || !d_K || !d_V || !d_O || !d_dO || !d_lse || !d_delta || !d_dQ || !d_dK || !d_dV ||
       !q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides ||
       !dk_strides || !dv_strides || !d_row_ptr || !d_entries || !d_order || !d_col_ptr ||
@@ -1192,4 +1196,86 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
 #undef TMAC_WATTN_BWD_F32
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
+}
+
+// Row sums of the allocation-free backward: a file-scope device array, one copy
+// per GPU, of TMAC_WATTN_BWD_SCRATCH_ROWS floats (16 MiB). Host code never
+// passes `scratch` itself to a kernel (in host code the name is a host-side
+// stand-in, not a device address): it passes the address hipGetSymbolAddress
+// returns for the current device.
+__device__ __align__(256) float scratch[TMAC_WATTN_BWD_SCRATCH_ROWS];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up once per device
+// (with that device current) and kept; nullptr with *err set on failure.
+float* scratch_on_current_device(int* err) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = static_cast<int>(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = TMAC_ERR_VALUE;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) {
+      *err = e != hipSuccess ? static_cast<int>(e) : TMAC_ERR_NULL;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const void* d_K,
+                              const int64_t k_strides[3], const void* d_V,
+                              const int64_t v_strides[3], const void* d_O,
+                              const int64_t o_strides[3], const void* d_dO,
+                              const int64_t do_strides[3], const float* d_lse, float* d_delta,
+                              void* d_dQ, const int64_t dq_strides[3], void* d_dK,
+                              const int64_t dk_strides[3], void* d_dV,
+                              const int64_t dv_strides[3], int B, int H, int S, int dh, int window,
+                              int n_persistent, int causal, int pattern, int block_size,
+                              float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
+                              const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
+                              const int32_t* d_entries_kv, const int32_t* d_order_kv,
+                              int n_lead_kv, int dtype, void* stream) {
+  return wattn_bwd_impl(d_Q, q_strides, d_K, k_strides, d_V, v_strides, d_O, o_strides, d_dO,
+                        do_strides, d_lse, d_delta, d_dQ, dq_strides, d_dK, dk_strides, d_dV,
+                        dv_strides, B, H, S, dh, window, n_persistent, causal, pattern, block_size,
+                        scale, d_row_ptr, d_entries, d_order, n_lead, d_col_ptr, d_entries_kv,
+                        d_order_kv, n_lead_kv, dtype, stream);
+}
+
+extern "C" int tmac_wattn_bwd_noalloc(
+    const void* d_Q, const int64_t q_strides[3], const void* d_K, const int64_t k_strides[3],
+    const void* d_V, const int64_t v_strides[3], const void* d_O, const int64_t o_strides[3],
+    const void* d_dO, const int64_t do_strides[3], const float* d_lse, void* d_dQ,
+    const int64_t dq_strides[3], void* d_dK, const int64_t dk_strides[3], void* d_dV,
+    const int64_t dv_strides[3], int B, int H, int S, int dh, int window, int n_persistent,
+    int causal, int pattern, int block_size, float scale, const int32_t* d_row_ptr,
+    const int32_t* d_entries, const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
+    const int32_t* d_entries_kv, const int32_t* d_order_kv, int n_lead_kv, int dtype,
+    void* stream) {
+  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
+  if (static_cast<int64_t>(B) * H * S > TMAC_WATTN_BWD_SCRATCH_ROWS) return TMAC_ERR_TOO_LARGE;
+  int err = TMAC_OK;
+  float* delta = scratch_on_current_device(&err);
+  if (!delta) return err;
+  // every row of delta is written by the row-sum kernel before it is read: no clearing
+  return wattn_bwd_impl(d_Q, q_strides, d_K, k_strides, d_V, v_strides, d_O, o_strides, d_dO,
+                        do_strides, d_lse, delta, d_dQ, dq_strides, d_dK, dk_strides, d_dV,
+                        dv_strides, B, H, S, dh, window, n_persistent, causal, pattern, block_size,
+                        scale, d_row_ptr, d_entries, d_order, n_lead, d_col_ptr, d_entries_kv,
+                        d_order_kv, n_lead_kv, dtype, stream);
 }
