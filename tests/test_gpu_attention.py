@@ -13,15 +13,17 @@ from oracle import attention as oa
 from oracle import masks as om
 from titans_core.kernels.window_attn import windowed_attention
 
+import sampled  # noqa: E402  (tests/sampled.py)
+
 pytestmark = pytest.mark.gpu
 
 
-def close(got, want, atol=2e-2, rtol=1e-2):
+def close(got, want, atol=2e-2, rtol=1e-2, what=""):
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     err = np.abs(got - want)
     ok = err <= atol + rtol * np.abs(want)
-    assert ok.all(), f"max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+    assert ok.all(), f"{what} max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
 
 
 def qkv(shape, dtype, seed):
@@ -111,7 +113,8 @@ def test_config1_module_fp32(dev):
 
 def test_config3_full_size(dev):
     """BASELINE config 3 (B=8, H=10, S=4096, w=512, Np=16, bf16): two (b, h) pairs
-    checked in full against the oracle, every output finite."""
+    checked in full against the oracle; in every one of the 80 (b, h) pairs, the
+    mask's boundary rows and 6 random rows against the oracle; every output finite."""
     B, H, S = 8, 10, 4096
     g = torch.Generator().manual_seed(3)
     q, k, v = (torch.randn(B, H, S, 64, generator=g).to(torch.bfloat16) for _ in range(3))
@@ -122,3 +125,10 @@ def test_config3_full_size(dev):
         ref = oa.masked_attention(q[b, h].float().numpy(), k[b, h].float().numpy(),
                                   v[b, h].float().numpy(), mask, dtype=np.float32)
         close(o[b, h].numpy(), ref)
+    rng = np.random.default_rng(30)
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    for b in range(B):
+        for h in range(H):
+            rows = sampled.sample_rows(S, 16, 512, rng)
+            ref = sampled.fwd_rows_ref(qn[b, h], kn[b, h], vn[b, h], mask, rows)
+            close(o[b, h].numpy()[rows], ref, what=f"(b, h) = ({b}, {h})")

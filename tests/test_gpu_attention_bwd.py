@@ -18,6 +18,8 @@ from oracle import attention as oa
 from oracle import masks as om
 from titans_core.kernels.window_attn import window_attn_fwd, windowed_attention
 
+import sampled  # noqa: E402  (tests/sampled.py)
+
 pytestmark = pytest.mark.gpu
 
 
@@ -123,7 +125,9 @@ def test_backward_through_fused_qkv_views(dev):
 
 def test_backward_full_size_cfg3(dev):
     """Config-3 shape (B=8, H=10, S=4096, w=512, Np=16, band): finite everywhere;
-    (b, h) = (0, 0) and (7, 9) in full against the oracle."""
+    (b, h) = (0, 0) and (7, 9) in full against the oracle; in every one of the 80
+    (b, h) pairs, dQ on the mask's boundary rows and 6 random rows, and dK, dV on 3
+    sequence keys (the first one and 2 random), against the oracle."""
     B, H, S, w, Np = 8, 10, 4096, 512, 16
     q, k, v, do = tensors((B, H, S, 64), torch.bfloat16, seed=15)
     _, dq, dk, dv = run_bwd(dev, q, k, v, do, w, Np, True, "band", 64)
@@ -134,6 +138,18 @@ def test_backward_full_size_cfg3(dev):
         want = oa.masked_attention_grads(*(t[b, h].float().numpy() for t in (q, k, v, do)), mask)
         for got, ref in zip(grads, want):
             close(got[b, h].numpy(), ref)
+    rng = np.random.default_rng(31)
+    qn, kn, vn, dn = (t.float().numpy() for t in (q, k, v, do))
+    gq, gk, gv = (t.numpy() for t in grads)
+    for b in range(B):
+        for h in range(H):
+            args = (qn[b, h], kn[b, h], vn[b, h], dn[b, h], mask)
+            rows = sampled.sample_rows(S, Np, w, rng)
+            close(gq[b, h][rows], sampled.dq_rows_ref(*args, rows), what=f"dq ({b}, {h})")
+            cols = np.array(sorted({Np, *rng.choice(np.arange(Np + 1, S), 2, replace=False)}))
+            ref_k, ref_v = sampled.dkv_cols_ref(*args, cols)
+            close(gk[b, h][cols], ref_k, what=f"dk ({b}, {h})")
+            close(gv[b, h][cols], ref_v, what=f"dv ({b}, {h})")
 
 
 def _module_grads_fp64(m, x, dy, mask, conv=False):

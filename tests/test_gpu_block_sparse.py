@@ -18,6 +18,8 @@ from oracle import masks as om
 from titans_core.kernels.conv import causal_dwconv
 from titans_core.kernels.window_attn import windowed_attention
 
+import sampled  # noqa: E402  (tests/sampled.py)
+
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / "golden" / "bsa_golden.npz"
@@ -133,7 +135,8 @@ def test_module_conv_weight_stack_follows_weight_updates(dev):
 
 def test_blockwin_full_size_with_global_persistent_rows(dev):
     """Config-3 shape (B=8, H=10, S=4096, w=512, Np=16) with the block-window pattern:
-    persistent rows attend to all 4096 keys; (b, h) = (0, 0) and (7, 9) in full."""
+    persistent rows attend to all 4096 keys; (b, h) = (0, 0) and (7, 9) in full, and
+    sampled rows of all 80 (b, h) pairs."""
     B, H, S = 8, 10, 4096
     g = torch.Generator().manual_seed(4)
     q, k, v = (torch.randn(B, H, S, 64, generator=g).to(torch.bfloat16) for _ in range(3))
@@ -145,6 +148,15 @@ def test_blockwin_full_size_with_global_persistent_rows(dev):
         ref = oa.masked_attention(q[b, h].float().numpy(), k[b, h].float().numpy(),
                                   v[b, h].float().numpy(), mask, dtype=np.float32)
         close(o[b, h].numpy(), ref)
+    # every (b, h): the persistent rows (which see all 4096 keys), the mask's boundary
+    # rows and 6 random rows
+    rng = np.random.default_rng(32)
+    qn, kn, vn = (t.float().numpy() for t in (q, k, v))
+    for b in range(B):
+        for h in range(H):
+            rows = np.array(sorted(set(sampled.sample_rows(S, 16, 512, rng).tolist()) | set(range(16))))
+            ref = sampled.fwd_rows_ref(qn[b, h], kn[b, h], vn[b, h], mask, rows)
+            close(o[b, h].numpy()[rows], ref)
 
 
 def test_create_from_config(dev):
