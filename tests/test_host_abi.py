@@ -300,3 +300,51 @@ def test_only_persistent_tokens_allowed_for_blockwin_only():
     assert k.shape == (3, 3) and (k == 1).all()     # every pair allowed
     with pytest.raises(ValueError):
         tile_kinds(24, 8, 24, True, "band", 64)
+
+
+@pytest.mark.parametrize("S,w,Np,pattern", [(4096, 512, 16, 0), (333, 128, 5, 1), (1, 0, 0, 0)])
+def test_work_lists_exact_and_short_capacity(lib, S, w, Np, pattern):
+    """Each work list fills a buffer of exactly its length, reports the length with a
+    NULL buffer, and refuses a buffer one entry short (TMAC_ERR_CAPACITY) without writing
+    past it (the sanitizer run of this file checks the writes)."""
+    n_b = -(-S // 128)
+    for fn in (lib.tmac_wattn_schedule, lib.tmac_wattn_schedule_kv):
+        ptr = np.zeros(n_b + 1, dtype=np.int32)
+        n = ctypes.c_int(-1)
+        assert fn(S, w, Np, 1, pattern, 64, 128, 32, ptr.ctypes.data, None, 0, ctypes.byref(n)) == 0
+        total = n.value
+        assert total == ptr[-1] and total > 0
+        exact = np.full(total, -1, dtype=np.int32)
+        assert fn(S, w, Np, 1, pattern, 64, 128, 32, ptr.ctypes.data, exact.ctypes.data, total,
+                  ctypes.byref(n)) == 0
+        assert (exact >= 0).all() and n.value == total
+        short = np.zeros(max(total - 1, 1), dtype=np.int32)
+        rc = fn(S, w, Np, 1, pattern, 64, 128, 32, ptr.ctypes.data, short.ctypes.data, total - 1,
+                ctypes.byref(n))
+        assert rc == -7, rc
+
+
+def test_transpose_rejects_malformed_indices(lib):
+    out = [np.zeros(n, dtype=np.int32) for n in (5, 8, 8, 4)]
+    ptrs = [a.ctypes.data for a in out]
+    for ci in ([[0, 1], [2, 4]], [[1, 1], [0, 2]], [[2, 1], [0, 3]], [[0, -1], [1, 2]]):
+        ci = np.array(ci, dtype=np.int32)
+        assert lib.tmac_bell_transpose(ci.ctypes.data, 2, 4, 2, *ptrs) == -3
+    ci = np.array([[0, 1], [2, 3]], dtype=np.int32)
+    assert lib.tmac_bell_transpose(ci.ctypes.data, 2, 4, 2, None, *ptrs[1:]) == -1
+    assert lib.tmac_bell_validate(ci.ctypes.data, 70000, 70000, 40000) == -2   # n_brow * width > 2^31 - 1
+    assert lib.tmac_bell_sample_col_idx(0, 70000, 70000, 40000, ci.ctypes.data) == -2
+
+
+def test_mask_spans_and_launch_order_edges(lib):
+    rows = np.zeros(3, dtype=np.int32)
+    cols = np.zeros(3, dtype=np.int32)
+    assert lib.tmac_wattn_mask_spans(1, 0, 0, 1, 0, 64, rows.ctypes.data, cols.ctypes.data) == 0
+    assert rows.tolist() == [0, 0, 0] and cols.tolist() == [0, 0, 0]
+    assert lib.tmac_wattn_mask_spans(1, 0, 0, 1, 0, 64, None, cols.ctypes.data) == -1
+    assert lib.tmac_wattn_mask_spans(0, 0, 0, 1, 0, 64, rows.ctypes.data, cols.ctypes.data) == -2
+    ptr = np.array([0], dtype=np.int32)
+    order = np.zeros(1, dtype=np.int32)
+    lead = ctypes.c_int(-1)
+    rc = lib.tmac_wattn_launch_order(ptr.ctypes.data, 0, order.ctypes.data, ctypes.byref(lead))
+    assert rc in (0, -2)

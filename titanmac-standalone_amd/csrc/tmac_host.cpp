@@ -66,6 +66,7 @@ extern "C" int tmac_bell_sample_col_idx(uint64_t seed, int n_brow, int n_bcol, i
                                         int32_t* h_col_idx) {
   if (!h_col_idx) return TMAC_ERR_NULL;
   if (n_brow <= 0 || n_bcol <= 0 || width <= 0 || width > n_bcol) return TMAC_ERR_SHAPE;
+  if (static_cast<int64_t>(n_brow) * width > INT32_MAX) return TMAC_ERR_SHAPE;
   SplitMix64 rng{seed};
   std::vector<int32_t> perm(n_bcol);
   for (int r = 0; r < n_brow; ++r) {
@@ -84,6 +85,8 @@ extern "C" int tmac_bell_sample_col_idx(uint64_t seed, int n_brow, int n_bcol, i
 extern "C" int tmac_bell_validate(const int32_t* h_col_idx, int n_brow, int n_bcol, int width) {
   if (!h_col_idx) return TMAC_ERR_NULL;
   if (n_brow <= 0 || n_bcol <= 0 || width <= 0 || width > n_bcol) return TMAC_ERR_SHAPE;
+  // entry indices (r * width + s) are ints in the transposed index and the kernels
+  if (static_cast<int64_t>(n_brow) * width > INT32_MAX) return TMAC_ERR_SHAPE;
   for (int r = 0; r < n_brow; ++r) {
     const int32_t* row = h_col_idx + static_cast<size_t>(r) * width;
     for (int s = 0; s < width; ++s) {
