@@ -33,10 +33,14 @@ Kernel time is measured with HIP events on the launch stream (torch's current
 stream) around exactly K back-to-back launches after W warm-up launches, with a
 device synchronisation on both sides; ms_per_step is that time over K.
 The CPU baseline runs the oracle's dense restatement of the reference path
-(X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only.
+(X @ to_dense(W) in fp32 numpy) on the host cores, rank 0 only; the reference-equivalent
+PyTorch paths of configs 1, 3 and 4 are timed on the CPU as secondary figures.
+roofline.traffic is measured by the run itself: two rocprofv3 counter passes (FETCH_SIZE,
+WRITE_SIZE) over `--mode traffic` of the current build, scaled by a plain 1 GiB copy.
 
 Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, conv, norm, mac,
-mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE).
+mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE),
+traffic (the copy then the SpMM, three launches each: what the counter passes profile).
 """
 from __future__ import annotations
 
@@ -64,6 +68,7 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 BS = 64
 
 CFG2 = dict(M=8192, n_brow=40, n_bcol=160, width=40, seed=0)
+TRAFFIC_REPS = 3  # launches of the copy and of the SpMM in --mode traffic
 CFG3 = dict(B=8, H=10, S=4096, dh=64, window=512, n_persistent=16, seed=3)
 CFG4 = dict(M=32768, n_brow=10, n_bcol=40, width=20, seed=4)
 
@@ -465,48 +470,171 @@ def dense_gemm_baseline(spmm, dev, steps: int, stream) -> float:
     return timed(lambda: torch.mm(X, Wd, out=Y), max(2, steps // 2), 3, stream)
 
 
+def cpu_threads() -> tuple[int, dict]:
+    """Threads for the CPU baselines and what the host reports. The GPU box gives each
+    one-GPU job a share of its CPUs and presets OMP_NUM_THREADS to that share (16);
+    threads beyond it would only oversubscribe cores that other jobs hold, so the
+    baselines use min(CPUs in this process's affinity mask, OMP_NUM_THREADS)."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    n = min(affinity, int(omp)) if omp and omp.isdigit() and int(omp) > 0 else affinity
+    model = None
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    info = {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "omp_num_threads_env": omp,
+            "cpu_model": model}
+    return max(1, n), info
+
+
 def cpu_baseline(spmm) -> dict:
-    """The oracle's dense restatement (fp32 numpy X @ to_dense(W)) on the host cores."""
+    """The oracle's dense restatement of config 2 (fp32 numpy X @ to_dense(W), the
+    reference's nn.Linear with the zero blocks stored) on the host cores: a 2048-row
+    sample for about 10 s, effective (stored-block) FLOPs counted as on the GPU."""
     sys.path.insert(0, str(ROOT))
     from oracle import block_ell as ob  # the checker / CPU baseline only
-    try:
-        from threadpoolctl import threadpool_info, threadpool_limits
-    except ImportError:  # pragma: no cover
-        threadpool_info = threadpool_limits = None
+    from threadpoolctl import threadpool_info, threadpool_limits
     c = CFG2
-    cores = min(os.cpu_count() or 1, 16)
+    n, info = cpu_threads()
     X = spmm["X_cpu"].float().numpy()
     W = ob.to_dense(spmm["pat"].col_idx, spmm["V_cpu"].float().numpy(), c["n_bcol"])
-    import contextlib
-    ob_rows = 2048
-    Xs = np.ascontiguousarray(X[:ob_rows])
-    limit = threadpool_limits(limits=cores) if threadpool_limits else contextlib.nullcontext()
-    with limit:
-        used = cores
-        if threadpool_info:
-            used = max([p.get("num_threads", 1) for p in threadpool_info()] or [cores])
+    rows = 2048
+    Xs = np.ascontiguousarray(X[:rows])
+    with threadpool_limits(limits=n, user_api="blas"):
+        blas = [p for p in threadpool_info() if p.get("user_api") == "blas"]
+        blas_threads = max([p.get("num_threads", 0) for p in blas] or [0])
+        _ = Xs @ W
         reps, t0 = 0, time.perf_counter()
-        while True:  # about 12 s of CPU work
+        while True:
             _ = Xs @ W
             reps += 1
             el = time.perf_counter() - t0
-            if el > 12.0:
+            if el > 10.0:
                 break
-    eff = 2 * ob_rows * c["n_brow"] * c["width"] * BS * BS
-    return {"value": round(eff * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(used),
+    eff = 2 * rows * c["n_brow"] * c["width"] * BS * BS
+    dense = 2 * rows * BS * c["n_brow"] * BS * c["n_bcol"]
+    return {"value": round(eff * reps / el / 1e12, 4), "unit": "TFLOP/s", "cores": int(blas_threads),
             "kind": "port",
-            "sample": f"oracle dense fp32 X[{ob_rows},2560] @ to_dense(W)[2560,10240], {reps} reps "
-                      f"in {el:.1f} s; effective (stored-block) FLOPs counted, as on the GPU"}
+            "sample": f"oracle dense fp32 X[{rows},2560] @ to_dense(W)[2560,10240] (numpy, "
+                      f"{blas[0].get('internal_api') if blas else '?'} BLAS), {reps} reps in {el:.1f} s; "
+                      f"effective (stored-block) FLOPs counted, as on the GPU",
+            "dense_gflops_per_thread": round(dense * reps / el / 1e9 / max(1, blas_threads), 1),
+            "torch_threads": torch.get_num_threads(), "blas_threads": blas_threads, **info}
 
 
-def load_traffic(kind: str) -> float | None:
-    """HBM bytes per launch of the kernel behind `kind`, from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json), or None."""
-    p = ROOT / "profiles" / "traffic.json"
+def cpu_secondary() -> dict:
+    """CPU timings of the reference-equivalent PyTorch paths of configs 1, 3 and 4 (fp32,
+    torch on the host, the same threads as cpu_baseline): the WindowedAttention module
+    (qkv GEMM -> SDPA with the additive [S, S] band mask -> out GEMM), the dense masked
+    SDPA of config 3, and the dense-equivalent dX of config 4 on a row sample."""
+    n, _ = cpu_threads()
+    old = torch.get_num_threads()
+    torch.set_num_threads(n)
+    F = torch.nn.functional
+    from titans_core.attn.windowed_attention import build_band_mask
+    res = {}
     try:
-        return float(json.loads(p.read_text())[kind]["traffic_bytes"])
-    except (OSError, ValueError, KeyError, TypeError):
+        def med(fn, reps):
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+            return float(np.median(ts))
+
+        g = torch.Generator().manual_seed(1)
+        # config 1: B=2, T=512, d=512, H=8, w=256, Np=16 (persistent tokens part of the sequence)
+        B1, T1, d1, H1 = 2, 512, 512, 8
+        x = torch.randn(B1, T1, d1, generator=g)
+        wqkv = torch.randn(3 * d1, d1, generator=g) * 0.02
+        wout = torch.randn(d1, d1, generator=g) * 0.02
+        add1 = torch.zeros(T1, T1).masked_fill(~build_band_mask(T1, 256, 16, "cpu", True),
+                                               float("-inf"))
+
+        def cfg1():
+            q, k, v = F.linear(x, wqkv).chunk(3, dim=-1)
+            q, k, v = (t.reshape(B1, T1, H1, -1).transpose(1, 2) for t in (q, k, v))
+            o = F.scaled_dot_product_attention(q, k, v, attn_mask=add1)
+            return F.linear(o.transpose(1, 2).reshape(B1, T1, d1), wout)
+
+        t1 = med(cfg1, 20)
+        res["cfg1_windowed_attention_module_fp32_ms"] = round(t1 * 1e3, 3)
+        res["cfg1_tokens_per_s"] = round(B1 * T1 / t1, 1)
+        # config 3: dense masked SDPA, B=8, H=10, S=4096, dh=64 (343.6 GFLOP per call)
+        c = CFG3
+        S = c["S"]
+        q3, k3, v3 = (torch.randn(c["B"], c["H"], S, c["dh"], generator=g) for _ in range(3))
+        add3 = torch.zeros(S, S).masked_fill(~build_band_mask(S, c["window"], c["n_persistent"], "cpu",
+                                                              True), float("-inf"))
+        t3 = med(lambda: F.scaled_dot_product_attention(q3, k3, v3, attn_mask=add3), 2)
+        res["cfg3_dense_masked_sdpa_fp32_ms"] = round(t3 * 1e3, 1)
+        res["cfg3_tokens_per_s"] = round(c["B"] * S / t3, 1)
+        del q3, k3, v3, add3
+        # config 4: dX = dY . W^T dense-equivalent, 4096-row sample of dY [32768, 2560]
+        c4 = CFG4
+        dy = torch.randn(4096, BS * c4["n_bcol"], generator=g)
+        w4 = torch.randn(BS * c4["n_brow"], BS * c4["n_bcol"], generator=g)
+        t4 = med(lambda: dy @ w4.T, 10)
+        eff4 = 2 * 4096 * c4["n_brow"] * c4["width"] * BS * BS
+        res["cfg4_dx_dense_fp32_effective_tflops"] = round(eff4 / t4 / 1e12, 4)
+        res["threads"] = torch.get_num_threads()
+    finally:
+        torch.set_num_threads(old)
+    return res
+
+
+def measure_traffic(timeout_s: int = 150) -> dict | None:
+    """HBM bytes per launch of the config-2 SpMM forward, measured now on the current
+    build: two rocprofv3 counter runs (FETCH_SIZE, then WRITE_SIZE) of `bench.py --mode
+    traffic`, which launches a plain 1 GiB device copy and the SpMM kernel; each counter is
+    scaled by what it reads for the copy of known size. None (with a message on stderr)
+    when rocprofv3 is unavailable or a run fails."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        print("bench.py: rocprofv3 not found; roofline.traffic is null", file=sys.stderr)
         return None
+    vals = {}
+    with tempfile.TemporaryDirectory(prefix="tmac_traffic_") as tmp:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = Path(tmp) / counter
+            cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter, "-f", "csv",
+                   "-d", str(d), "-o", "run", "--", sys.executable, str(ROOT / "bench.py"),
+                   "--mode", "traffic"]
+            r = subprocess.run(cmd, capture_output=True, text=True, cwd=ROOT)
+            files = sorted(d.rglob("*counter_collection.csv"))
+            if r.returncode != 0 and not files:
+                print(f"bench.py: rocprofv3 {counter} run failed (rc {r.returncode}); "
+                      f"roofline.traffic is null\n{r.stderr[-1000:]}", file=sys.stderr)
+                return None
+            rows = [row for f in files for row in csv.DictReader(open(f))]
+            # the runtime splits each 1 GiB copy into several dispatches: the copy's figure
+            # is the sum over its dispatches per copy; the SpMM is one dispatch per launch
+            for kind, sub in (("copy", "copyBuffer"), ("spmm", "bell_")):
+                v = [float(row["Counter_Value"]) for row in rows
+                     if sub in row.get("Kernel_Name", "") and row.get("Counter_Name") == counter]
+                if not v:
+                    print(f"bench.py: no {counter} samples for {kind}; roofline.traffic is null",
+                          file=sys.stderr)
+                    return None
+                vals[(kind, counter)] = sum(v) / TRAFFIC_REPS if kind == "copy" else float(np.mean(v))
+    gib_kib = float(1 << 20)  # the copy reads and writes 1 GiB = 1,048,576 KiB
+    f_fetch = gib_kib / vals[("copy", "FETCH_SIZE")]
+    f_write = gib_kib / vals[("copy", "WRITE_SIZE")]
+    rd = vals[("spmm", "FETCH_SIZE")] * f_fetch * 1024
+    wr = vals[("spmm", "WRITE_SIZE")] * f_write * 1024
+    return {"traffic_bytes": rd + wr, "read_bytes": rd, "write_bytes": wr,
+            "fetch_scale": f_fetch, "write_scale": f_write,
+            "spmm_FETCH_SIZE_KiB": vals[("spmm", "FETCH_SIZE")],
+            "spmm_WRITE_SIZE_KiB": vals[("spmm", "WRITE_SIZE")]}
 
 
 def main() -> int:
@@ -515,8 +643,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 measurement of roofline.traffic (null)")
     ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "conv",
-                                                     "norm", "mac", "mac_ttm", "memupd", "copy"])
+                                                     "norm", "mac", "mac_ttm", "memupd", "copy",
+                                                     "traffic"])
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the hot path's kernels run on one MI355X and this "
@@ -529,6 +660,21 @@ def main() -> int:
     torch.cuda.set_device(dev)
     stream = torch.cuda.current_stream(dev)
     K, W = args.steps, args.warmup
+
+    if args.mode == "traffic":
+        # what measure_traffic's counter runs see: a 1 GiB device copy, then the SpMM
+        src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(TRAFFIC_REPS):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        spmm = setup_spmm(dev)
+        for _ in range(TRAFFIC_REPS):
+            spmm["launch"]()
+        torch.cuda.synchronize()
+        print(json.dumps({"mode": "traffic", "done": True}))
+        return 0
 
     if args.mode == "copy":
         src = torch.empty(1 << 29, dtype=torch.int16, device=dev).fill_(1)  # 1 GiB
@@ -608,7 +754,8 @@ def main() -> int:
     s = out["spmm"]
     a = out["attn"]
     dense_ms = min(a["sdpa_masked_ms"], a["bmm_softmax_bmm_ms"])
-    traffic = load_traffic("spmm")
+    tr = None if args.no_traffic else measure_traffic()
+    traffic = None if tr is None else round(tr["traffic_bytes"])
     line = {
         "metric": METRIC,
         "value": round(s["tflops"], 3),
@@ -673,8 +820,14 @@ def main() -> int:
             "neural_memory_update_cfg5_hbm_gbs_compulsory": round(out["memupd"]["gbs"], 1),
         },
     }
+    if tr is not None:
+        line["secondary"]["spmm_traffic_read_bytes"] = round(tr["read_bytes"])
+        line["secondary"]["spmm_traffic_write_bytes"] = round(tr["write_bytes"])
+        line["secondary"]["traffic_counter_scales"] = [round(tr["fetch_scale"], 4),
+                                                       round(tr["write_scale"], 4)]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(spmm)
+        line["secondary"]["cpu"] = cpu_secondary()
     print(json.dumps(line))
     return 0
 
