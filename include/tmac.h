@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 3
+#define TMAC_ABI_VERSION 4
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -64,6 +64,12 @@ typedef enum {
   TMAC_PATTERN_BAND = 0,    /* build_band_mask: attn/windowed_attention.py:97-152 */
   TMAC_PATTERN_BLOCKWIN = 1 /* BlockSparseAttention: attn/block_sparse_attention.py:277-334 */
 } tmac_pattern;
+
+/* Format of a caller's attention mask (tmac_attn_opts.mask_format). */
+typedef enum {
+  TMAC_MASK_BOOL = 0,    /* uint8, nonzero = attend (the reference's bool mask) */
+  TMAC_MASK_ADD_F32 = 1  /* fp32 added to the scaled scores (the reference's additive mask; -inf = masked) */
+} tmac_mask_format;
 
 /* Human-readable text for a return code (negative tmac_status or positive hipError_t). */
 const char* tmac_status_string(int code);
@@ -264,6 +270,86 @@ int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const int32_t* d_col_ptr, const int32_t* d_entries_kv,
                    const int32_t* d_order_kv, int n_lead_kv,
                    int dtype, void* stream);
+
+/* Options of tmac_wattn_fwd_ex / tmac_wattn_bwd_ex: a caller's attention mask
+ * and attention dropout. A zero-initialised struct (or a NULL pointer) means
+ * neither: the calls then equal tmac_wattn_fwd / tmac_wattn_bwd bit for bit. */
+typedef struct {
+  /* Caller's mask, replacing the pattern arguments (window, n_persistent,
+   * causal, pattern, block_size and the schedule arrays are then ignored and
+   * may be NULL), as WindowedAttention.forward's attn_mask replaces its band
+   * mask (attn/windowed_attention.py:307-315). [mask_batch, mask_heads, S, S]
+   * with element strides mask_strides (batch, head, query; keys contiguous);
+   * mask_batch is 1 (broadcast) or B, mask_heads 1 or H. NULL: no mask. A
+   * query row with no allowed key gets output 0, lse -inf and gradients 0. */
+  const void* d_mask;
+  int mask_format;          /* tmac_mask_format; fp32 masks 4-byte aligned */
+  int mask_batch, mask_heads;
+  int64_t mask_strides[3];  /* mask_strides[2] >= S */
+  /* Work lists of the mask: tmac_wattn_mask_workspace(S, mask_batch,
+   * mask_heads) bytes, 256-byte aligned, filled by tmac_wattn_mask_lists from
+   * this mask (on the stream, before the attention calls that use it). */
+  void* d_mask_ws;
+  size_t mask_ws_bytes;
+  /* Attention dropout after the softmax, F.scaled_dot_product_attention's
+   * dropout_p (attn/windowed_attention.py:318-323) and
+   * BlockSparseAttention's F.dropout of the weights
+   * (attn/block_sparse_attention.py:196-197): each probability of (b, h, q, k)
+   * is kept with probability 1 - p and scaled by 1 / (1 - p); the row sums
+   * (lse) use the undropped probabilities. The keep decision is the Philox
+   * 4x32-10 draw (Salmon et al., SC 2011) of counter
+   * {k / 4, q, b * H + h, 0} under key {seed low 32 bits, seed high 32 bits},
+   * word k % 4, compared with p * 2^32 (kept iff draw >= floor(p * 2^32)): the
+   * same seed gives the same mask in forward and backward. 0 <= p < 1. */
+  float dropout_p;
+  uint64_t dropout_seed;
+} tmac_attn_opts;
+
+/* Bytes of the work-list workspace of a mask of [mask_batch, mask_heads, S, S];
+ * 0 for a non-positive argument. No counterpart in the reference (which masks
+ * dense scores): lists of the 64-wide tiles each 128-row block visits. */
+size_t tmac_wattn_mask_workspace(int S, int mask_batch, int mask_heads);
+
+/* Builds the work lists of opts->d_mask into opts->d_mask_ws on `stream`
+ * (device work only, no host synchronisation): per (mask row, 128-query
+ * block) the 64-key tiles holding an allowed pair, and per (mask row,
+ * 128-key block) the 64-query tiles, each with a 2-bit kind per 32-wide
+ * slice (0 none allowed, 1 all allowed with bias 0, 2 mixed). Run it once per
+ * mask; forward and backward calls with that mask then reuse the lists. */
+int tmac_wattn_mask_lists(const tmac_attn_opts* opts, int S, void* stream);
+
+/* tmac_wattn_fwd with options (tmac_attn_opts): a caller's mask and/or
+ * dropout. Same kernels, templated on the options. */
+int tmac_wattn_fwd_ex(const void* d_Q, const int64_t q_strides[3],
+                      const void* d_K, const int64_t k_strides[3],
+                      const void* d_V, const int64_t v_strides[3],
+                      void* d_O, const int64_t o_strides[3], float* d_lse,
+                      int B, int H, int S, int dh, int window, int n_persistent,
+                      int causal, int pattern, int block_size, float scale,
+                      const int32_t* d_row_ptr, const int32_t* d_entries,
+                      const int32_t* d_order, int n_lead, int dtype, void* stream,
+                      const tmac_attn_opts* opts);
+
+/* tmac_wattn_bwd with options; the options (mask, dropout_p, dropout_seed)
+ * must be those of the forward whose lse is passed. With dropout, P·Z (Z the
+ * keep-and-scale factors) replaces P in dV = (P·Z)ᵀ·dO and
+ * dS = P ⊙ (Z ⊙ dO·Vᵀ − rowsum(dO ⊙ O)). */
+int tmac_wattn_bwd_ex(const void* d_Q, const int64_t q_strides[3],
+                      const void* d_K, const int64_t k_strides[3],
+                      const void* d_V, const int64_t v_strides[3],
+                      const void* d_O, const int64_t o_strides[3],
+                      const void* d_dO, const int64_t do_strides[3],
+                      const float* d_lse, float* d_delta,
+                      void* d_dQ, const int64_t dq_strides[3],
+                      void* d_dK, const int64_t dk_strides[3],
+                      void* d_dV, const int64_t dv_strides[3],
+                      int B, int H, int S, int dh, int window, int n_persistent,
+                      int causal, int pattern, int block_size, float scale,
+                      const int32_t* d_row_ptr, const int32_t* d_entries,
+                      const int32_t* d_order, int n_lead,
+                      const int32_t* d_col_ptr, const int32_t* d_entries_kv,
+                      const int32_t* d_order_kv, int n_lead_kv,
+                      int dtype, void* stream, const tmac_attn_opts* opts);
 
 /* Rows of the static scratch of tmac_wattn_bwd_noalloc (B*H*S at most). */
 #define TMAC_WATTN_BWD_SCRATCH_ROWS (4 * 1024 * 1024)

@@ -60,6 +60,68 @@ def masked_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.n
     return scale * (ds @ k), scale * (np.swapaxes(ds, -1, -2) @ q), dv
 
 
+def biased_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarray,
+                     scale: float | None = None, drop: np.ndarray | None = None,
+                     dtype=np.float64, return_lse: bool = False):
+    """softmax(q·kᵀ·scale + bias), times the dropout factors `drop` when given, ·v.
+
+    WindowedAttention.forward with a caller's attn_mask (attn/windowed_attention.py
+    :307-323): a bool mask becomes the additive bias 0 / -inf (:311-313), a float
+    mask is added as it is (:315), and SDPA adds it to the scaled scores; dropout
+    (dropout_p in training) multiplies the probabilities after the softmax by 0 or
+    1 / (1 - p). bias and drop broadcast against the [..., S_q, S_k] scores. A row
+    whose every key is masked gives output 0 and lse -inf, as torch's SDPA does.
+    The row sums (lse) use the undropped probabilities.
+    """
+    q = np.asarray(q, dtype=dtype)
+    k = np.asarray(k, dtype=dtype)
+    v = np.asarray(v, dtype=dtype)
+    if scale is None:
+        scale = 1.0 / np.sqrt(q.shape[-1])
+    s = (q @ np.swapaxes(k, -1, -2)) * scale + np.asarray(bias, dtype=dtype)
+    m = s.max(axis=-1, keepdims=True)
+    dead = ~np.isfinite(m)  # every key masked
+    p = np.exp(s - np.where(dead, 0.0, m))
+    den = p.sum(axis=-1, keepdims=True)
+    pd = p if drop is None else p * np.asarray(drop, dtype=dtype)
+    out = (pd @ v) / np.where(dead, 1.0, den)
+    if return_lse:
+        with np.errstate(divide="ignore"):
+            return out, np.where(dead, -np.inf, m + np.log(den))[..., 0]
+    return out
+
+
+def biased_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.ndarray,
+                           bias: np.ndarray, scale: float | None = None,
+                           drop: np.ndarray | None = None, dtype=np.float64,
+                           out: np.ndarray | None = None):
+    """(dq, dk, dv) of biased_attention for the output gradient `do`.
+
+    With P = softmax(S), S = q·kᵀ·scale + bias, Z the dropout factors (1 without
+    dropout) and O = (P ⊙ Z)·v: dV = (P ⊙ Z)ᵀ·dO, dP' = dO·Vᵀ, Δ = rowsum(dO ⊙ O)
+    (= rowsum(P ⊙ Z ⊙ dP')), dS = P ⊙ (Z ⊙ dP' − Δ), dq = scale·dS·k,
+    dk = scale·dSᵀ·q. Fully masked rows get no gradient. `out`, when given, is
+    the forward output as stored (e.g. rounded to 16 bits) and enters Δ in place
+    of the exact O, as the saved output does in SDPA's backward.
+    """
+    q, k, v, do = (np.asarray(t, dtype=dtype) for t in (q, k, v, do))
+    if scale is None:
+        scale = 1.0 / np.sqrt(q.shape[-1])
+    s = (q @ np.swapaxes(k, -1, -2)) * scale + np.asarray(bias, dtype=dtype)
+    m = s.max(axis=-1, keepdims=True)
+    dead = ~np.isfinite(m)
+    p = np.exp(s - np.where(dead, 0.0, m))
+    p /= np.where(dead, 1.0, p.sum(axis=-1, keepdims=True))
+    z = np.ones_like(p) if drop is None else np.broadcast_to(np.asarray(drop, dtype=dtype), p.shape)
+    pz = p * z
+    o = pz @ v if out is None else np.asarray(out, dtype=dtype)
+    dv = np.swapaxes(pz, -1, -2) @ do
+    dp = do @ np.swapaxes(v, -1, -2)
+    delta = (do * o).sum(axis=-1, keepdims=True)
+    ds = p * (z * dp - delta)
+    return scale * (ds @ k), scale * (np.swapaxes(ds, -1, -2) @ q), dv
+
+
 def windowed_attention_module(x: np.ndarray, w_qkv: np.ndarray, w_out: np.ndarray, n_heads: int,
                               window_size: int, n_persistent: int, causal: bool = True,
                               dtype=np.float64) -> np.ndarray:

@@ -1,0 +1,75 @@
+"""Attention dropout keep decisions (numpy) — TEST INFRASTRUCTURE ONLY.
+
+The reference drops attention probabilities with torch's own generator
+(F.scaled_dot_product_attention(dropout_p=...) in WindowedAttention.forward,
+attn/windowed_attention.py:318-323, and F.dropout of the weights in
+BlockSparseAttention, attn/block_sparse_attention.py:196-197): each probability
+is zeroed with probability p and the kept ones scaled by 1 / (1 - p). Which
+entries are dropped is not reproducible across libraries, so the drop-in keeps
+the distribution and draws its decisions from a counter-based generator that
+forward and backward can both recompute from a seed:
+
+Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+1, 2, 3", SC 2011): 10 rounds on a 4x32-bit counter under a 2x32-bit key,
+round multipliers 0xD2511F53 and 0xCD9E8D57, Weyl key increments 0x9E3779B9
+and 0xBB67AE85. Pinned by the Random123 known-answer vectors (tests).
+
+Decision of pair (bh, q, k) for seed s and probability p: counter
+{k // 4, q, bh, 0}, key {s mod 2^32, s // 2^32}, output word k % 4; kept iff
+word >= floor(p · 2^32) (p as float32, then exact).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+M0, M1 = 0xD2511F53, 0xCD9E8D57
+W0, W1 = 0x9E3779B9, 0xBB67AE85
+_MASK32 = np.uint64(0xFFFFFFFF)
+
+
+def philox4x32_10(ctr: np.ndarray, key) -> np.ndarray:
+    """Philox4x32-10 of counters ctr [..., 4] (uint32) under key (k0, k1); returns [..., 4] uint32."""
+    c = [np.asarray(ctr[..., i], dtype=np.uint64) for i in range(4)]
+    k0, k1 = np.uint64(int(key[0]) & 0xFFFFFFFF), np.uint64(int(key[1]) & 0xFFFFFFFF)
+    for r in range(10):
+        if r:
+            k0 = (k0 + np.uint64(W0)) & _MASK32
+            k1 = (k1 + np.uint64(W1)) & _MASK32
+        p0 = c[0] * np.uint64(M0)  # full 64-bit products of 32-bit operands
+        p1 = c[2] * np.uint64(M1)
+        hi0, lo0 = p0 >> np.uint64(32), p0 & _MASK32
+        hi1, lo1 = p1 >> np.uint64(32), p1 & _MASK32
+        c = [hi1 ^ c[1] ^ k0, lo1, hi0 ^ c[3] ^ k1, lo0]
+    return np.stack([x.astype(np.uint32) for x in c], axis=-1)
+
+
+def threshold(p: float) -> int:
+    """floor(p · 2^32) of p rounded to float32, clamped to 2^32 - 1."""
+    t = np.floor(float(np.float32(p)) * 4294967296.0)
+    return int(min(t, 4294967295.0))
+
+
+def keep_mask(bh: int, rows: np.ndarray, cols: np.ndarray, seed: int, p: float) -> np.ndarray:
+    """bool [len(rows), len(cols)]: whether pair (bh, q, k) survives dropout p."""
+    rows = np.asarray(rows, dtype=np.int64)
+    cols = np.asarray(cols, dtype=np.int64)
+    ctr = np.zeros((rows.size, cols.size, 4), dtype=np.uint32)
+    ctr[..., 0] = (cols // 4)[None, :]
+    ctr[..., 1] = rows[:, None]
+    ctr[..., 2] = bh
+    out = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))
+    word = np.take_along_axis(out, np.broadcast_to((cols % 4)[None, :, None],
+                                                   (rows.size, cols.size, 1)), axis=-1)[..., 0]
+    return word >= np.uint32(threshold(p)) if threshold(p) < 2**32 else np.zeros(word.shape, bool)
+
+
+def drop_factors(B: int, H: int, S: int, seed: int, p: float, rows=None) -> np.ndarray:
+    """float64 [B, H, len(rows), S]: 1 / (1 - p) where kept, else 0 (rows default: all)."""
+    rows = np.arange(S) if rows is None else np.asarray(rows)
+    scale = 1.0 / (1.0 - float(np.float32(p)))
+    z = np.empty((B, H, rows.size, S))
+    cols = np.arange(S)
+    for b in range(B):
+        for h in range(H):
+            z[b, h] = keep_mask(b * H + h, rows, cols, seed, p) * scale
+    return z

@@ -113,9 +113,11 @@ def schedule(mask: np.ndarray, q_block: int = 128, sub_rows: int = 32, k_tile: i
     entries = k_tile_index | (kind of sub-slice j) << (16 + 2j), listed for every
     key tile with a non-empty sub-slice, ascending per query block.
     """
-    S = mask.shape[0]
+    return _lists_from_kinds(tile_kinds(mask, sub_rows, k_tile), mask.shape[0], q_block, sub_rows)
+
+
+def _lists_from_kinds(kinds: np.ndarray, S: int, q_block: int, sub_rows: int):
     n_sub = q_block // sub_rows
-    kinds = tile_kinds(mask, sub_rows, k_tile)
     n_qb = -(-S // q_block)
     n_sub_total = kinds.shape[0]
     row_ptr = [0]
@@ -131,6 +133,27 @@ def schedule(mask: np.ndarray, q_block: int = 128, sub_rows: int = 32, k_tile: i
                 entries.append(kt | (word << 16))
         row_ptr.append(len(entries))
     return np.asarray(row_ptr, dtype=np.int32), np.asarray(entries, dtype=np.int64).astype(np.int32)
+
+
+def bias_tile_kinds(bias: np.ndarray, tq: int, tk: int) -> np.ndarray:
+    """tile_kinds of a caller's additive mask (bool masks as 0 / -inf): 0 when every
+    pair is -inf, 1 when every pair has bias exactly 0, else 2 (the kernel then
+    adds the bias element by element). Positions past S count as masked."""
+    bias = np.asarray(bias)
+    if bias.dtype == bool:
+        allowed, zero = bias, bias
+    else:
+        allowed, zero = bias != -np.inf, bias == 0
+    ka, kz = tile_kinds(allowed, tq, tk), tile_kinds(zero, tq, tk)
+    return np.where(kz == FULL, FULL, np.where(ka == EMPTY, EMPTY, PARTIAL)).astype(np.uint8)
+
+
+def schedule_bias(bias: np.ndarray, q_block: int = 128, sub_rows: int = 32, k_tile: int = 64):
+    """schedule() of a caller's mask [S, S] (bool or additive float): the query-major
+    work list tmac_wattn_mask_lists builds on the device for one mask row. The
+    key-major list is schedule_bias of the transposed mask."""
+    return _lists_from_kinds(bias_tile_kinds(bias, sub_rows, k_tile), bias.shape[0], q_block,
+                             sub_rows)
 
 
 def schedule_kv(mask: np.ndarray, k_block: int = 128, sub_cols: int = 32, q_tile: int = 64):

@@ -80,8 +80,12 @@ def test_hot_path_refuses_cpu_tensors():
     a = WindowedAttention(WindowConfig(window_size=8, num_heads=2, head_dim=64, n_persistent=2))
     with pytest.raises(RuntimeError, match="runs only on the GPU"):
         a(torch.randn(1, 16, 128))
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="runs only on the GPU"):
         a(torch.randn(1, 16, 128), attn_mask=torch.ones(16, 16, dtype=torch.bool))
+    a.train()
+    a.dropout_p = 0.1
+    with pytest.raises(RuntimeError, match="runs only on the GPU"):
+        a(torch.randn(1, 16, 128))
     lin = BlockELLLinear(128, 128, density=0.5).to(torch.bfloat16)
     with pytest.raises(RuntimeError, match="runs only on the GPU"):
         lin(torch.randn(3, 128).to(torch.bfloat16))

@@ -1,0 +1,287 @@
+"""GPU parity of attention with a caller's mask and with attention dropout.
+
+A caller's attn_mask (bool, True = attend, or additive float; [S, S],
+[H|1, S, S] or [B|1, H|1, S, S]) replaces the band / block-window pattern, as
+WindowedAttention.forward's attn_mask does (attn/windowed_attention.py:307-315);
+dropout_p drops probabilities after the softmax (SDPA's dropout_p, :321;
+BlockSparseAttention's F.dropout, attn/block_sparse_attention.py:196-197).
+
+Oracle: oracle.attention.biased_attention / biased_attention_grads (pinned
+against torch SDPA and autograd in test_oracle_dropout.py) with the dropout
+factors of oracle.dropout (Philox4x32-10, pinned by the Random123 known-answer
+vectors), so the kernels' keep decisions are checked exactly, not statistically.
+Bars: 16-bit |got - want| <= 2e-2 + 1e-2 |want| after division of both by
+max(1, max |want|), with Δ = rowsum(dO ⊙ O) of the gradients taken from the
+16-bit output the forward stored (as SDPA's backward takes its saved output:
+with dropout, O is not a multiple of one V row even where a row attends one
+key, and the exact-O Δ would leave a 16-bit cancellation residue that sums over
+every row attending a key); fp32 within 1e-4 of the largest entry. The device work
+lists of a mask are checked bit for bit against oracle.masks.schedule_bias.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import dropout as od
+from oracle import masks as om
+from titans_core.kernels import _lib
+from titans_core.kernels import window_attn as wa
+from titans_core.kernels.window_attn import windowed_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def close(got, want, atol=2e-2, rtol=1e-2, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    sc = max(1.0, float(np.abs(want).max())) if want.size else 1.0
+    got, want = got / sc, want / sc
+    err = np.abs(got - want)
+    ok = err <= atol + rtol * np.abs(want)
+    assert ok.all(), f"{what} max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+def close_f32(got, want, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    sc = max(1.0, float(np.abs(want).max()))
+    err = np.abs(got - want).max() / sc
+    assert err <= 1e-4, f"{what} max err {err:.3g}"
+
+
+def tensors(shape, dtype, seed, n=4):
+    g = torch.Generator().manual_seed(seed)
+    return [torch.randn(*shape, generator=g).to(dtype) for _ in range(n)]
+
+
+def random_bool_mask(rng, lead, S):
+    """Random structure with every tile kind: dense random pairs, an all-True
+    square, an all-False band of rows, a fully masked row, the diagonal."""
+    m = rng.random(lead + (S, S)) < 0.35
+    m |= np.eye(S, dtype=bool)
+    if S > 130:
+        m[..., 64:128, 0:128] = True          # full 32x64 slices (kind 1)
+        m[..., 128:192, :] = False            # empty slices (kind 0) ...
+        m[..., 128:192, 130] = True           # ... next to one partial column
+    if S > 5:
+        m[..., 5, :] = False                  # a row with every key masked
+    return m
+
+
+def random_bias(rng, lead, S):
+    m = random_bool_mask(rng, lead, S)
+    b = np.where(m, rng.standard_normal(lead + (S, S)) * 1.5, -np.inf)
+    if S > 130:
+        b[..., 64:128, 0:128] = 0.0           # bias exactly 0: kind 1
+    return b
+
+
+def as_bias(mask):
+    return np.where(mask, 0.0, -np.inf) if mask.dtype == bool else mask
+
+
+def oracle_fwd_bwd(q, k, v, do, bias, scale, z, out=None):
+    """Per (b, h) oracle with broadcasting of the mask's leading dims. `out`: the
+    forward output as the GPU stored it, for Δ = rowsum(dO ⊙ O) of the gradients
+    (SDPA's backward also takes its saved 16-bit output)."""
+    B, H = q.shape[:2]
+    b4 = np.broadcast_to(bias.reshape((1,) * (4 - bias.ndim) + bias.shape), (B, H) + bias.shape[-2:])
+    o = np.empty(q.shape)
+    g = [np.empty(q.shape) for _ in range(3)]
+    for b in range(B):
+        for h in range(H):
+            zz = None if z is None else z[b, h]
+            o[b, h] = oa.biased_attention(q[b, h], k[b, h], v[b, h], b4[b, h], scale, zz)
+            if do is not None:
+                ob = None if out is None else out[b, h]
+                for t, r in zip(g, oa.biased_attention_grads(q[b, h], k[b, h], v[b, h], do[b, h],
+                                                              b4[b, h], scale, zz, out=ob)):
+                    t[b, h] = r
+    return o, g
+
+
+def run(dev, q, k, v, do, mask_t, p, seed, w=0, Np=0, pattern="band", bs=64, scale=None):
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = windowed_attention(qd, kd, vd, w, Np, True, pattern, bs, scale,
+                           attn_mask=None if mask_t is None else mask_t.to(dev),
+                           dropout_p=p, seed=seed)
+    o.backward(do.to(dev))
+    return [t.detach().float().cpu().numpy() for t in (o, qd.grad, kd.grad, vd.grad)]
+
+
+MASK_CASES = [  # B, H, S, dh, mask leading dims, kind
+    (1, 1, 1, 64, (), "bool"), (1, 2, 17, 64, (), "bool"), (2, 2, 200, 64, (), "bool"),
+    (2, 3, 300, 64, (2, 3), "bool"), (2, 2, 257, 64, (2, 1), "float"), (1, 3, 333, 32, (3,), "float"),
+    (1, 2, 260, 128, (), "float"), (2, 1, 129, 64, (1, 1), "bool")]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("B,H,S,dh,lead,kind", MASK_CASES)
+def test_caller_mask_fwd_bwd(dev, dtype, B, H, S, dh, lead, kind):
+    rng = np.random.default_rng(S + dh + len(lead))
+    mask = random_bool_mask(rng, lead, S) if kind == "bool" else random_bias(rng, lead, S)
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=S)
+    mt = torch.from_numpy(mask)
+    o, dq, dk, dv = run(dev, q, k, v, do, mt, 0.0, 0)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), as_bias(mask),
+                            1.0 / np.sqrt(dh), None, None if dtype == torch.float32 else o)
+    chk = close_f32 if dtype == torch.float32 else close
+    chk(o, wo, what="out")
+    for got, want, name in zip((dq, dk, dv), wg, "qkv"):
+        chk(got, want, what=f"d{name}")
+    if S > 5:
+        assert np.all(o[..., 5, :] == 0)      # the fully masked row
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,S,w,Np,pattern,bs,p", [
+    (1, 2, 200, 64, 4, "band", 64, 0.1), (2, 2, 300, 100, 5, "band", 64, 0.5),
+    (1, 1, 333, 128, 16, "blockwin", 64, 0.3), (1, 2, 129, 1000, 0, "band", 64, 0.9)])
+def test_dropout_with_pattern(dev, dtype, B, H, S, w, Np, pattern, bs, p):
+    q, k, v, do = tensors((B, H, S, 64), dtype, seed=7 * S)
+    seed = 0x1234_5678_9ABC + S
+    o, dq, dk, dv = run(dev, q, k, v, do, None, p, seed, w, Np, pattern, bs)
+    mask = om.make_mask(S, w, Np, True, pattern, bs)
+    z = od.drop_factors(B, H, S, seed, p)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), as_bias(mask), 0.125, z,
+                            None if dtype == torch.float32 else o)
+    chk = close_f32 if dtype == torch.float32 else close
+    chk(o, wo, what="out")
+    for got, want, name in zip((dq, dk, dv), wg, "qkv"):
+        chk(got, want, what=f"d{name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_dropout_with_caller_mask(dev, dtype):
+    B, H, S, dh, p = 2, 2, 260, 64, 0.25
+    rng = np.random.default_rng(11)
+    bias = random_bias(rng, (2, 1), S)
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=13)
+    seed = 987654321987
+    o, dq, dk, dv = run(dev, q, k, v, do, torch.from_numpy(bias).float(), p, seed)
+    z = od.drop_factors(B, H, S, seed, p)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), bias, 0.125, z,
+                            None if dtype == torch.float32 else o)
+    chk = close_f32 if dtype == torch.float32 else close
+    chk(o, wo, what="out")
+    for got, want, name in zip((dq, dk, dv), wg, "qkv"):
+        chk(got, want, what=f"d{name}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_options_off_is_plain_path_bit_for_bit(dev, dtype):
+    """tmac_wattn_fwd_ex / _bwd_ex without mask or dropout = tmac_wattn_fwd / _bwd."""
+    q, k, v, do = (t.to(dev) for t in tensors((2, 3, 300, 64), dtype, seed=3))
+    args = (100, 5, True, _lib.PATTERN_BAND, 64, 0.125)
+    o1, l1 = wa._window_attn_fwd(q, k, v, *args, need_lse=True)
+    o2, l2, _ = wa._window_attn_fwd_ex(q, k, v, None, *args, 0.0, 0, need_lse=True)
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    g1 = wa._window_attn_bwd(do.transpose(1, 2).contiguous(), q, k, v, o1, l1, *args)
+    g2 = wa._window_attn_bwd_ex(do.transpose(1, 2).contiguous(), q, k, v, o1, l1, None,
+                                torch.empty(0, dtype=torch.uint8, device=dev), *args, 0.0, 0)
+    for a, b in zip(g1, g2):
+        assert torch.equal(a, b)
+
+
+def test_seed_reproducible_and_distinct(dev):
+    q, k, v, _ = (t.to(dev) for t in tensors((1, 2, 256, 64), torch.bfloat16, seed=4))
+    a = windowed_attention(q, k, v, 64, 4, dropout_p=0.3, seed=42)
+    b = windowed_attention(q, k, v, 64, 4, dropout_p=0.3, seed=42)
+    c = windowed_attention(q, k, v, 64, 4, dropout_p=0.3, seed=43)
+    assert torch.equal(a, b) and not torch.equal(a, c)
+    torch.manual_seed(0)
+    d = windowed_attention(q, k, v, 64, 4, dropout_p=0.3)
+    torch.manual_seed(0)
+    e = windowed_attention(q, k, v, 64, 4, dropout_p=0.3)
+    assert torch.equal(d, e)
+
+
+def test_broadcast_mask_forms_agree_bit_for_bit(dev):
+    """[S, S], [1, 1, S, S], [H, S, S] with equal heads, and an expanded [B, H, S, S]
+    view (stride 0, not copied) give the same bits."""
+    B, H, S = 2, 3, 200
+    rng = np.random.default_rng(5)
+    m = torch.from_numpy(random_bool_mask(rng, (), S)).to(dev)
+    q, k, v, _ = (t.to(dev) for t in tensors((B, H, S, 64), torch.bfloat16, seed=5))
+    ref = windowed_attention(q, k, v, 0, 0, attn_mask=m)
+    for form in (m[None, None], m.expand(B, H, S, S), m[None].repeat(H, 1, 1),
+                 m[None, None].repeat(B, H, 1, 1)):
+        assert torch.equal(windowed_attention(q, k, v, 0, 0, attn_mask=form), ref)
+    bias = torch.zeros(S, S, device=dev).masked_fill(~m, float("-inf"))
+    close(windowed_attention(q, k, v, 0, 0, attn_mask=bias).float().cpu(), ref.float().cpu(),
+          what="additive 0/-inf vs bool")
+    assert torch.equal(windowed_attention(q, k, v, 0, 0, attn_mask=bias.to(torch.bfloat16)),
+                       windowed_attention(q, k, v, 0, 0, attn_mask=bias))
+
+
+def test_band_mask_as_caller_mask_matches_pattern(dev):
+    """The band mask passed as a tensor agrees with the in-kernel band pattern (both
+    within the bar of the oracle; not bit for bit: the mask path adds a bias term)."""
+    B, H, S, w, Np = 1, 4, 1024, 256, 16
+    q, k, v, do = tensors((B, H, S, 64), torch.bfloat16, seed=8)
+    mask = om.band_mask(S, w, Np)
+    a = run(dev, q, k, v, do, torch.from_numpy(mask), 0.0, 0)
+    b = run(dev, q, k, v, do, None, 0.0, 0, w, Np)
+    for x, y, name in zip(a, b, ("out", "dq", "dk", "dv")):
+        close(x, y, what=name)
+
+
+@pytest.mark.parametrize("lead,kind", [((), "bool"), ((2, 3), "float"), ((1, 3), "bool")])
+@pytest.mark.parametrize("S", [1, 64, 200, 333])
+def test_device_work_lists_bit_exact(dev, lead, kind, S):
+    B, H = 2, 3
+    rng = np.random.default_rng(S)
+    mask = random_bool_mask(rng, lead, S) if kind == "bool" else random_bias(rng, lead, S)
+    mt = torch.from_numpy(mask).to(dev)
+    if kind == "float":
+        mt = mt.float()
+    (m, fmt, mb, mh, strides), ws = wa.mask_work_lists(mt, B, H, S)
+    torch.cuda.synchronize()
+    raw = ws.cpu().numpy()
+    n_b, n_t = -(-S // 128), -(-S // 64)
+    rows = mb * mh * n_b
+    kinds = (n_b * 4 + 255) // 256 * 256
+    ent_off = kinds + (2 * rows * n_t + 255) // 256 * 256
+    cnt_off = ent_off + (2 * rows * n_t * 4 + 255) // 256 * 256
+    ent = raw[ent_off:ent_off + 2 * rows * n_t * 4].view(np.int32).reshape(2, rows, n_t)
+    cnt = raw[cnt_off:cnt_off + 2 * rows * 4].view(np.int32).reshape(2, rows)
+    assert np.array_equal(raw[:n_b * 4].view(np.int32), np.arange(n_b))
+    m4 = mask.reshape((1,) * (4 - mask.ndim) + mask.shape)
+    for r in range(mb * mh):
+        one = m4[r // mh, r % mh] if m4.shape[0] > 1 else m4[0, r % mh]
+        for side, mm in ((0, one), (1, np.ascontiguousarray(one.T))):
+            rp, e = om.schedule_bias(mm)
+            for blk in range(n_b):
+                row = r * n_b + blk
+                want = e[rp[blk]:rp[blk + 1]]
+                assert cnt[side, row] == want.size, (side, r, blk)
+                assert np.array_equal(ent[side, row, :want.size], want), (side, r, blk)
+
+
+def test_module_dropout_train_and_eval(dev):
+    import titans_core as tc
+    torch.manual_seed(0)
+    cfg = tc.attn.windowed_attention.WindowConfig(window_size=64, num_heads=4, head_dim=64,
+                                                  n_persistent=4, dropout=0.2)
+    m = tc.attn.windowed_attention.WindowedAttention(cfg).to(dev, torch.bfloat16)
+    x = torch.randn(2, 256, 256, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    m.train()
+    y = m(x)
+    y.float().square().mean().backward()
+    assert torch.isfinite(y).all() and torch.isfinite(x.grad).all()
+    m.eval()
+    with torch.no_grad():
+        e1 = m(x)
+        mask = tc.attn.windowed_attention.build_band_mask(256, 64, 4, str(dev))
+        e2 = m(x, attn_mask=mask)
+    close(e1.float().cpu(), e2.float().cpu(), what="band mask as attn_mask")
+
+
+def test_block_sparse_module_dropout_trains(dev):
+    import titans_core as tc
+    torch.manual_seed(1)
+    m = tc.attn.block_sparse_attention.BlockSparseAttention(256, 4, 128, 64, 8, dropout=0.1)
+    m = m.to(dev, torch.bfloat16).train()
+    x = torch.randn(2, 300, 256, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    m(x).float().square().mean().backward()
+    assert torch.isfinite(x.grad).all()

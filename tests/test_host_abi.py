@@ -29,7 +29,8 @@ def test_library_exports_every_declared_symbol(lib):
     assert len(names) >= 12
     for n in names:
         assert hasattr(lib, n), n
-        assert n in _lib.SIGNATURES or n == "tmac_status_string", f"{n} has no ctypes signature"
+        assert n in _lib.SIGNATURES or n in ("tmac_status_string", "tmac_wattn_mask_workspace"), \
+            f"{n} has no ctypes signature"
     assert lib.tmac_abi_version() == _lib.ABI_VERSION
 
 
@@ -348,3 +349,71 @@ def test_mask_spans_and_launch_order_edges(lib):
     lead = ctypes.c_int(-1)
     rc = lib.tmac_wattn_launch_order(ptr.ctypes.data, 0, order.ctypes.data, ctypes.byref(lead))
     assert rc in (0, -2)
+
+
+def test_mask_workspace_size(lib):
+    for S, mb, mh in [(1, 1, 1), (4096, 1, 1), (4096, 4, 10), (300, 2, 1), (129, 1, 3)]:
+        n = lib.tmac_wattn_mask_workspace(S, mb, mh)
+        n_b, n_t = -(-S // 128), -(-S // 64)
+        rows = mb * mh * n_b
+        assert n % 256 == 0
+        assert n >= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4
+        assert n <= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + 4 * 256
+    for bad in [(0, 1, 1), (64, 0, 1), (64, 1, 0), (-5, 1, 1)]:
+        assert lib.tmac_wattn_mask_workspace(*bad) == 0
+
+
+def _opts(**kw):
+    from titans_core.kernels.window_attn import AttnOpts
+    o = AttnOpts()
+    for k, v in kw.items():
+        if k == "mask_strides":
+            o.mask_strides[0], o.mask_strides[1], o.mask_strides[2] = v
+        else:
+            setattr(o, k, v)
+    return o
+
+
+def test_wattn_ex_option_errors(lib):
+    """Option checks of tmac_wattn_fwd_ex / _bwd_ex / _mask_lists (nothing is launched)."""
+    st = (ctypes.c_int64 * 3)(4096 * 1920, 64, 1920)
+    S = 4096
+    fwd = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, None, 8, 10, S, 64, 512, 16, 1, 0, 64, 0.125,
+           FAKE, FAKE, FAKE, 0, 1, None]
+    bwd = [FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, st, FAKE, FAKE, FAKE, st, FAKE, st,
+           FAKE, st, 8, 10, S, 64, 512, 16, 1, 0, 64, 0.125, FAKE, FAKE, FAKE, 1,
+           FAKE, FAKE, FAKE, 1, 1, None]
+    ws_ok = lib.tmac_wattn_mask_workspace(S, 1, 1)
+    good_mask = dict(d_mask=1 << 20, mask_format=0, mask_batch=1, mask_heads=1,
+                     mask_strides=(0, 0, S), d_mask_ws=1 << 24, mask_ws_bytes=ws_ok)
+    cases = [
+        (dict(dropout_p=1.0), -8), (dict(dropout_p=-0.1), -8), (dict(dropout_p=float("nan")), -8),
+        (dict(good_mask, mask_format=7), -4),
+        (dict(good_mask, mask_batch=3), -2), (dict(good_mask, mask_heads=4), -2),
+        (dict(good_mask, mask_strides=(0, 0, S - 1)), -2),
+        (dict(good_mask, mask_strides=(-1, 0, S)), -2),
+        (dict(good_mask, d_mask_ws=None), -6), (dict(good_mask, mask_ws_bytes=ws_ok - 1), -6),
+        (dict(good_mask, d_mask_ws=(1 << 24) + 16), -5),
+        (dict(good_mask, mask_format=1, d_mask=(1 << 20) + 2), -5),
+    ]
+    for kw, want in cases:
+        o = _opts(**kw)
+        assert lib.tmac_wattn_fwd_ex(*fwd, ctypes.byref(o)) == want, kw
+        assert lib.tmac_wattn_bwd_ex(*bwd, ctypes.byref(o)) == want, kw
+    # with a mask the pattern arguments are not checked, but the rest still is
+    o = _opts(**dict(good_mask, dropout_p=2.0))
+    a = list(fwd); a[14] = S   # n_persistent = S: invalid for the band pattern, unused here
+    assert lib.tmac_wattn_fwd_ex(*a, ctypes.byref(o)) == -8   # the dropout_p
+    a = list(fwd); a[12] = 48
+    assert lib.tmac_wattn_fwd_ex(*a, ctypes.byref(_opts(**good_mask))) == -2
+    # without a mask the schedule arrays are required
+    a = list(bwd); a[28] = None
+    assert lib.tmac_wattn_bwd_ex(*a, ctypes.byref(_opts())) == -1
+    # tmac_wattn_mask_lists
+    assert lib.tmac_wattn_mask_lists(None, S, None) == -1
+    assert lib.tmac_wattn_mask_lists(ctypes.byref(_opts()), S, None) == -1
+    assert lib.tmac_wattn_mask_lists(ctypes.byref(_opts(**good_mask)), 0, None) == -2
+    assert lib.tmac_wattn_mask_lists(ctypes.byref(_opts(**dict(good_mask, mask_format=5))),
+                                     S, None) == -4
+    assert lib.tmac_wattn_mask_lists(ctypes.byref(_opts(**dict(good_mask, mask_ws_bytes=8))),
+                                     S, None) == -6

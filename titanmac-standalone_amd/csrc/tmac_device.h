@@ -227,6 +227,92 @@ __host__ __device__ inline Span mask_col_span(const MaskParams& p, int j) {
   return s;
 }
 
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+// 1, 2, 3", SC 2011): ten rounds of a keyed bijection on a 128-bit counter; the
+// multipliers and Weyl increments are the paper's. Attention dropout draws one
+// call per (query, group of 4 keys, batch*head): counter {key / 4, query, bh, 0},
+// key {seed low, seed high}; output word key % 4 decides (query, key).
+struct U32x4 {
+  uint32_t x, y, z, w;
+};
+__host__ __device__ inline uint32_t mulhi32(uint32_t a, uint32_t b) {
+  return static_cast<uint32_t>((static_cast<uint64_t>(a) * b) >> 32);
+}
+__host__ __device__ inline U32x4 philox4x32_10(U32x4 c, uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = mulhi32(0xD2511F53u, c.x), lo0 = 0xD2511F53u * c.x;
+    const uint32_t hi1 = mulhi32(0xCD9E8D57u, c.z), lo1 = 0xCD9E8D57u * c.z;
+    c = U32x4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c;
+}
+
+// Extra features of the attention kernels (template flag bits): a caller's mask
+// tensor instead of the band / block-window pattern (kFeatMask), attention dropout
+// (kFeatDrop).
+constexpr int kFeatMask = 1, kFeatDrop = 2;
+
+struct AttnX {
+  const void* mask;      // TMAC_MASK_BOOL: uint8 (0 = masked); TMAC_MASK_ADD_F32: fp32 added to the scores
+  int fmt;
+  int64_t msb, msh, msq; // element strides of the mask's batch, head, query dims (key stride 1)
+  int mb1, mh1, MH;      // batch / head dims of size 1 (broadcast); number of mask heads
+  const int32_t* cnt;    // custom work lists: entries of each list row
+  int cap;               // entries a list row can hold (row r starts at r * cap)
+  uint32_t seed0, seed1; // dropout seed
+  uint32_t thresh;       // dropped when the 32-bit draw is below thresh (= p * 2^32)
+  float keep_scale;      // 1 / (1 - p)
+};
+
+// Row of the custom work lists of (b, head): the mask's own (batch, head) row.
+__device__ __forceinline__ int mask_row(const AttnX& x, int b, int hd) {
+  return (x.mb1 ? 0 : b) * x.MH + (x.mh1 ? 0 : hd);
+}
+
+// Natural-log bias the caller's mask adds to score (q, k): 0 or -inf for a bool
+// mask; positions at or past S are masked.
+__device__ __forceinline__ float mask_bias(const AttnX& x, int b, int hd, int q, int k, int S) {
+  if (q >= S || k >= S) return -INFINITY;
+  const int64_t off = (x.mb1 ? 0 : static_cast<int64_t>(b) * x.msb) +
+                      (x.mh1 ? 0 : static_cast<int64_t>(hd) * x.msh) +
+                      static_cast<int64_t>(q) * x.msq + k;
+  if (x.fmt == TMAC_MASK_BOOL) return static_cast<const uint8_t*>(x.mask)[off] ? 0.f : -INFINITY;
+  return static_cast<const float*>(x.mask)[off];
+}
+
+// Dropout factor of (bh, q, k) for each of the four keys k0..k0+3 (k0 a multiple
+// of 4): keep_scale or 0.
+__device__ __forceinline__ void drop4(const AttnX& x, int bh, int q, int k0, float (&z)[4]) {
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k0) >> 2, static_cast<uint32_t>(q),
+                                      static_cast<uint32_t>(bh), 0u},
+                                x.seed0, x.seed1);
+  z[0] = r.x >= x.thresh ? x.keep_scale : 0.f;
+  z[1] = r.y >= x.thresh ? x.keep_scale : 0.f;
+  z[2] = r.z >= x.thresh ? x.keep_scale : 0.f;
+  z[3] = r.w >= x.thresh ? x.keep_scale : 0.f;
+}
+// Keep bits of (bh, q, k0..k0+3), bit i for key k0 + i (k0 a multiple of 4).
+__device__ __forceinline__ uint32_t keep4(const AttnX& x, int bh, int q, int k0) {
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k0) >> 2, static_cast<uint32_t>(q),
+                                      static_cast<uint32_t>(bh), 0u},
+                                x.seed0, x.seed1);
+  return static_cast<uint32_t>(r.x >= x.thresh) | (static_cast<uint32_t>(r.y >= x.thresh) << 1) |
+         (static_cast<uint32_t>(r.z >= x.thresh) << 2) |
+         (static_cast<uint32_t>(r.w >= x.thresh) << 3);
+}
+// Dropout factor of the single pair (bh, q, k).
+__device__ __forceinline__ float drop1(const AttnX& x, int bh, int q, int k) {
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k) >> 2, static_cast<uint32_t>(q),
+                                      static_cast<uint32_t>(bh), 0u},
+                                x.seed0, x.seed1);
+  const int t = k & 3;
+  const uint32_t v = t == 0 ? r.x : (t == 1 ? r.y : (t == 2 ? r.z : r.w));
+  return v >= x.thresh ? x.keep_scale : 0.f;
+}
+
 // Launch map of a per-(b, h) block work list whose lists differ in length.
 // order[0..n_blk) names the blocks heaviest (longest list) first. Workgroup ids
 // [0, n_bh * n_lead) take the n_lead heaviest blocks of every (b, h), so they

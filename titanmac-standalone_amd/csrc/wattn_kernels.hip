@@ -30,6 +30,7 @@
 
 #include <math.h>
 
+#include <initializer_list>
 #include <mutex>
 
 #include "tmac_device.h"
@@ -40,6 +41,16 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+
+// Row log-sum-exp in log2 units for the backward. A row that a caller's mask
+// masks fully has lse = -inf (and output 0): it gets +inf, so each of its
+// probabilities exp2(s - l2) is 0 (also for s = -inf).
+template <bool CM>
+__device__ __forceinline__ float lse_log2(float lse) {
+  const float l2 = lse * kLog2e;
+  if constexpr (CM) return lse == -INFINITY ? INFINITY : l2;
+  return l2;
+}
 
 // 64-row tiles of head dimension D (32, 64 or 128) in LDS: rows padded to
 // D + 8 elements, so the 16-byte row reads of 16 consecutive rows and the
@@ -57,15 +68,24 @@ struct Tile {
   static constexpr int kDt = D / 32;      // 32-wide head-dimension tiles of an output
 };
 
-// Four workgroups per CU at D <= 64 (at most 128 VGPRs, 36 KB of LDS each), two at D = 128.
-template <int DT, int D>
-__global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
+// Four workgroups per CU at D <= 64 (at most 128 VGPRs, 36 KB of LDS each), two at D = 128
+// and with a mask or dropout (whose extra state would spill at 128 VGPRs).
+//
+// FEAT (kFeatMask, kFeatDrop bits, tmac_device.h): with kFeatMask the caller's mask
+// tensor replaces the pattern (work lists built from it on the device, partial
+// slices masked element by element from the tensor, scores kept in log2 units
+// with the mask's bias added); with kFeatDrop each probability that enters O·V is
+// kept with probability 1 - p and scaled by 1 / (1 - p) (Philox draws), while the
+// row sum takes the undropped probabilities (dropout follows the softmax).
+template <int DT, int D, int FEAT = 0>
+__global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_mfma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
   // [buffer][K, V] 64 x D tiles.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
@@ -94,7 +114,18 @@ __global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
     for (int kk = 0; kk < T::kKk; ++kk) qf[kk] = ldg16(qp + 16 * kk);
   }
 
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
+  // Scores enter the softmax as st * sc: raw scores times scale·log2e, or, with a
+  // caller's mask, already in log2 units (sc = 1).
+  const float sc = CM ? 1.f : scale_log2;
 
   // K/V tile staging: T::kPasses 16-byte chunks of each tile per thread (rows
   // r0 + pass * T::kRpp, chunk tid % T::kCpr). Offsets within a tile are fixed per
@@ -174,7 +205,20 @@ __global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
         }
       // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
       // scores; scale_log2 > 0, so the row maximum commutes with the scaling).
-      if (kind == 2) {
+      if constexpr (CM) {
+        // log2 units; on partial slices the caller's mask adds its bias (or -inf)
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) st[kh] *= scale_log2;
+        if (kind == 2) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+              st[kh][j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
+            }
+        }
+      } else if (kind == 2) {
         // key - (kt*64 + 4h) is a constant per element, so the span bounds move
         // to this lane's origin and each test compares a constant with them.
         const int base = kt * 64 + 4 * h;
@@ -192,7 +236,7 @@ __global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
         for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kh][j]);
-      mx = xor32_max(mx) * scale_log2;
+      mx = xor32_max(mx) * sc;
       const bool move = mx > m_ref + kTau;  // false while the row is fully masked
       if (__builtin_amdgcn_ballot_w64(move)) {
         // lanes that keep their reference scale by 1 (also when it is still -inf)
@@ -213,12 +257,25 @@ __global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int kh = ks >> 1, j0 = 8 * (ks & 1);
+        // dropout factors of the 8 keys: two groups of 4 consecutive keys
+        float z[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+        if constexpr (DR) {
+          float z4[4];
+          const int k0 = kt * 64 + 32 * kh + 8 * (j0 >> 2) + 4 * h;
+          drop4(ax, bh, q_row, k0, z4);
+          z[0] = z4[0]; z[1] = z4[1]; z[2] = z4[2]; z[3] = z4[3];
+          drop4(ax, bh, q_row, k0 + 8, z4);
+          z[4] = z4[0]; z[5] = z4[1]; z[6] = z4[2]; z[7] = z4[3];
+        }
         uint32_t w[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t], scale_log2, -m_use));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t + 1], scale_log2, -m_use));
-          w[t] = Mfma<DT>::pack2(p0, p1);
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t], sc, -m_use));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(st[kh][j0 + 2 * t + 1], sc, -m_use));
+          if constexpr (DR)
+            w[t] = Mfma<DT>::pack2(p0 * z[2 * t], p1 * z[2 * t + 1]);
+          else
+            w[t] = Mfma<DT>::pack2(p0, p1);
           r4[t] += p0 + p1;
         }
         pb[ks] = u32x4{w[0], w[1], w[2], w[3]};
@@ -257,15 +314,17 @@ __global__ __launch_bounds__(256, D > 64 ? 2 : 4) void wattn_fwd_mfma_kernel(
     lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
 }
 
-// fp32 path: one query row per thread, 128 rows per workgroup (2 waves).
-template <int D>
+// fp32 path: one query row per thread, 128 rows per workgroup (2 waves). FEAT
+// as for the MFMA kernel.
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
   __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
 
@@ -296,7 +355,15 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 
   const float* Kbh = K + b * ksb + hd * ksh;
   const float* Vbh = V + b * vsb + hd * vsh;
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
   for (int e = e0; e < e1; ++e) {
     const int ent = entries[e];
     const int kt = ent & 0xffff;
@@ -320,7 +387,11 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
       float acc = 0.f;
 #pragma unroll
       for (int d = 0; d < D; ++d) acc = fmaf(q[d], kt_lds[j * D + d], acc);
-      if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
+      if constexpr (CM) {
+        if (kind == 2) acc += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
+      } else {
+        if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
+      }
       s[j] = acc;
       mx = fmaxf(mx, acc);
     }
@@ -330,12 +401,22 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
     l_run *= alpha;
 #pragma unroll
     for (int d = 0; d < D; ++d) o[d] *= alpha;
+    // dropout: keep bits of the tile's 64 keys, drawn before the unrolled loop
+    uint64_t keep = ~0ull;
+    if constexpr (DR) {
+      keep = 0;
+#pragma unroll 1
+      for (int g = 0; g < 16; ++g)
+        keep |= static_cast<uint64_t>(keep4(ax, bh, q_row, kt * 64 + 4 * g)) << (4 * g);
+    }
 #pragma unroll
     for (int j = 0; j < 64; ++j) {
       const float pj = exp2f(s[j] - m_use);
       l_run += pj;
+      float pv = pj;
+      if constexpr (DR) pv = ((keep >> j) & 1) ? pj * ax.keep_scale : 0.f;
 #pragma unroll
-      for (int d = 0; d < D; ++d) o[d] = fmaf(pj, vt_lds[j * D + d], o[d]);
+      for (int d = 0; d < D; ++d) o[d] = fmaf(pv, vt_lds[j * D + d], o[d]);
     }
     m_run = m_new;
   }
@@ -426,7 +507,9 @@ __device__ __forceinline__ void store_row(uint16_t* rowp, const f32x16 (&acc)[ND
 // (lane = key, 16 queries per lane), P = exp2(S·c − LSE·log2e) and dS, then
 // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, with dOᵀ and Qᵀ read by transpose reads in the
 // accumulator's permuted query order and P, dS packed straight from registers.
-template <int DT, int D>
+// FEAT as for the forward: with kFeatDrop, dV takes the dropped probabilities
+// P ⊙ Z and dS = P ⊙ (Z ⊙ dP − Δ) (Z the forward's factors, redrawn from the seed).
+template <int DT, int D, int FEAT = 0>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -435,7 +518,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
   // [buffer][Q, dO] 64 x D tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
@@ -469,7 +553,16 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
   const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
   const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
 
-  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + kb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = col_ptr[kb];
+    e1 = col_ptr[kb + 1];
+  }
+  const float sc = CM ? 1.f : scale_log2;
 
   u32x4 pre[2 * T::kPasses];
   float st_pre = 0.f;
@@ -499,7 +592,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     }
     if (tid < 128) {
       const int qr = min(qt * 64 + (tid & 63), S - 1);
-      st_pre = tid < 64 ? lse_bh[qr] * kLog2e : dl_bh[qr];
+      st_pre = tid < 64 ? lse_log2<CM>(lse_bh[qr]) : dl_bh[qr];
     }
   };
   auto sstore = [&](int buf) __attribute__((always_inline)) {
@@ -548,7 +641,16 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
         // s[j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4. The
         // span bounds move to this lane's origin (qt*64 + 32qh + 4h), so each
         // test compares a per-element constant with them.
-        if (kind == 2) {
+        if constexpr (CM) {
+          s *= scale_log2;
+          if (kind == 2) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
+              s[j] += mask_bias(ax, b, hd, qr, key, S) * kLog2e;
+            }
+          }
+        } else if (kind == 2) {
           const int base = qt * 64 + 32 * qh + 4 * h;
           const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
@@ -566,9 +668,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int j = 4 * g + t;
-            const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], scale_log2, -lv[t]));
-            s[j] = pj;
-            dp[j] = pj * (dp[j] - dv4[t]);
+            const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
+            if constexpr (DR) {
+              const float z = drop1(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h + t, key);
+              s[j] = pj * z;
+              dp[j] = pj * (z * dp[j] - dv4[t]);
+            } else {
+              s[j] = pj;
+              dp[j] = pj * (dp[j] - dv4[t]);
+            }
           }
         }
         // dVᵀ[d][key] += Σ_q dO[q][d] P[q][key]; dKᵀ[d][key] += Σ_q Q[q][d] dS[q][key].
@@ -603,7 +711,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
 // K and V are staged in LDS; the wave computes Sᵀ, dPᵀ, P and dSᵀ (lane = query,
 // 16 keys per lane), then dQᵀ += Kᵀ·dSᵀ with Kᵀ read by transpose reads in the
 // accumulator's permuted key order.
-template <int DT, int D>
+// FEAT as for the forward: with kFeatDrop, dS = P ⊙ (Z ⊙ dP − Δ).
+template <int DT, int D, int FEAT = 0>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -611,7 +720,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
 
@@ -638,11 +748,20 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
       gf[kk] = ldg16(gp + 16 * kk);
     }
   }
-  const float l2 = lse[static_cast<int64_t>(bh) * S + min(q_row, S - 1)] * kLog2e;
+  const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + min(q_row, S - 1)]);
   const float dl = delta[static_cast<int64_t>(bh) * S + min(q_row, S - 1)];
   const uint16_t* Kbh = K + b * ksb + hd * ksh;
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
+  const float sc = CM ? 1.f : scale_log2;
 
   u32x4 pre[2 * T::kPasses];
   const int r0 = tid / T::kCpr, c8 = (tid % T::kCpr) * 8;
@@ -714,7 +833,19 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
       }
       // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4; the
       // span bounds move to this lane's origin (kt*64 + 4h).
-      if (kind == 2) {
+      if constexpr (CM) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) s[kh] *= scale_log2;
+        if (kind == 2) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+              s[kh][j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
+            }
+        }
+      } else if (kind == 2) {
         const int base = kt * 64 + 4 * h;
         const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
@@ -728,9 +859,15 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const float pj = __builtin_amdgcn_exp2f(fmaf(s[kh][j], scale_log2, -l2));
-          dp[kh][j] = pj * (dp[kh][j] - dl);
+        for (int jg = 0; jg < 4; ++jg) {
+          float z[4] = {1.f, 1.f, 1.f, 1.f};
+          if constexpr (DR) drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * jg + 4 * h, z);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int j = 4 * jg + t;
+            const float pj = __builtin_amdgcn_exp2f(fmaf(s[kh][j], sc, -l2));
+            dp[kh][j] = DR ? pj * (z[t] * dp[kh][j] - dl) : pj * (dp[kh][j] - dl);
+          }
         }
       // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
 #pragma unroll
@@ -784,7 +921,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
 
 // fp32 dQ: one query row per thread (128 per workgroup, the forward's work
 // list); K and V tiles staged in LDS and read as broadcasts.
-template <int D>
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -792,7 +929,8 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
   __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
 
@@ -826,12 +964,20 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
   }
 #pragma unroll
   for (int d = 0; d < D; ++d) dq[d] = 0.f;
-  const float l2 = lse[static_cast<int64_t>(bh) * S + qc] * kLog2e;
+  const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + qc]);
   const float dl = delta[static_cast<int64_t>(bh) * S + qc];
 
   const float* Kbh = K + b * ksb + hd * ksh;
   const float* Vbh = V + b * vsb + hd * vsh;
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
   for (int e = e0; e < e1; ++e) {
     const int ent = entries[e];
     const int kt = ent & 0xffff;
@@ -854,8 +1000,14 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
         sj = fmaf(q[d], kt_lds[j * D + d], sj);
         dp = fmaf(g[d], vt_lds[j * D + d], dp);
       }
+      if constexpr (CM) {
+        if (kind == 2) sj += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
+      }
       float pj = __builtin_amdgcn_exp2f(sj - l2);
-      if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
+      if constexpr (!CM) {
+        if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
+      }
+      if constexpr (DR) dp *= drop1(ax, bh, q_row, kt * 64 + j);
       const float ds = pj * (dp - dl);
 #pragma unroll
       for (int d = 0; d < D; ++d) dq[d] = fmaf(ds, kt_lds[j * D + d], dq[d]);
@@ -872,7 +1024,7 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
 // fp32 dK, dV: two lanes per key (lane and lane + 32 hold head dims 0..D/2-1
 // and D/2..D-1), 32 keys per wave, 128 per workgroup (the key-major work
 // list); Q, dO, LSE and Δ of each listed 64-query tile staged in LDS.
-template <int D>
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -881,7 +1033,8 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kHd = D / 2;  // head dims per lane
   __shared__ __attribute__((aligned(16))) float q_lds[64 * D];
   __shared__ __attribute__((aligned(16))) float g_lds[64 * D];
@@ -925,7 +1078,15 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
   const float* Gbh = dO + b * gsb + hd * gsh;
   const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
   const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
-  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  int e0, e1;
+  if constexpr (CM) {
+    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + kb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = col_ptr[kb];
+    e1 = col_ptr[kb + 1];
+  }
   for (int e = e0; e < e1; ++e) {
     const int ent = entries[e];
     const int qt = ent & 0xffff;
@@ -940,7 +1101,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
     }
     if (tid < 64) {
       const int qr = min(qt * 64 + tid, S - 1);
-      l2_lds[tid] = lse_bh[qr] * kLog2e;
+      l2_lds[tid] = lse_log2<CM>(lse_bh[qr]);
       dl_lds[tid] = dl_bh[qr];
     }
     __syncthreads();
@@ -957,12 +1118,24 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
       }
       sp += __shfl_xor(sp, 32);
       dpp += __shfl_xor(dpp, 32);
-      float pi = __builtin_amdgcn_exp2f(sp * scale_log2 - l2_lds[i]);
-      if (kind == 2 && !span_has(span, qt * 64 + i)) pi = 0.f;
+      float sl = sp * scale_log2;
+      if constexpr (CM) {
+        if (kind == 2) sl += mask_bias(ax, b, hd, qt * 64 + i, key, S) * kLog2e;
+      }
+      float pi = __builtin_amdgcn_exp2f(sl - l2_lds[i]);
+      if constexpr (!CM) {
+        if (kind == 2 && !span_has(span, qt * 64 + i)) pi = 0.f;
+      }
+      float pz = pi;
+      if constexpr (DR) {
+        const float z = drop1(ax, bh, qt * 64 + i, key);
+        pz = pi * z;
+        dpp *= z;
+      }
       const float ds = pi * (dpp - dl_lds[i]);
 #pragma unroll
       for (int d = 0; d < kHd; ++d) {
-        dv[d] = fmaf(pi, gi[d], dv[d]);
+        dv[d] = fmaf(pz, gi[d], dv[d]);
         dk[d] = fmaf(ds, qi[d], dk[d]);
       }
     }
@@ -976,6 +1149,179 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
         f32x4{dk[d] * scale, dk[d + 1] * scale, dk[d + 2] * scale, dk[d + 3] * scale};
     *reinterpret_cast<f32x4*>(dvp + d) = f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]};
   }
+}
+
+// Work lists of a caller's mask (kFeatMask), built on the device in two launches.
+//
+// 1. wattn_mask_kinds_kernel: one workgroup per (mask row mr, 128x128 square
+//    (query block i, key block j)); wave w reads the square's 32 query rows
+//    32w..32w+31, lane l the keys l and 64 + l of each, so every mask byte (or
+//    float) is read once, 64 consecutive keys per wave load. Each 32x32
+//    sub-block gets (any allowed, all allowed with bias 0). From them:
+//      kinds_q[(mr * n_b + i) * n_t + t]  for the key tiles t = 2j, 2j + 1,
+//      kinds_kv[(mr * n_b + j) * n_t + u] for the query tiles u = 2i, 2i + 1,
+//    2 bits per 32-wide slice of the block (query slices for the query-major
+//    lists, key slices for the key-major ones): 0 nothing allowed, 1 all
+//    allowed with bias 0, 2 otherwise. Positions at or past S count as masked.
+// 2. wattn_mask_compact_kernel: one wave per list row (query-major rows, then
+//    key-major rows): entries[row * n_t + c] = t | kinds << 16 for the tiles t
+//    with a nonzero kind, t ascending, and cnt[row] = their number. Wave 0 also
+//    writes the identity launch order of the blocks.
+__global__ __launch_bounds__(256) void wattn_mask_kinds_kernel(AttnX ax, int S, int n_b, int n_t,
+                                                               uint8_t* __restrict__ kinds_q,
+                                                               uint8_t* __restrict__ kinds_kv) {
+  __shared__ uint32_t flags[4];  // per wave: (any, all) bits of its four 32x32 sub-blocks
+  const int j = blockIdx.x, i = blockIdx.y, mr = blockIdx.z;
+  const int bm = mr / ax.MH, hm = mr - bm * ax.MH;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  bool any0 = false, all0 = true, any1 = false, all1 = true;
+  const int k0 = j * 128 + lane, k1 = k0 + 64;
+#pragma unroll 8
+  for (int r = 0; r < 32; ++r) {
+    const int q = i * 128 + 32 * wave + r;
+    const float v0 = mask_bias(ax, bm, hm, q, k0, S);
+    const float v1 = mask_bias(ax, bm, hm, q, k1, S);
+    any0 |= !(v0 == -INFINITY);
+    all0 &= (v0 == 0.f);
+    any1 |= !(v1 == -INFINITY);
+    all1 &= (v1 == 0.f);
+  }
+  // sub-block c (key columns 32c..32c+31 of the square) of this wave's 32 rows
+  const uint64_t ba0 = __ballot(any0), bl0 = __ballot(all0);
+  const uint64_t ba1 = __ballot(any1), bl1 = __ballot(all1);
+  if (lane == 0) {
+    uint32_t f = 0;
+    f |= (static_cast<uint32_t>(ba0 & 0xffffffffull) != 0) << 0;
+    f |= (static_cast<uint32_t>(ba0 >> 32) != 0) << 1;
+    f |= (static_cast<uint32_t>(ba1 & 0xffffffffull) != 0) << 2;
+    f |= (static_cast<uint32_t>(ba1 >> 32) != 0) << 3;
+    f |= (static_cast<uint32_t>(bl0 & 0xffffffffull) == 0xffffffffu) << 4;
+    f |= (static_cast<uint32_t>(bl0 >> 32) == 0xffffffffu) << 5;
+    f |= (static_cast<uint32_t>(bl1 & 0xffffffffull) == 0xffffffffu) << 6;
+    f |= (static_cast<uint32_t>(bl1 >> 32) == 0xffffffffu) << 7;
+    flags[wave] = f;
+  }
+  __syncthreads();
+  if (tid < 4) {
+    // tid 0, 1: query-major kinds of key tile 2j + tid; tid 2, 3: key-major kinds
+    // of query tile 2i + tid - 2.
+    const int h = tid & 1;
+    uint32_t kb = 0;
+    for (int sl = 0; sl < 4; ++sl) {
+      bool any, all;
+      if (tid < 2) {  // query slice sl, sub-blocks (sl, 2h), (sl, 2h + 1)
+        const uint32_t f = flags[sl];
+        any = ((f >> (2 * h)) & 3) != 0;
+        all = ((f >> (4 + 2 * h)) & 3) == 3;
+      } else {  // key slice sl, sub-blocks (2h, sl), (2h + 1, sl)
+        const uint32_t f0 = flags[2 * h], f1 = flags[2 * h + 1];
+        any = ((f0 >> sl) & 1) | ((f1 >> sl) & 1);
+        all = ((f0 >> (4 + sl)) & 1) & ((f1 >> (4 + sl)) & 1);
+      }
+      kb |= static_cast<uint32_t>(!any ? 0 : (all ? 1 : 2)) << (2 * sl);
+    }
+    if (tid < 2) {
+      const int t = 2 * j + h;
+      if (t < n_t) kinds_q[(static_cast<int64_t>(mr) * n_b + i) * n_t + t] = static_cast<uint8_t>(kb);
+    } else {
+      const int u = 2 * i + h;
+      if (u < n_t) kinds_kv[(static_cast<int64_t>(mr) * n_b + j) * n_t + u] = static_cast<uint8_t>(kb);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void wattn_mask_compact_kernel(
+    const uint8_t* __restrict__ kinds, int n_rows, int n_t, int n_b, int32_t* __restrict__ entries,
+    int32_t* __restrict__ cnt, int32_t* __restrict__ order) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (blockIdx.x == 0 && threadIdx.x < 64)
+    for (int b = lane; b < n_b; b += 64) order[b] = b;
+  if (row >= n_rows) return;
+  const uint8_t* kr = kinds + static_cast<int64_t>(row) * n_t;
+  int32_t* er = entries + static_cast<int64_t>(row) * n_t;
+  int count = 0;
+  for (int t0 = 0; t0 < n_t; t0 += 64) {
+    const int t = t0 + lane;
+    const int kb = t < n_t ? kr[t] : 0;
+    const uint64_t m = __ballot(kb != 0);
+    if (kb != 0) {
+      const int before = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      er[count + before] = t | (kb << 16);
+    }
+    count += __popcll(m);
+  }
+  if (lane == 0) cnt[row] = count;
+}
+
+// Byte offsets of the parts of a mask workspace (each 256-byte aligned): the
+// launch order; the tile kinds, query-major rows then key-major rows; the
+// entries, same order; the counts, same order.
+struct MaskWs {
+  size_t order, kinds_q, kinds_kv, ent_q, ent_kv, cnt_q, cnt_kv, total;
+  int64_t rows;  // list rows of each orientation: mask rows x blocks
+};
+inline MaskWs mask_ws_layout(int S, int mask_batch, int mask_heads) {
+  auto up = [](size_t x) { return (x + 255) & ~static_cast<size_t>(255); };
+  const size_t n_b = (S + 127) / 128, n_t = (S + 63) / 64;
+  const size_t rows = static_cast<size_t>(mask_batch) * mask_heads * n_b;
+  MaskWs w;
+  w.rows = static_cast<int64_t>(rows);
+  w.order = 0;
+  w.kinds_q = up(n_b * 4);
+  w.kinds_kv = w.kinds_q + rows * n_t;
+  w.ent_q = w.kinds_q + up(2 * rows * n_t);
+  w.ent_kv = w.ent_q + rows * n_t * 4;
+  w.cnt_q = w.ent_q + up(2 * rows * n_t * 4);
+  w.cnt_kv = w.cnt_q + rows * 4;
+  w.total = w.cnt_q + up(2 * rows * 4);
+  return w;
+}
+
+// Checks the options of the *_ex entry points and fills the kernels' AttnX (with
+// the query-major counts; the caller switches to the key-major ones). feat gets the
+// kFeat bits.
+int make_attn_x(const tmac_attn_opts* o, int B, int H, int S, AttnX* x, int* feat) {
+  *x = AttnX{};
+  *feat = 0;
+  x->keep_scale = 1.f;
+  if (!o) return TMAC_OK;
+  if (!(o->dropout_p >= 0.f && o->dropout_p < 1.f)) return TMAC_ERR_VALUE;
+  if (o->dropout_p > 0.f) {
+    *feat |= kFeatDrop;
+    const double th = static_cast<double>(o->dropout_p) * 4294967296.0;
+    x->thresh = th >= 4294967295.0 ? 0xffffffffu : static_cast<uint32_t>(th);
+    x->keep_scale = 1.f / (1.f - o->dropout_p);
+    x->seed0 = static_cast<uint32_t>(o->dropout_seed);
+    x->seed1 = static_cast<uint32_t>(o->dropout_seed >> 32);
+  }
+  if (o->d_mask) {
+    if (o->mask_format != TMAC_MASK_BOOL && o->mask_format != TMAC_MASK_ADD_F32) return TMAC_ERR_DTYPE;
+    if (!(o->mask_batch == 1 || o->mask_batch == B) || !(o->mask_heads == 1 || o->mask_heads == H))
+      return TMAC_ERR_SHAPE;
+    for (int i = 0; i < 3; ++i)
+      if (o->mask_strides[i] < 0) return TMAC_ERR_SHAPE;
+    if (o->mask_strides[2] < S) return TMAC_ERR_SHAPE;
+    if (o->mask_format == TMAC_MASK_ADD_F32 && (reinterpret_cast<uintptr_t>(o->d_mask) & 3u))
+      return TMAC_ERR_ALIGN;
+    const MaskWs w = mask_ws_layout(S, o->mask_batch, o->mask_heads);
+    if (!o->d_mask_ws || o->mask_ws_bytes < w.total) return TMAC_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(o->d_mask_ws) & 255u) return TMAC_ERR_ALIGN;
+    *feat |= kFeatMask;
+    x->mask = o->d_mask;
+    x->fmt = o->mask_format;
+    x->msb = o->mask_strides[0];
+    x->msh = o->mask_strides[1];
+    x->msq = o->mask_strides[2];
+    x->mb1 = o->mask_batch == 1;
+    x->mh1 = o->mask_heads == 1;
+    x->MH = o->mask_heads;
+    x->cnt = reinterpret_cast<const int32_t*>(static_cast<const char*>(o->d_mask_ws) + w.cnt_q);
+    x->cap = (S + 63) / 64;
+  }
+  return TMAC_OK;
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -993,31 +1339,237 @@ inline WorkMap make_work_map(int n_bh, int n_blk, int n_lead, unsigned* grid) {
   return m;
 }
 
-template <int D>
-void launch_wattn_fwd(int dtype, unsigned grid, hipStream_t s, const void* d_Q, const void* d_K,
-                      const void* d_V, void* d_O, float* d_lse, const int64_t* qs,
-                      const int64_t* ks, const int64_t* vs, const int64_t* os, int H,
-                      const MaskParams& mp, float scale_log2, const int32_t* d_row_ptr,
-                      const int32_t* d_entries, const int32_t* d_order, const WorkMap& wm) {
-  if (dtype == TMAC_F32) {
-    hipLaunchKernelGGL((wattn_fwd_f32_kernel<D>), dim3(grid), dim3(128), 0, s,
-                       static_cast<const float*>(d_Q), static_cast<const float*>(d_K),
-                       static_cast<const float*>(d_V), static_cast<float*>(d_O), d_lse, qs[0],
-                       qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1], os[2],
-                       H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
-  } else if (dtype == TMAC_BF16) {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16, D>), dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
-                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
+// Arguments of one attention launch (forward or backward), gathered so the
+// kernels can be dispatched over dtype, head dimension and feature bits.
+struct AttnLaunch {
+  const void *Q, *K, *V, *O, *dO;
+  void *Out, *dQ, *dK, *dV;
+  float* lse_out;
+  const float* lse;
+  float* delta;
+  const int64_t *qs, *ks, *vs, *os, *gs, *dqs, *dks, *dvs;
+  int B, H, S, dh, dtype;
+  MaskParams mp;
+  float scale, scale_log2;
+  const int32_t *row_ptr, *entries, *order, *col_ptr, *entries_kv, *order_kv;
+  WorkMap wm_q, wm_kv;
+  unsigned grid_q, grid_kv;
+  AttnX ax_q, ax_kv;  // the caller's mask with the query-major / key-major counts
+  hipStream_t s;
+};
+
+template <int D, int FEAT>
+void launch_fwd(const AttnLaunch& a) {
+  const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os;
+  if (a.dtype == TMAC_F32) {
+    hipLaunchKernelGGL((wattn_fwd_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s,
+                       static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
+                       static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
                        qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+                       os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order, a.wm_q,
+                       a.ax_q);
+  } else if (a.dtype == TMAC_BF16) {
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16, D, FEAT>), dim3(a.grid_q), dim3(256), 0,
+                       a.s, static_cast<const uint16_t*>(a.Q), static_cast<const uint16_t*>(a.K),
+                       static_cast<const uint16_t*>(a.V), static_cast<uint16_t*>(a.Out),
+                       a.lse_out, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                       os[0], os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries,
+                       a.order, a.wm_q, a.ax_q);
   } else {
-    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16, D>), dim3(grid), dim3(256), 0, s,
-                       static_cast<const uint16_t*>(d_Q), static_cast<const uint16_t*>(d_K),
-                       static_cast<const uint16_t*>(d_V), static_cast<uint16_t*>(d_O), d_lse,
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], H, mp, scale_log2, d_row_ptr, d_entries, d_order, wm);
+    hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_F16, D, FEAT>), dim3(a.grid_q), dim3(256), 0,
+                       a.s, static_cast<const uint16_t*>(a.Q), static_cast<const uint16_t*>(a.K),
+                       static_cast<const uint16_t*>(a.V), static_cast<uint16_t*>(a.Out),
+                       a.lse_out, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
+                       os[0], os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries,
+                       a.order, a.wm_q, a.ax_q);
   }
+}
+
+// Backward, 16-bit MFMA kernels: row sums, then dK/dV, then dQ.
+template <int DT, int D, int FEAT>
+void launch_bwd_mfma(const AttnLaunch& a) {
+  const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os, *gs = a.gs, *dqs = a.dqs,
+                *dks = a.dks, *dvs = a.dvs;
+  const auto* Q = static_cast<const uint16_t*>(a.Q);
+  const auto* K = static_cast<const uint16_t*>(a.K);
+  const auto* V = static_cast<const uint16_t*>(a.V);
+  const auto* O = static_cast<const uint16_t*>(a.O);
+  const auto* G = static_cast<const uint16_t*>(a.dO);
+  const int64_t n_rows = static_cast<int64_t>(a.B) * a.H * a.S;
+  const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);  // 2048/D rows each
+  hipLaunchKernelGGL((wattn_bwd_delta_kernel<DT, D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
+                     a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
+  hipLaunchKernelGGL((wattn_bwd_kv_kernel<DT, D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
+                     V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
+                     static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
+                     vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0],
+                     dvs[1], dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
+                     a.order_kv, a.wm_kv, a.ax_kv);
+  hipLaunchKernelGGL((wattn_bwd_q_kernel<DT, D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V,
+                     G, a.lse, a.delta, static_cast<uint16_t*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+                     ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
+                     dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
+                     a.wm_q, a.ax_q);
+}
+
+// Backward, fp32 FMA kernels.
+template <int D, int FEAT>
+void launch_bwd_f32(const AttnLaunch& a) {
+  const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os, *gs = a.gs, *dqs = a.dqs,
+                *dks = a.dks, *dvs = a.dvs;
+  const auto* Q = static_cast<const float*>(a.Q);
+  const auto* K = static_cast<const float*>(a.K);
+  const auto* V = static_cast<const float*>(a.V);
+  const auto* O = static_cast<const float*>(a.O);
+  const auto* G = static_cast<const float*>(a.dO);
+  const int64_t n_rows = static_cast<int64_t>(a.B) * a.H * a.S;
+  const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);
+  hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
+                     a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
+  hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
+                     V, G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
+                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
+                     gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
+                     a.scale_log2, a.col_ptr, a.entries_kv, a.order_kv, a.wm_kv, a.ax_kv);
+  hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s, Q, K, V,
+                     G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+                     ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
+                     dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
+                     a.wm_q, a.ax_q);
+}
+
+template <int FEAT>
+void dispatch(const AttnLaunch& a, bool bwd) {
+  const int d = a.dh;
+  if (!bwd) {
+    if (d == 32) launch_fwd<32, FEAT>(a);
+    else if (d == 64) launch_fwd<64, FEAT>(a);
+    else launch_fwd<128, FEAT>(a);
+  } else if (a.dtype == TMAC_F32) {
+    if (d == 32) launch_bwd_f32<32, FEAT>(a);
+    else if (d == 64) launch_bwd_f32<64, FEAT>(a);
+    else launch_bwd_f32<128, FEAT>(a);
+  } else if (a.dtype == TMAC_BF16) {
+    if (d == 32) launch_bwd_mfma<TMAC_BF16, 32, FEAT>(a);
+    else if (d == 64) launch_bwd_mfma<TMAC_BF16, 64, FEAT>(a);
+    else launch_bwd_mfma<TMAC_BF16, 128, FEAT>(a);
+  } else {
+    if (d == 32) launch_bwd_mfma<TMAC_F16, 32, FEAT>(a);
+    else if (d == 64) launch_bwd_mfma<TMAC_F16, 64, FEAT>(a);
+    else launch_bwd_mfma<TMAC_F16, 128, FEAT>(a);
+  }
+}
+
+// Checks shared by the forward and backward: sizes, dtype, strides, pointer
+// alignment, and (without a caller's mask) the pattern's arguments.
+int check_common(int B, int H, int S, int dh, int window, int n_persistent, int pattern,
+                 int block_size, float scale, int dtype, bool masked,
+                 std::initializer_list<const int64_t*> strides,
+                 std::initializer_list<const void*> ptrs) {
+  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
+  if (dh != 32 && dh != 64 && dh != 128) return TMAC_ERR_SHAPE;
+  if (!masked) {
+    if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
+    if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
+    if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
+    if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
+  }
+  if (!(scale > 0.f)) return TMAC_ERR_VALUE;
+  if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16-byte vector
+  for (const int64_t* st : strides)
+    for (int i = 0; i < 3; ++i)
+      if (st[i] < 0 || st[i] % vec) return TMAC_ERR_ALIGN;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return TMAC_ERR_ALIGN;
+  if (static_cast<int64_t>(B) * H * ((S + 127) / 128) > (1ll << 30)) return TMAC_ERR_SHAPE;
+  return TMAC_OK;
+}
+
+// Fills the pattern / mask part of a launch: work lists, launch maps, AttnX.
+int setup_lists(AttnLaunch& a, const tmac_attn_opts* opts, int window, int n_persistent,
+                int causal, int pattern, int block_size, const int32_t* row_ptr,
+                const int32_t* entries, const int32_t* order, int n_lead,
+                const int32_t* col_ptr, const int32_t* entries_kv, const int32_t* order_kv,
+                int n_lead_kv, int* feat) {
+  const int n_qb = (a.S + 127) / 128;  // 128-query blocks (fwd, dQ) and 128-key blocks (dK, dV)
+  const int st = make_attn_x(opts, a.B, a.H, a.S, &a.ax_q, feat);
+  if (st != TMAC_OK) return st;
+  a.ax_kv = a.ax_q;
+  a.mp = MaskParams{a.S, min(window, a.S), n_persistent, causal ? 1 : 0, pattern, block_size};
+  if (*feat & kFeatMask) {
+    const MaskWs w = mask_ws_layout(a.S, opts->mask_batch, opts->mask_heads);
+    const char* ws = static_cast<const char*>(opts->d_mask_ws);
+    a.ax_kv.cnt = reinterpret_cast<const int32_t*>(ws + w.cnt_kv);
+    a.entries = reinterpret_cast<const int32_t*>(ws + w.ent_q);
+    a.entries_kv = reinterpret_cast<const int32_t*>(ws + w.ent_kv);
+    a.order = a.order_kv = reinterpret_cast<const int32_t*>(ws + w.order);
+    a.row_ptr = a.col_ptr = nullptr;
+    n_lead = n_lead_kv = 0;  // identity order, no lead blocks
+    a.mp = MaskParams{a.S, a.S, 0, 0, TMAC_PATTERN_BAND, 1};
+  } else {
+    if (!row_ptr || !entries || !order) return TMAC_ERR_NULL;
+    a.row_ptr = row_ptr;
+    a.entries = entries;
+    a.order = order;
+    a.col_ptr = col_ptr;
+    a.entries_kv = entries_kv;
+    a.order_kv = order_kv;
+  }
+  if (n_lead < 0 || n_lead > n_qb || n_lead_kv < 0 || n_lead_kv > n_qb) return TMAC_ERR_VALUE;
+  a.wm_q = make_work_map(a.B * a.H, n_qb, n_lead, &a.grid_q);
+  a.wm_kv = make_work_map(a.B * a.H, n_qb, n_lead_kv, &a.grid_kv);
+  return TMAC_OK;
+}
+
+int launch_status(const AttnLaunch& a, int feat, bool bwd) {
+  switch (feat) {
+    case 0: dispatch<0>(a, bwd); break;
+    case kFeatMask: dispatch<kFeatMask>(a, bwd); break;
+    case kFeatDrop: dispatch<kFeatDrop>(a, bwd); break;
+    default: dispatch<kFeatMask | kFeatDrop>(a, bwd); break;
+  }
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
+}
+
+int wattn_fwd_impl(const void* d_Q, const int64_t q_strides[3], const void* d_K,
+                   const int64_t k_strides[3], const void* d_V, const int64_t v_strides[3],
+                   void* d_O, const int64_t o_strides[3], float* d_lse, int B, int H, int S,
+                   int dh, int window, int n_persistent, int causal, int pattern, int block_size,
+                   float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
+                   const int32_t* d_order, int n_lead, int dtype, void* stream,
+                   const tmac_attn_opts* opts) {
+  if (!d_Q || !d_K || !d_V || !d_O || !q_strides || !k_strides || !v_strides || !o_strides)
+    return TMAC_ERR_NULL;
+  const bool masked = opts && opts->d_mask;
+  int st = check_common(B, H, S, dh, window, n_persistent, pattern, block_size, scale, dtype,
+                        masked, {q_strides, k_strides, v_strides, o_strides},
+                        {d_Q, d_K, d_V, d_O});
+  if (st != TMAC_OK) return st;
+  AttnLaunch a{};
+  a.Q = d_Q;
+  a.K = d_K;
+  a.V = d_V;
+  a.Out = d_O;
+  a.lse_out = d_lse;
+  a.qs = q_strides;
+  a.ks = k_strides;
+  a.vs = v_strides;
+  a.os = o_strides;
+  a.B = B;
+  a.H = H;
+  a.S = S;
+  a.dh = dh;
+  a.dtype = dtype;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.s = static_cast<hipStream_t>(stream);
+  int feat = 0;
+  st = setup_lists(a, opts, window, n_persistent, causal, pattern, block_size, d_row_ptr,
+                   d_entries, d_order, n_lead, nullptr, nullptr, nullptr, 0, &feat);
+  if (st != TMAC_OK) return st;
+  return launch_status(a, feat, false);
 }
 
 }  // namespace
@@ -1029,59 +1581,61 @@ extern "C" int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3], const
                               int n_persistent, int causal, int pattern, int block_size,
                               float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
                               const int32_t* d_order, int n_lead, int dtype, void* stream) {
-  if (!d_Q || !d_K || !d_V || !d_O || !q_strides || !k_strides || !v_strides || !o_strides ||
-      !d_row_ptr || !d_entries || !d_order)
-    return TMAC_ERR_NULL;
-  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
-  if (dh != 32 && dh != 64 && dh != 128) return TMAC_ERR_SHAPE;
-  if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
-  if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
-  if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
-  if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
-  if (!(scale > 0.f)) return TMAC_ERR_VALUE;
-  if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
-  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16-byte vector
-  const int64_t* all[4] = {q_strides, k_strides, v_strides, o_strides};
-  for (const int64_t* st : all)
-    for (int i = 0; i < 3; ++i)
-      if (st[i] < 0 || st[i] % vec) return TMAC_ERR_ALIGN;
-  if (!aligned16(d_Q) || !aligned16(d_K) || !aligned16(d_V) || !aligned16(d_O))
-    return TMAC_ERR_ALIGN;
+  return wattn_fwd_impl(d_Q, q_strides, d_K, k_strides, d_V, v_strides, d_O, o_strides, d_lse, B,
+                        H, S, dh, window, n_persistent, causal, pattern, block_size, scale,
+                        d_row_ptr, d_entries, d_order, n_lead, dtype, stream, nullptr);
+}
 
-  const int n_qb = (S + 127) / 128;
-  if (static_cast<int64_t>(B) * H * n_qb > (1ll << 30)) return TMAC_ERR_SHAPE;
-  if (n_lead < 0 || n_lead > n_qb) return TMAC_ERR_VALUE;
-  unsigned grid = 0;
-  const WorkMap wm = make_work_map(B * H, n_qb, n_lead, &grid);
-  const MaskParams mp{S, min(window, S), n_persistent, causal ? 1 : 0, pattern, block_size};
-  const float scale_log2 = scale * kLog2e;
+extern "C" int tmac_wattn_fwd_ex(const void* d_Q, const int64_t q_strides[3], const void* d_K,
+                                 const int64_t k_strides[3], const void* d_V,
+                                 const int64_t v_strides[3], void* d_O,
+                                 const int64_t o_strides[3], float* d_lse, int B, int H, int S,
+                                 int dh, int window, int n_persistent, int causal, int pattern,
+                                 int block_size, float scale, const int32_t* d_row_ptr,
+                                 const int32_t* d_entries, const int32_t* d_order, int n_lead,
+                                 int dtype, void* stream, const tmac_attn_opts* opts) {
+  return wattn_fwd_impl(d_Q, q_strides, d_K, k_strides, d_V, v_strides, d_O, o_strides, d_lse, B,
+                        H, S, dh, window, n_persistent, causal, pattern, block_size, scale,
+                        d_row_ptr, d_entries, d_order, n_lead, dtype, stream, opts);
+}
+
+extern "C" size_t tmac_wattn_mask_workspace(int S, int mask_batch, int mask_heads) {
+  if (S <= 0 || mask_batch <= 0 || mask_heads <= 0) return 0;
+  return mask_ws_layout(S, mask_batch, mask_heads).total;
+}
+
+extern "C" int tmac_wattn_mask_lists(const tmac_attn_opts* opts, int S, void* stream) {
+  if (!opts || !opts->d_mask || !opts->d_mask_ws) return TMAC_ERR_NULL;
+  if (S <= 0 || opts->mask_batch <= 0 || opts->mask_heads <= 0) return TMAC_ERR_SHAPE;
+  const int n_b = (S + 127) / 128, n_t = (S + 63) / 64;
+  const int64_t n_mr = static_cast<int64_t>(opts->mask_batch) * opts->mask_heads;
+  if (n_mr > 65535 || n_b > 65535 || n_mr * n_b > (1ll << 29)) return TMAC_ERR_SHAPE;  // grid y, z
+  AttnX x;
+  int feat = 0;
+  const int st = make_attn_x(opts, opts->mask_batch, opts->mask_heads, S, &x, &feat);
+  if (st != TMAC_OK) return st;
+  const MaskWs w = mask_ws_layout(S, opts->mask_batch, opts->mask_heads);
+  char* ws = static_cast<char*>(opts->d_mask_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int64_t* qs = q_strides;
-  const int64_t* ks = k_strides;
-  const int64_t* vs = v_strides;
-  const int64_t* os = o_strides;
-  switch (dh) {
-    case 32:
-      launch_wattn_fwd<32>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
-                           scale_log2, d_row_ptr, d_entries, d_order, wm);
-      break;
-    case 64:
-      launch_wattn_fwd<64>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
-                           scale_log2, d_row_ptr, d_entries, d_order, wm);
-      break;
-    default:
-      launch_wattn_fwd<128>(dtype, grid, s, d_Q, d_K, d_V, d_O, d_lse, qs, ks, vs, os, H, mp,
-                            scale_log2, d_row_ptr, d_entries, d_order, wm);
-      break;
-  }
+  auto* kinds_q = reinterpret_cast<uint8_t*>(ws + w.kinds_q);
+  hipLaunchKernelGGL(wattn_mask_kinds_kernel, dim3(n_b, n_b, static_cast<unsigned>(n_mr)),
+                     dim3(256), 0, s, x, S, n_b, n_t, kinds_q,
+                     reinterpret_cast<uint8_t*>(ws + w.kinds_kv));
+  const int64_t n_rows = 2 * w.rows;  // query-major rows, then key-major rows
+  hipLaunchKernelGGL(wattn_mask_compact_kernel, dim3(static_cast<unsigned>((n_rows + 3) / 4)),
+                     dim3(256), 0, s, kinds_q, static_cast<int>(n_rows), n_t, n_b,
+                     reinterpret_cast<int32_t*>(ws + w.ent_q),
+                     reinterpret_cast<int32_t*>(ws + w.cnt_q),
+                     reinterpret_cast<int32_t*>(ws + w.order));
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }
 
 namespace {
 
-// Shared body of tmac_wattn_bwd and tmac_wattn_bwd_noalloc: d_delta is the
-// fp32 [B, H, S] row-sum buffer (the caller's workspace, or the static scratch).
+// Shared body of tmac_wattn_bwd, tmac_wattn_bwd_ex and tmac_wattn_bwd_noalloc:
+// d_delta is the fp32 [B, H, S] row-sum buffer (the caller's workspace, or the
+// static scratch).
 int wattn_bwd_impl(const void* d_Q, const int64_t q_strides[3], const void* d_K,
                    const int64_t k_strides[3], const void* d_V, const int64_t v_strides[3],
                    const void* d_O, const int64_t o_strides[3], const void* d_dO,
@@ -1092,110 +1646,54 @@ int wattn_bwd_impl(const void* d_Q, const int64_t q_strides[3], const void* d_K,
                    float scale, const int32_t* d_row_ptr, const int32_t* d_entries,
                    const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
                    const int32_t* d_entries_kv, const int32_t* d_order_kv, int n_lead_kv,
-                   int dtype, void* stream) {
+                   int dtype, void* stream, const tmac_attn_opts* opts) {
   if (!d_Q || !d_K || !d_V || !d_O || !d_dO || !d_lse || !d_delta || !d_dQ || !d_dK || !d_dV ||
       !q_strides || !k_strides || !v_strides || !o_strides || !do_strides || !dq_strides ||
-      !dk_strides || !dv_strides || !d_row_ptr || !d_entries || !d_order || !d_col_ptr ||
-      !d_entries_kv || !d_order_kv)
+      !dk_strides || !dv_strides)
     return TMAC_ERR_NULL;
-  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
-  if (dh != 32 && dh != 64 && dh != 128) return TMAC_ERR_SHAPE;
-  if (pattern != TMAC_PATTERN_BAND && pattern != TMAC_PATTERN_BLOCKWIN) return TMAC_ERR_VALUE;
-  if (n_persistent < 0 || window < 0 || n_persistent > S) return TMAC_ERR_VALUE;
-  if (pattern == TMAC_PATTERN_BAND && n_persistent == S) return TMAC_ERR_VALUE;
-  if (pattern == TMAC_PATTERN_BLOCKWIN && block_size <= 0) return TMAC_ERR_VALUE;
-  if (!(scale > 0.f)) return TMAC_ERR_VALUE;
-  if (dtype != TMAC_F32 && dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
-  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16-byte vector
-  const int64_t* all[8] = {q_strides, k_strides, v_strides, o_strides,
-                           do_strides, dq_strides, dk_strides, dv_strides};
-  for (const int64_t* st : all)
-    for (int i = 0; i < 3; ++i)
-      if (st[i] < 0 || st[i] % vec) return TMAC_ERR_ALIGN;
-  const void* ptrs[8] = {d_Q, d_K, d_V, d_O, d_dO, d_dQ, d_dK, d_dV};
-  for (const void* p : ptrs)
-    if (!aligned16(p)) return TMAC_ERR_ALIGN;
-
-  const int n_qb = (S + 127) / 128;  // 128-query blocks (dQ) and 128-key blocks (dK, dV)
-  if (static_cast<int64_t>(B) * H * n_qb > (1ll << 30)) return TMAC_ERR_SHAPE;
-  if (n_lead < 0 || n_lead > n_qb || n_lead_kv < 0 || n_lead_kv > n_qb) return TMAC_ERR_VALUE;
-  unsigned grid_q = 0, grid_kv = 0;
-  const WorkMap wm_q = make_work_map(B * H, n_qb, n_lead, &grid_q);
-  const WorkMap wm_kv = make_work_map(B * H, n_qb, n_lead_kv, &grid_kv);
-  const MaskParams mp{S, min(window, S), n_persistent, causal ? 1 : 0, pattern, block_size};
-  const float scale_log2 = scale * kLog2e;
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const auto* Q = static_cast<const uint16_t*>(d_Q);
-  const auto* K = static_cast<const uint16_t*>(d_K);
-  const auto* V = static_cast<const uint16_t*>(d_V);
-  const auto* O = static_cast<const uint16_t*>(d_O);
-  const auto* G = static_cast<const uint16_t*>(d_dO);
-  auto* dQ = static_cast<uint16_t*>(d_dQ);
-  auto* dK = static_cast<uint16_t*>(d_dK);
-  auto* dV = static_cast<uint16_t*>(d_dV);
-  const int64_t *qs = q_strides, *ks = k_strides, *vs = v_strides, *os = o_strides,
-                *gs = do_strides, *dqs = dq_strides, *dks = dk_strides, *dvs = dv_strides;
-  const int64_t n_rows = static_cast<int64_t>(B) * H * S;
-  // row-sum kernel: 2048/D rows per workgroup
-  const unsigned dgrid = static_cast<unsigned>((n_rows * dh + 2047) / 2048);
-#define TMAC_WATTN_BWD(DTV, DV)                                                                      \
-  do {                                                                                               \
-    hipLaunchKernelGGL((wattn_bwd_delta_kernel<DTV, DV>), dim3(dgrid), dim3(256), 0, s, O, G,        \
-                       d_delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);             \
-    hipLaunchKernelGGL((wattn_bwd_kv_kernel<DTV, DV>), dim3(grid_kv), dim3(256), 0, s, Q, K, V, G,   \
-                       d_lse, d_delta, dK, dV, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],      \
-                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],    \
-                       dvs[2], H, mp, scale, scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv); \
-    hipLaunchKernelGGL((wattn_bwd_q_kernel<DTV, DV>), dim3(grid_q), dim3(256), 0, s, Q, K, V, G,     \
-                       d_lse, d_delta, dQ, qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1],   \
-                       vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H, mp, scale, scale_log2, \
-                       d_row_ptr, d_entries, d_order, wm_q);                                         \
-  } while (0)
-#define TMAC_WATTN_BWD_F32(DV)                                                                       \
-  do {                                                                                               \
-    hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<DV>), dim3(dgrid), dim3(256), 0, s, Of, Gf,       \
-                       d_delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], H, S, n_rows);             \
-    hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<DV>), dim3(grid_kv), dim3(256), 0, s, Qf, Kf, Vf,    \
-                       Gf, d_lse, d_delta, static_cast<float*>(d_dK), static_cast<float*>(d_dV),     \
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],  \
-                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], H, mp, scale,          \
-                       scale_log2, d_col_ptr, d_entries_kv, d_order_kv, wm_kv);                      \
-    hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<DV>), dim3(grid_q), dim3(128), 0, s, Qf, Kf, Vf, Gf,  \
-                       d_lse, d_delta, static_cast<float*>(d_dQ), qs[0], qs[1], qs[2], ks[0], ks[1], \
-                       ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1], dqs[2], H,   \
-                       mp, scale, scale_log2, d_row_ptr, d_entries, d_order, wm_q);                  \
-  } while (0)
-  if (dtype == TMAC_F32) {
-    const auto* Qf = static_cast<const float*>(d_Q);
-    const auto* Kf = static_cast<const float*>(d_K);
-    const auto* Vf = static_cast<const float*>(d_V);
-    const auto* Of = static_cast<const float*>(d_O);
-    const auto* Gf = static_cast<const float*>(d_dO);
-    if (dh == 32)
-      TMAC_WATTN_BWD_F32(32);
-    else if (dh == 64)
-      TMAC_WATTN_BWD_F32(64);
-    else
-      TMAC_WATTN_BWD_F32(128);
-  } else if (dtype == TMAC_BF16) {
-    if (dh == 32)
-      TMAC_WATTN_BWD(TMAC_BF16, 32);
-    else if (dh == 64)
-      TMAC_WATTN_BWD(TMAC_BF16, 64);
-    else
-      TMAC_WATTN_BWD(TMAC_BF16, 128);
-  } else {
-    if (dh == 32)
-      TMAC_WATTN_BWD(TMAC_F16, 32);
-    else if (dh == 64)
-      TMAC_WATTN_BWD(TMAC_F16, 64);
-    else
-      TMAC_WATTN_BWD(TMAC_F16, 128);
-  }
-#undef TMAC_WATTN_BWD
-#undef TMAC_WATTN_BWD_F32
-  const hipError_t err = hipGetLastError();
-  return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
+  const bool masked = opts && opts->d_mask;
+  if (!masked && (!d_row_ptr || !d_entries || !d_order || !d_col_ptr || !d_entries_kv ||
+                  !d_order_kv))
+    return TMAC_ERR_NULL;
+  int st = check_common(B, H, S, dh, window, n_persistent, pattern, block_size, scale, dtype,
+                        masked,
+                        {q_strides, k_strides, v_strides, o_strides, do_strides, dq_strides,
+                         dk_strides, dv_strides},
+                        {d_Q, d_K, d_V, d_O, d_dO, d_dQ, d_dK, d_dV});
+  if (st != TMAC_OK) return st;
+  AttnLaunch a{};
+  a.Q = d_Q;
+  a.K = d_K;
+  a.V = d_V;
+  a.O = d_O;
+  a.dO = d_dO;
+  a.dQ = d_dQ;
+  a.dK = d_dK;
+  a.dV = d_dV;
+  a.lse = d_lse;
+  a.delta = d_delta;
+  a.qs = q_strides;
+  a.ks = k_strides;
+  a.vs = v_strides;
+  a.os = o_strides;
+  a.gs = do_strides;
+  a.dqs = dq_strides;
+  a.dks = dk_strides;
+  a.dvs = dv_strides;
+  a.B = B;
+  a.H = H;
+  a.S = S;
+  a.dh = dh;
+  a.dtype = dtype;
+  a.scale = scale;
+  a.scale_log2 = scale * kLog2e;
+  a.s = static_cast<hipStream_t>(stream);
+  int feat = 0;
+  st = setup_lists(a, opts, window, n_persistent, causal, pattern, block_size, d_row_ptr,
+                   d_entries, d_order, n_lead, d_col_ptr, d_entries_kv, d_order_kv, n_lead_kv,
+                   &feat);
+  if (st != TMAC_OK) return st;
+  return launch_status(a, feat, true);
 }
 
 // Row sums of the allocation-free backward: a file-scope device array, one copy
@@ -1254,7 +1752,24 @@ extern "C" int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3], const
                         do_strides, d_lse, d_delta, d_dQ, dq_strides, d_dK, dk_strides, d_dV,
                         dv_strides, B, H, S, dh, window, n_persistent, causal, pattern, block_size,
                         scale, d_row_ptr, d_entries, d_order, n_lead, d_col_ptr, d_entries_kv,
-                        d_order_kv, n_lead_kv, dtype, stream);
+                        d_order_kv, n_lead_kv, dtype, stream, nullptr);
+}
+
+extern "C" int tmac_wattn_bwd_ex(
+    const void* d_Q, const int64_t q_strides[3], const void* d_K, const int64_t k_strides[3],
+    const void* d_V, const int64_t v_strides[3], const void* d_O, const int64_t o_strides[3],
+    const void* d_dO, const int64_t do_strides[3], const float* d_lse, float* d_delta, void* d_dQ,
+    const int64_t dq_strides[3], void* d_dK, const int64_t dk_strides[3], void* d_dV,
+    const int64_t dv_strides[3], int B, int H, int S, int dh, int window, int n_persistent,
+    int causal, int pattern, int block_size, float scale, const int32_t* d_row_ptr,
+    const int32_t* d_entries, const int32_t* d_order, int n_lead, const int32_t* d_col_ptr,
+    const int32_t* d_entries_kv, const int32_t* d_order_kv, int n_lead_kv, int dtype,
+    void* stream, const tmac_attn_opts* opts) {
+  return wattn_bwd_impl(d_Q, q_strides, d_K, k_strides, d_V, v_strides, d_O, o_strides, d_dO,
+                        do_strides, d_lse, d_delta, d_dQ, dq_strides, d_dK, dk_strides, d_dV,
+                        dv_strides, B, H, S, dh, window, n_persistent, causal, pattern, block_size,
+                        scale, d_row_ptr, d_entries, d_order, n_lead, d_col_ptr, d_entries_kv,
+                        d_order_kv, n_lead_kv, dtype, stream, opts);
 }
 
 extern "C" int tmac_wattn_bwd_noalloc(
@@ -1277,5 +1792,5 @@ extern "C" int tmac_wattn_bwd_noalloc(
                         do_strides, d_lse, delta, d_dQ, dq_strides, d_dK, dk_strides, d_dV,
                         dv_strides, B, H, S, dh, window, n_persistent, causal, pattern, block_size,
                         scale, d_row_ptr, d_entries, d_order, n_lead, d_col_ptr, d_entries_kv,
-                        d_order_kv, n_lead_kv, dtype, stream);
+                        d_order_kv, n_lead_kv, dtype, stream, nullptr);
 }

@@ -78,9 +78,9 @@ class BlockSparseAttention(nn.Module):
         return cached[1]
 
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        """x [B, T, d_model] -> [B, T, d_model]. attn_mask is ignored, as in the reference (:218)."""
-        if self.training and self.dropout_p > 0:
-            raise NotImplementedError("attention dropout is not implemented in the HIP kernel")
+        """x [B, T, d_model] -> [B, T, d_model]. attn_mask is ignored, as in the reference (:218).
+        In training, attention weights are dropped with p = dropout (:196-197) and the output
+        projection is followed by nn.Dropout (:342)."""
         B, T, D = x.shape
         qkv = self.qkv_proj(x)
         if self.use_conv:
@@ -90,7 +90,8 @@ class BlockSparseAttention(nn.Module):
         k = k.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         v = v.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         out = windowed_attention(q, k, v, self.window_size, self.n_persistent, self.causal,
-                                 pattern="blockwin", block_size=self.block_size, scale=self.scale)
+                                 pattern="blockwin", block_size=self.block_size, scale=self.scale,
+                                 dropout_p=self.dropout_p if self.training else 0.0)
         out = out.transpose(1, 2).reshape(B, T, self.d_model)
         return self.dropout(self.out_proj(out))
 

@@ -113,13 +113,14 @@ class WindowedAttention(nn.Module):
         return self._mask_cache[key]
 
     def forward(self, x: torch.Tensor, attn_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
-        if attn_mask is not None:
-            raise NotImplementedError(
-                "WindowedAttention on MI355X computes the band + persistent mask inside the "
-                "kernel; a custom attn_mask is not supported (the reference's callers all pass "
-                "attn_mask=None)")
-        if self.training and self.dropout_p > 0:
-            raise NotImplementedError("attention dropout is not implemented in the HIP kernel")
+        """x [B, T, d_model] -> [B, T, d_model] (reference :277-334).
+
+        attn_mask: None (the band + persistent mask, computed inside the kernel) or a
+        caller's mask [T, T] / [B|1, H|1, T, T], bool (True = attend) or additive
+        float, which replaces the band mask as in the reference (:307-315). In
+        training, attention probabilities are dropped with p = dropout (SDPA's
+        dropout_p, :321), and the output projection is followed by nn.Dropout (:332).
+        """
         B, T, D = x.shape
         qkv = self.qkv_proj(x)
         q, k, v = qkv.chunk(3, dim=-1)
@@ -127,6 +128,8 @@ class WindowedAttention(nn.Module):
         q = q.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         k = k.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
         v = v.view(B, T, self.n_heads, self.d_head).transpose(1, 2)
-        out = windowed_attention(q, k, v, self.window_size, self.num_persistent, self.causal)
+        p = self.dropout_p if self.training else 0.0
+        out = windowed_attention(q, k, v, self.window_size, self.num_persistent, self.causal,
+                                 attn_mask=attn_mask, dropout_p=p)
         out = out.transpose(1, 2).reshape(B, T, self.d_model)
         return self.dropout(self.out_proj(out))

@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -34,7 +34,8 @@ _lib = None
 _i, _i64, _u64, _vp, _sz = ctypes.c_int, ctypes.c_int64, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_size_t
 _i64p = ctypes.POINTER(ctypes.c_int64)
 
-# name -> argtypes (every function returns int except tmac_status_string)
+# name -> argtypes (every function returns int except tmac_status_string and
+# tmac_wattn_mask_workspace, set below)
 SIGNATURES = {
     "tmac_abi_version": [],
     "tmac_bell_sample_col_idx": [_u64, _i, _i, _i, _vp],
@@ -60,6 +61,14 @@ SIGNATURES = {
                                _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp,
                                _i, _vp, _vp, _vp, _i, _i, _vp],
+    "tmac_wattn_fwd_ex": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp,
+                          _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
+                          _i, _vp, _vp],
+    "tmac_wattn_bwd_ex": [_vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp,
+                          _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                          _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
+                          _vp, _vp, _vp, _i, _i, _vp, _vp],
+    "tmac_wattn_mask_lists": [_vp, _i, _vp],
     "tmac_dwconv_causal": [_vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_dwconv_causal_bwd_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
     "tmac_dwconv_causal_bwd": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _i,
@@ -96,6 +105,8 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(L, name)
                 fn.argtypes = args
                 fn.restype = _i
+            L.tmac_wattn_mask_workspace.argtypes = [_i, _i, _i]
+            L.tmac_wattn_mask_workspace.restype = _sz
             L.tmac_status_string.argtypes = [_i]
             L.tmac_status_string.restype = ctypes.c_char_p
             got = L.tmac_abi_version()

@@ -16,6 +16,12 @@ partial ones.
 Masks: ``pattern="band"`` is build_band_mask (attn/windowed_attention.py:97-152);
 ``pattern="blockwin"`` is the effective mask of BlockSparseAttention
 (attn/block_sparse_attention.py:277-334) with block size ``block_size``.
+A caller's ``attn_mask`` (bool, True = attend, or additive float, broadcastable
+to [B, H, S, S]) replaces the pattern, as in WindowedAttention.forward
+(:307-315): its tile work lists are built on the device from the tensor
+(``tmac_wattn_mask_lists``) and partial tiles read it element by element.
+``dropout_p`` drops attention probabilities after the softmax with
+Philox4x32-10 decisions recomputed from one seed in forward and backward.
 """
 from __future__ import annotations
 
@@ -275,27 +281,282 @@ def _backward(ctx, grad_out, grad_lse):
 window_attn_fwd.register_autograd(_backward, setup_context=_setup)
 
 
+# ---------------------------------------------------------------------------
+# Caller's mask and dropout (tmac_wattn_fwd_ex / tmac_wattn_bwd_ex).
+
+MASK_BOOL, MASK_ADD_F32 = 0, 1
+
+
+class AttnOpts(ctypes.Structure):
+    """tmac_attn_opts (include/tmac.h)."""
+    _fields_ = [("d_mask", ctypes.c_void_p), ("mask_format", ctypes.c_int),
+                ("mask_batch", ctypes.c_int), ("mask_heads", ctypes.c_int),
+                ("mask_strides", ctypes.c_int64 * 3), ("d_mask_ws", ctypes.c_void_p),
+                ("mask_ws_bytes", ctypes.c_size_t), ("dropout_p", ctypes.c_float),
+                ("dropout_seed", ctypes.c_uint64)]
+
+
+def mask_operand(mask: torch.Tensor, B: int, H: int, S: int):
+    """(tensor, format, mask_batch, mask_heads, strides) of a caller's mask for the kernels.
+
+    mask: bool (True = attend) or floating (added to the scaled scores; -inf =
+    masked), shape [S, S], [H|1, S, S] or [B|1, H|1, S, S] (torch broadcasting,
+    as SDPA's attn_mask); keys need not be contiguous (copied if not). Bool
+    masks are read in place as bytes; other float dtypes are converted to fp32.
+    Expanded (stride-0) batch or head dimensions stay broadcast, without a copy.
+    """
+    if mask.dim() < 2 or mask.dim() > 4 or tuple(mask.shape[-2:]) != (S, S):
+        raise ValueError(f"attn_mask must be [S, S], [H, S, S] or [B, H, S, S] with S = {S}; "
+                         f"got {tuple(mask.shape)}")
+    m = mask
+    while m.dim() < 4:
+        m = m.unsqueeze(0)
+    mb, mh = int(m.shape[0]), int(m.shape[1])
+    if mb not in (1, B) or mh not in (1, H):
+        raise ValueError(f"attn_mask {tuple(mask.shape)} does not broadcast to [{B}, {H}, {S}, {S}]")
+    if m.dtype == torch.bool:
+        fmt = MASK_BOOL
+        if m.stride(3) != 1 or m.stride(2) < S:
+            m = m.contiguous()
+        m = m.view(torch.uint8)
+    elif m.is_floating_point():
+        fmt = MASK_ADD_F32
+        if m.dtype != torch.float32:
+            m = m.float()
+        if m.stride(3) != 1 or m.stride(2) < S:
+            m = m.contiguous()
+    else:
+        raise TypeError(f"attn_mask must be bool or floating point, got {mask.dtype}")
+    if mb > 1 and m.stride(0) == 0:
+        m, mb = m[:1], 1
+    if mh > 1 and m.stride(1) == 0:
+        m, mh = m[:, :1], 1
+    strides = (m.stride(0) if mb > 1 else 0, m.stride(1) if mh > 1 else 0, m.stride(2))
+    return m, fmt, mb, mh, strides
+
+
+def _opts(mask_t, fmt, mb, mh, strides, ws, dropout_p, seed) -> AttnOpts:
+    o = AttnOpts()
+    if mask_t is not None:
+        o.d_mask = mask_t.data_ptr()
+        o.mask_format = fmt
+        o.mask_batch, o.mask_heads = mb, mh
+        o.mask_strides[0], o.mask_strides[1], o.mask_strides[2] = strides
+        o.d_mask_ws = ws.data_ptr()
+        o.mask_ws_bytes = ws.numel()
+    o.dropout_p = float(dropout_p)
+    o.dropout_seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    return o
+
+
+def mask_work_lists(mask: torch.Tensor, B: int, H: int, S: int):
+    """(mask operand, its fields, workspace): the device work lists of a caller's mask,
+    built on the current stream (tmac_wattn_mask_lists); the workspace is uint8."""
+    m, fmt, mb, mh, strides = mask_operand(mask, B, H, S)
+    dev = m.device
+    nbytes = _lib.lib().tmac_wattn_mask_workspace(S, mb, mh)
+    if nbytes <= 0:
+        raise ValueError("tmac_wattn_mask_workspace: invalid mask shape")
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    if ws.data_ptr() % 256:
+        raise RuntimeError("mask workspace is not 256-byte aligned")
+    o = _opts(m, fmt, mb, mh, strides, ws, 0.0, 0)
+    with _lib.device_guard(dev):
+        rc = _lib.lib().tmac_wattn_mask_lists(ctypes.byref(o), S, _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_wattn_mask_lists")
+    return (m, fmt, mb, mh, strides), ws
+
+
+def _window_attn_fwd_ex(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        mask: Optional[torch.Tensor], window_size: int, n_persistent: int,
+                        causal: bool, pattern: int, block_size: int, scale: float,
+                        dropout_p: float, seed: int,
+                        need_lse: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """_window_attn_fwd with a caller's mask (replacing the pattern) and/or dropout.
+
+    Returns (out [B, S, H, dh], lse [B, H, S] or empty, ws): ws is the uint8 work-list
+    workspace of the mask (empty without one), which the backward reuses.
+    """
+    _check_qkv(q, k, v)
+    B, H, S, dh = (int(s) for s in q.shape)
+    dev = _lib.require_device(q, k, v, what="windowed_attention")
+    if not (0.0 <= dropout_p < 1.0):
+        raise ValueError(f"dropout_p must be in [0, 1), got {dropout_p}")
+    out = torch.empty((B, S, H, dh), dtype=q.dtype, device=dev)
+    lse = torch.empty((B, H, S) if need_lse else (0,), dtype=torch.float32, device=dev)
+    ws = torch.empty(0, dtype=torch.uint8, device=dev)
+    if B * H * S == 0:
+        return out, lse, ws
+    row_ptr = entries = order = None
+    n_lead = 0
+    if mask is not None:
+        _lib.require_device(q, mask, what="windowed_attention attn_mask")
+        (m, fmt, mb, mh, strides), ws = mask_work_lists(mask, B, H, S)
+        o = _opts(m, fmt, mb, mh, strides, ws, dropout_p, seed)
+    else:
+        row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
+                                                            pattern, block_size, dev)
+        o = _opts(None, 0, 0, 0, (0, 0, 0), None, dropout_p, seed)
+    o_view = out.permute(0, 2, 1, 3)
+    with _lib.device_guard(dev):
+        rc = _lib.lib().tmac_wattn_fwd_ex(
+            _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
+            _lib.ptr(out), _strides3(o_view), _lib.ptr(lse) if need_lse else None, B, H, S, dh,
+            window_size, n_persistent, int(causal), pattern, block_size, float(scale),
+            _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(order), n_lead,
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(dev), ctypes.byref(o))
+    _lib.check(rc, "tmac_wattn_fwd_ex")
+    return out, lse, ws
+
+
+window_attn_fwd_ex = torch.library.custom_op("titanmac::window_attn_fwd_ex",
+                                             mutates_args=())(_window_attn_fwd_ex)
+
+
+@window_attn_fwd_ex.register_fake
+def _(q, k, v, mask, window_size, n_persistent, causal, pattern, block_size, scale, dropout_p,
+      seed, need_lse=False):
+    B, H, S, dh = q.shape
+    lse = q.new_empty((B, H, S) if need_lse else (0,), dtype=torch.float32)
+    nbytes = 0 if mask is None else _lib.lib().tmac_wattn_mask_workspace(
+        S, *mask_operand(mask, B, H, S)[2:4])
+    return q.new_empty((B, S, H, dh)), lse, q.new_empty((nbytes,), dtype=torch.uint8)
+
+
+def _window_attn_bwd_ex(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
+                        v: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
+                        mask: Optional[torch.Tensor], ws: torch.Tensor, window_size: int,
+                        n_persistent: int, causal: bool, pattern: int, block_size: int,
+                        scale: float, dropout_p: float,
+                        seed: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(dq, dk, dv) of _window_attn_fwd_ex: same mask, workspace, dropout_p and seed."""
+    _check_qkv(q, k, v)
+    B, H, S, dh = (int(s) for s in q.shape)
+    if out.shape != (B, S, H, dh) or grad_out.shape != (B, S, H, dh):
+        raise ValueError("out and grad_out must be [B, S, H, dh] as window_attn_fwd_ex returns")
+    if lse.shape != (B, H, S) or lse.dtype != torch.float32:
+        raise ValueError("lse must be the fp32 [B, H, S] log-sum-exp from window_attn_fwd_ex")
+    dev = _lib.require_device(grad_out, q, k, v, out, lse, what="windowed_attention backward")
+    grad_out = grad_out.to(q.dtype)
+    if grad_out.stride(3) != 1 or any(s % 8 for s in grad_out.stride()[:3]) \
+            or grad_out.data_ptr() % 16:
+        grad_out = grad_out.contiguous()
+    lse = lse.contiguous()
+    grads = [torch.empty((B, S, H, dh), dtype=q.dtype, device=dev) for _ in range(3)]
+    views = [g.permute(0, 2, 1, 3) for g in grads]
+    if B * H * S == 0:
+        return tuple(views)
+    delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    row_ptr = entries = order = col_ptr = entries_kv = order_kv = None
+    n_lead = n_lead_kv = 0
+    if mask is not None:
+        m, fmt, mb, mh, strides = mask_operand(mask, B, H, S)
+        if ws.numel() < _lib.lib().tmac_wattn_mask_workspace(S, mb, mh):
+            raise ValueError("ws must be the mask workspace window_attn_fwd_ex returned")
+        o = _opts(m, fmt, mb, mh, strides, ws, dropout_p, seed)
+    else:
+        row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
+                                                            pattern, block_size, dev)
+        col_ptr, entries_kv, order_kv, n_lead_kv = _device_work_list_kv(
+            S, window_size, n_persistent, causal, pattern, block_size, dev)
+        o = _opts(None, 0, 0, 0, (0, 0, 0), None, dropout_p, seed)
+    o_view, g_view = out.permute(0, 2, 1, 3), grad_out.permute(0, 2, 1, 3)
+    with _lib.device_guard(dev):
+        rc = _lib.lib().tmac_wattn_bwd_ex(
+            _lib.ptr(q), _strides3(q), _lib.ptr(k), _strides3(k), _lib.ptr(v), _strides3(v),
+            _lib.ptr(out), _strides3(o_view), _lib.ptr(grad_out), _strides3(g_view),
+            _lib.ptr(lse), _lib.ptr(delta),
+            _lib.ptr(grads[0]), _strides3(views[0]), _lib.ptr(grads[1]), _strides3(views[1]),
+            _lib.ptr(grads[2]), _strides3(views[2]),
+            B, H, S, dh, window_size, n_persistent, int(causal), pattern, block_size,
+            float(scale), _lib.ptr(row_ptr), _lib.ptr(entries), _lib.ptr(order), n_lead,
+            _lib.ptr(col_ptr), _lib.ptr(entries_kv), _lib.ptr(order_kv), n_lead_kv,
+            _lib.dtype_code(q.dtype), _lib.stream_ptr(dev), ctypes.byref(o))
+    _lib.check(rc, "tmac_wattn_bwd_ex")
+    return tuple(views)
+
+
+window_attn_bwd_ex = torch.library.custom_op("titanmac::window_attn_bwd_ex",
+                                             mutates_args=())(_window_attn_bwd_ex)
+
+
+@window_attn_bwd_ex.register_fake
+def _(grad_out, q, k, v, out, lse, mask, ws, window_size, n_persistent, causal, pattern,
+      block_size, scale, dropout_p, seed):
+    B, H, S, dh = q.shape
+    return tuple(q.new_empty((B, S, H, dh)).permute(0, 2, 1, 3) for _ in range(3))
+
+
+def _setup_ex(ctx, inputs, output):
+    (q, k, v, mask, window_size, n_persistent, causal, pattern, block_size, scale, dropout_p,
+     seed, need_lse) = inputs
+    out, lse, ws = output
+    if need_lse:
+        ctx.save_for_backward(q, k, v, out, lse, mask, ws)
+    ctx.args = (window_size, n_persistent, causal, pattern, block_size, scale, dropout_p, seed)
+    ctx.need_lse = need_lse
+
+
+def _backward_ex(ctx, grad_out, grad_lse, grad_ws):
+    if not ctx.need_lse:
+        raise RuntimeError("window_attn_fwd_ex was called with need_lse=False; its backward "
+                           "needs the log-sum-exp (windowed_attention sets it under autograd)")
+    q, k, v, out, lse, mask, ws = ctx.saved_tensors
+    op = _window_attn_bwd_ex if _lib.direct_call(grad_out, q, k, v) else window_attn_bwd_ex
+    dq, dk, dv = op(grad_out, q, k, v, out, lse, mask, ws, *ctx.args)
+    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
+
+
+window_attn_fwd_ex.register_autograd(_backward_ex, setup_context=_setup_ex)
+
+
+def new_dropout_seed() -> int:
+    """A 63-bit dropout seed from torch's default CPU generator (so torch.manual_seed
+    makes the dropout pattern reproducible, as it does for the reference's dropout)."""
+    return int(torch.randint(0, 2**63 - 1, (), dtype=torch.int64).item())
+
+
 def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_size: int,
                        n_persistent: int, causal: bool = True, pattern="band",
-                       block_size: int = 64, scale: Optional[float] = None) -> torch.Tensor:
+                       block_size: int = 64, scale: Optional[float] = None,
+                       attn_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0,
+                       seed: Optional[int] = None) -> torch.Tensor:
     """softmax(q·kᵀ·scale + mask)·v on allowed pairs only; q/k/v and result [B, H, S, dh].
 
     scale defaults to 1/sqrt(head_dim), SDPA's default (attn/windowed_attention.py:318-323).
     Raises ValueError where build_band_mask does (n_persistent >= S, window_size < 0);
     the block-window pattern also accepts n_persistent == S (only persistent
     tokens), as BlockSparseAttention does.
+
+    attn_mask (optional): bool (True = attend) or additive float mask broadcastable
+    to [B, H, S, S]; it replaces the pattern (window_size, n_persistent, causal,
+    pattern, block_size are then unused), as in WindowedAttention.forward
+    (:307-315). Rows with no allowed key give 0. No gradient flows to the mask.
+    dropout_p: attention dropout after the softmax (kept probabilities scaled by
+    1 / (1 - p)); seed: its Philox seed (default: drawn from torch's CPU
+    generator), reused by the backward.
     """
     S = q.shape[2]
     code = _pattern_code(pattern)
-    if n_persistent > S or (code == _lib.PATTERN_BAND and n_persistent == S):
-        raise ValueError(f"num_persistent_tokens ({n_persistent}) must be < seq_len ({S})")
-    if window_size < 0:
-        raise ValueError(f"window_size must be non-negative, got {window_size}")
+    if attn_mask is None:
+        if n_persistent > S or (code == _lib.PATTERN_BAND and n_persistent == S):
+            raise ValueError(f"num_persistent_tokens ({n_persistent}) must be < seq_len ({S})")
+        if window_size < 0:
+            raise ValueError(f"window_size must be non-negative, got {window_size}")
+    elif attn_mask.requires_grad:
+        raise NotImplementedError("windowed_attention computes no gradient for attn_mask")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
     need_lse = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
                                             or v.requires_grad)
-    op = _window_attn_fwd if _lib.direct_call(q, k, v) else window_attn_fwd
-    out, _ = op(q, k, v, int(window_size), int(n_persistent), bool(causal), code, int(block_size),
-                float(scale), need_lse)
+    if attn_mask is None and dropout_p == 0.0:
+        op = _window_attn_fwd if _lib.direct_call(q, k, v) else window_attn_fwd
+        out, _ = op(q, k, v, int(window_size), int(n_persistent), bool(causal), code,
+                    int(block_size), float(scale), need_lse)
+        return out.transpose(1, 2)
+    if seed is None:
+        seed = new_dropout_seed() if dropout_p > 0.0 else 0
+    op = _window_attn_fwd_ex if _lib.direct_call(q, k, v) else window_attn_fwd_ex
+    out, _, _ = op(q, k, v, attn_mask, int(window_size), int(n_persistent), bool(causal), code,
+                   int(block_size), float(scale), float(dropout_p), int(seed), need_lse)
     return out.transpose(1, 2)
