@@ -183,7 +183,7 @@ def setup_attn(dev, S=None, pattern=None, block_size=64):
     flops = 4 * c["dh"] * pairs * bh
     bytes_ = 4 * bh * c["S"] * c["dh"] * 2
     return dict(launch=launch, flops=flops, bytes=bytes_, tokens=c["B"] * c["S"],
-                keep=(qkv, out, row_ptr, entries, order), q=q, k=k, v=v)
+                keep=(qkv, out, row_ptr, entries, order), q=q, k=k, v=v, fwd_args=args)
 
 
 def setup_attn_bwd(dev, att):
@@ -220,9 +220,56 @@ def setup_attn_bwd(dev, att):
 
     pairs = band_pairs(S, c["window"], c["n_persistent"])
     flops = 10 * dh * pairs * B * H  # dS·K, dSᵀ·Q, Pᵀ·dO, dO·Vᵀ, Q·Kᵀ: 5 products of 2·dh per pair
-    return dict(launch=launch, flops=flops, tokens=B * S, do=do, out=out,
+    return dict(launch=launch, flops=flops, tokens=B * S, do=do, out=out, bwd_args=args,
                 keep=(out, lse, do, grads, delta, row_ptr, entries, order, col_ptr, entries_kv,
                       order_kv))
+
+
+def setup_attn_ex(dev, att, bwd, mask: bool, dropout_p: float):
+    """Config-3 attention through tmac_wattn_fwd_ex / _bwd_ex: the band mask passed as a
+    caller's bool [S, S] tensor (mask=True, work lists built on the device by
+    tmac_wattn_mask_lists) and/or attention dropout. Returns fwd and bwd launches and the
+    mask-list build launch."""
+    import ctypes
+    from titans_core.kernels.window_attn import AttnOpts
+    from titans_core.attn.windowed_attention import build_band_mask
+    c = CFG3
+    B, H, S, dh = c["B"], c["H"], c["S"], c["dh"]
+    L = _lib.lib()
+    o = AttnOpts()
+    o.dropout_p = dropout_p
+    o.dropout_seed = 12345
+    keep = []
+    if mask:
+        m = build_band_mask(S, c["window"], c["n_persistent"], str(dev)).view(torch.uint8)
+        ws = torch.empty(L.tmac_wattn_mask_workspace(S, 1, 1), dtype=torch.uint8, device=dev)
+        o.d_mask, o.mask_format, o.mask_batch, o.mask_heads = m.data_ptr(), 0, 1, 1
+        o.mask_strides[2] = m.stride(0)
+        o.d_mask_ws, o.mask_ws_bytes = ws.data_ptr(), ws.numel()
+        keep += [m, ws]
+    stream = _lib.stream_ptr(dev)
+
+    def lists():
+        rc = L.tmac_wattn_mask_lists(ctypes.byref(o), S, stream)
+        if rc:
+            _lib.check(rc, "tmac_wattn_mask_lists")
+
+    if mask:
+        lists()
+    fa = att["fwd_args"]
+    ba = bwd["bwd_args"]
+
+    def fwd():
+        rc = L.tmac_wattn_fwd_ex(*fa, ctypes.byref(o))
+        if rc:
+            _lib.check(rc, "tmac_wattn_fwd_ex")
+
+    def bwd_launch():
+        rc = L.tmac_wattn_bwd_ex(*ba, ctypes.byref(o))
+        if rc:
+            _lib.check(rc, "tmac_wattn_bwd_ex")
+
+    return dict(fwd=fwd, bwd=bwd_launch, lists=lists if mask else None, keep=(keep, o))
 
 
 def dense_attention_bwd_baseline(att, bwd, steps: int, stream):
@@ -645,7 +692,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 measurement of roofline.traffic (null)")
-    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "dx", "sddmm", "conv",
+    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "attn_ex", "dx",
+                                                     "sddmm", "conv",
                                                      "norm", "mac", "mac_ttm", "memupd", "copy",
                                                      "traffic"])
     args = ap.parse_args()
@@ -715,6 +763,20 @@ def main() -> int:
         out["attn_bwd"] = dict(ms=ms, tokens_per_s=bwd["tokens"] / ms * 1e3,
                                tflops=bwd["flops"] / ms / 1e9)
         out["attn_bwd"]["dense_bwd_ms"] = dense_attention_bwd_baseline(att, bwd, K, stream)
+    if args.mode in ("all", "attn_ex"):
+        if args.mode == "attn_ex":
+            att = setup_attn(dev)
+            bwd = setup_attn_bwd(dev, att)
+        ex = {}
+        for key, mask, p in (("mask", True, 0.0), ("dropout", False, 0.1),
+                             ("mask_dropout", True, 0.1)):
+            wl = setup_attn_ex(dev, att, bwd, mask, p)
+            ex[key] = dict(fwd_ms=timed(wl["fwd"], K, W, stream),
+                           bwd_ms=timed(wl["bwd"], K, W, stream))
+            if wl["lists"] is not None and "lists_ms" not in ex:
+                ex["lists_ms"] = timed(wl["lists"], K, W, stream)
+            del wl
+        out["attn_ex"] = ex
     if args.mode in ("all", "dx", "sddmm"):
         bw = setup_dx_sddmm(dev)
         if args.mode in ("all", "dx"):
@@ -795,6 +857,13 @@ def main() -> int:
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
             "attn_bwd_speedup_vs_dense": round(out["attn_bwd"]["dense_bwd_ms"] / out["attn_bwd"]["ms"], 2),
+            "windowed_attn_fwd_caller_mask_ms": round(out["attn_ex"]["mask"]["fwd_ms"], 5),
+            "windowed_attn_bwd_caller_mask_ms": round(out["attn_ex"]["mask"]["bwd_ms"], 5),
+            "windowed_attn_mask_lists_us": round(out["attn_ex"]["lists_ms"] * 1e3, 2),
+            "windowed_attn_fwd_dropout0.1_ms": round(out["attn_ex"]["dropout"]["fwd_ms"], 5),
+            "windowed_attn_bwd_dropout0.1_ms": round(out["attn_ex"]["dropout"]["bwd_ms"], 5),
+            "windowed_attn_fwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["fwd_ms"], 5),
+            "windowed_attn_bwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["bwd_ms"], 5),
             "bell_fwd_cfg2_m64_us": round(out["spmm"]["m64_ms"] * 1e3, 2),
             "bell_fwd_cfg2_m64_weight_tbs": round(out["spmm"]["m64_weight_tbs"], 3),
             "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),

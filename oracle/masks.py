@@ -135,17 +135,25 @@ def _lists_from_kinds(kinds: np.ndarray, S: int, q_block: int, sub_rows: int):
     return np.asarray(row_ptr, dtype=np.int32), np.asarray(entries, dtype=np.int64).astype(np.int32)
 
 
+BIASED = 3
+
+
 def bias_tile_kinds(bias: np.ndarray, tq: int, tk: int) -> np.ndarray:
     """tile_kinds of a caller's additive mask (bool masks as 0 / -inf): 0 when every
-    pair is -inf, 1 when every pair has bias exactly 0, else 2 (the kernel then
-    adds the bias element by element). Positions past S count as masked."""
+    pair is -inf, 1 when every pair has bias exactly 0, 3 when some allowed pair has
+    a nonzero bias (the kernel then adds the bias element by element), else 2 (the
+    allowed pairs all have bias 0: the kernel masks from a bitmap). Positions past
+    S count as masked."""
     bias = np.asarray(bias)
     if bias.dtype == bool:
-        allowed, zero = bias, bias
+        allowed, zero, nonzero = bias, bias, np.zeros_like(bias)
     else:
         allowed, zero = bias != -np.inf, bias == 0
+        nonzero = allowed & ~zero
     ka, kz = tile_kinds(allowed, tq, tk), tile_kinds(zero, tq, tk)
-    return np.where(kz == FULL, FULL, np.where(ka == EMPTY, EMPTY, PARTIAL)).astype(np.uint8)
+    kn = tile_kinds(nonzero, tq, tk)
+    out = np.where(ka == EMPTY, EMPTY, np.where(kn != EMPTY, BIASED, PARTIAL))
+    return np.where(kz == FULL, FULL, out).astype(np.uint8)
 
 
 def schedule_bias(bias: np.ndarray, q_block: int = 128, sub_rows: int = 32, k_tile: int = 64):

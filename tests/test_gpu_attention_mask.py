@@ -16,7 +16,8 @@ max(1, max |want|), with Δ = rowsum(dO ⊙ O) of the gradients taken from the
 with dropout, O is not a multiple of one V row even where a row attends one
 key, and the exact-O Δ would leave a 16-bit cancellation residue that sums over
 every row attending a key); fp32 within 1e-4 of the largest entry. The device work
-lists of a mask are checked bit for bit against oracle.masks.schedule_bias.
+lists and allowed-pair bitmaps of a mask are checked bit for bit against
+oracle.masks.schedule_bias and the mask itself.
 """
 import numpy as np
 import pytest
@@ -245,11 +246,20 @@ def test_device_work_lists_bit_exact(dev, lead, kind, S):
     cnt_off = ent_off + (2 * rows * n_t * 4 + 255) // 256 * 256
     ent = raw[ent_off:ent_off + 2 * rows * n_t * 4].view(np.int32).reshape(2, rows, n_t)
     cnt = raw[cnt_off:cnt_off + 2 * rows * 4].view(np.int32).reshape(2, rows)
+    bits_off = cnt_off + (2 * rows * 4 + 255) // 256 * 256
+    words = mb * mh * n_b * 128 * n_t
+    bits = raw[bits_off:bits_off + 2 * words * 8].view(np.uint64).reshape(2, mb * mh, n_b * 128, n_t)
     assert np.array_equal(raw[:n_b * 4].view(np.int32), np.arange(n_b))
     m4 = mask.reshape((1,) * (4 - mask.ndim) + mask.shape)
     for r in range(mb * mh):
         one = m4[r // mh, r % mh] if m4.shape[0] > 1 else m4[0, r % mh]
         for side, mm in ((0, one), (1, np.ascontiguousarray(one.T))):
+            # bitmap: word (position p, tile t) bit i = pair (p, 64t + i) allowed
+            allowed = np.zeros((n_b * 128, n_t * 64), dtype=bool)
+            allowed[:S, :S] = (mm != -np.inf) if mm.dtype != bool else mm
+            want_bits = np.packbits(allowed.reshape(n_b * 128, n_t, 64), axis=-1,
+                                    bitorder="little").view(np.uint64)[..., 0]
+            assert np.array_equal(bits[side, r], want_bits), (side, r)
             rp, e = om.schedule_bias(mm)
             for blk in range(n_b):
                 row = r * n_b + blk

@@ -356,9 +356,10 @@ def test_mask_workspace_size(lib):
         n = lib.tmac_wattn_mask_workspace(S, mb, mh)
         n_b, n_t = -(-S // 128), -(-S // 64)
         rows = mb * mh * n_b
+        bitmaps = 2 * mb * mh * n_b * 128 * n_t * 8
         assert n % 256 == 0
-        assert n >= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4
-        assert n <= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + 4 * 256
+        assert n >= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps
+        assert n <= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps + 4 * 256
     for bad in [(0, 1, 1), (64, 0, 1), (64, 1, 0), (-5, 1, 1)]:
         assert lib.tmac_wattn_mask_workspace(*bad) == 0
 

@@ -235,14 +235,25 @@ __host__ __device__ inline Span mask_col_span(const MaskParams& p, int j) {
 struct U32x4 {
   uint32_t x, y, z, w;
 };
-__host__ __device__ inline uint32_t mulhi32(uint32_t a, uint32_t b) {
-  return static_cast<uint32_t>((static_cast<uint64_t>(a) * b) >> 32);
+// 64-bit product of two 32-bit values. On the device one v_mad_u64_u32 gives
+// both halves; left to itself the compiler emits v_mul_hi_u32 and v_mul_lo_u32,
+// two quarter-rate instructions, for the same product.
+__host__ __device__ inline uint64_t mul_wide_u32(uint32_t a, uint32_t m) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint64_t p, carry;  // carry: the instruction's carry-out (an SGPR pair), unused
+  asm("v_mad_u64_u32 %0, %1, %2, %3, 0" : "=v"(p), "=s"(carry) : "v"(a), "s"(m));
+  return p;
+#else
+  return static_cast<uint64_t>(a) * m;
+#endif
 }
 __host__ __device__ inline U32x4 philox4x32_10(U32x4 c, uint32_t k0, uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
-    const uint32_t hi0 = mulhi32(0xD2511F53u, c.x), lo0 = 0xD2511F53u * c.x;
-    const uint32_t hi1 = mulhi32(0xCD9E8D57u, c.z), lo1 = 0xCD9E8D57u * c.z;
+    const uint64_t p0 = mul_wide_u32(c.x, 0xD2511F53u);
+    const uint64_t p1 = mul_wide_u32(c.z, 0xCD9E8D57u);
+    const uint32_t hi0 = static_cast<uint32_t>(p0 >> 32), lo0 = static_cast<uint32_t>(p0);
+    const uint32_t hi1 = static_cast<uint32_t>(p1 >> 32), lo1 = static_cast<uint32_t>(p1);
     c = U32x4{hi1 ^ c.y ^ k0, lo1, hi0 ^ c.w ^ k1, lo0};
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
@@ -261,7 +272,9 @@ struct AttnX {
   int64_t msb, msh, msq; // element strides of the mask's batch, head, query dims (key stride 1)
   int mb1, mh1, MH;      // batch / head dims of size 1 (broadcast); number of mask heads
   const int32_t* cnt;    // custom work lists: entries of each list row
-  int cap;               // entries a list row can hold (row r starts at r * cap)
+  int cap;               // entries a list row can hold (row r starts at r * cap) = 64-wide tiles
+  const uint64_t* bits;  // allowed-pair bitmap: word (mask row, position, tile) holds 64 bits,
+                         // one per position of the other axis in that tile
   uint32_t seed0, seed1; // dropout seed
   uint32_t thresh;       // dropped when the 32-bit draw is below thresh (= p * 2^32)
   float keep_scale;      // 1 / (1 - p)
@@ -270,6 +283,14 @@ struct AttnX {
 // Row of the custom work lists of (b, head): the mask's own (batch, head) row.
 __device__ __forceinline__ int mask_row(const AttnX& x, int b, int hd) {
   return (x.mb1 ? 0 : b) * x.MH + (x.mh1 ? 0 : hd);
+}
+
+// Bitmap word of list position r (a query for the query-major bitmap, a key for the
+// key-major one) against 64-wide tile t of the other axis, in mask row mrow; bit i
+// is position 64t + i. Rows are padded to a multiple of 128.
+__device__ __forceinline__ uint64_t mask_word(const AttnX& x, int mrow, int r, int t, int S) {
+  const int64_t rows = static_cast<int64_t>((S + 127) >> 7) << 7;
+  return x.bits[(mrow * rows + r) * x.cap + t];
 }
 
 // Natural-log bias the caller's mask adds to score (q, k): 0 or -inf for a bool
@@ -303,6 +324,24 @@ __device__ __forceinline__ uint32_t keep4(const AttnX& x, int bh, int q, int k0)
          (static_cast<uint32_t>(r.z >= x.thresh) << 2) |
          (static_cast<uint32_t>(r.w >= x.thresh) << 3);
 }
+// Keep bits of a lane that holds key k and the four queries q0..q0+3 (q0 a
+// multiple of 4), where the four lanes of its quad (lane & ~3 .. +3, all active)
+// hold the keys (k & ~3) + 0..3 with the same q0 and iq = lane & 3 = k & 3: bit 4t
+// of the result is the decision of (q0 + t, k). Each lane draws one Philox call,
+// counter {k / 4, q0 + iq, bh, 0}, whose four words decide the quad's four keys
+// at query q0 + iq; the quad then exchanges those 4-bit groups (DPP broadcasts
+// within the quad), so each decision costs a quarter call, as in the row layout.
+__device__ __forceinline__ uint32_t keep_quad(const AttnX& x, int bh, int q0, int k, int iq) {
+  const uint32_t nib = keep4(x, bh, q0 + iq, k & ~3);
+  uint32_t all = 0;
+  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0x00, 0xf, 0xf, false));
+  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0x55, 0xf, 0xf, false)) << 4;
+  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0xaa, 0xf, 0xf, false)) << 8;
+  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0xff, 0xf, 0xf, false)) << 12;
+  // bit 4t + iq: query q0 + t, key (k & ~3) + iq = k
+  return all >> iq;
+}
+
 // Dropout factor of the single pair (bh, q, k).
 __device__ __forceinline__ float drop1(const AttnX& x, int bh, int q, int k) {
   const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k) >> 2, static_cast<uint32_t>(q),

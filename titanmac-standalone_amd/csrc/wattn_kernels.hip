@@ -45,6 +45,14 @@ constexpr float kLn2 = 0.6931471805599453f;
 // Row log-sum-exp in log2 units for the backward. A row that a caller's mask
 // masks fully has lse = -inf (and output 0): it gets +inf, so each of its
 // probabilities exp2(s - l2) is 0 (also for s = -inf).
+// Caller's-mask slices of kind 2 (allowed pairs all have bias 0): v[j] keeps its
+// score where bit 8(j/4) + j%4 of w is set, else -inf. w holds this lane's 32
+// positions of a 32-wide half tile, already shifted to the lane's origin.
+__device__ __forceinline__ void apply_bits(f32x16& v, uint32_t w) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = ((w >> (8 * (j >> 2) + (j & 3))) & 1u) ? v[j] : -INFINITY;
+}
+
 template <bool CM>
 __device__ __forceinline__ float lse_log2(float lse) {
   const float l2 = lse * kLog2e;
@@ -114,9 +122,10 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
     for (int kk = 0; kk < T::kKk; ++kk) qf[kk] = ldg16(qp + 16 * kk);
   }
 
-  int e0, e1;
+  int e0, e1, mrow = 0;
   if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + qb;
     e0 = row * ax.cap;
     e1 = e0 + ax.cnt[row];
   } else {
@@ -126,6 +135,8 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
   // Scores enter the softmax as st * sc: raw scores times scale·log2e, or, with a
   // caller's mask, already in log2 units (sc = 1).
   const float sc = CM ? 1.f : scale_log2;
+  // caller's mask: this row's allowed-key bits of the current and the next tile
+  uint64_t wb = 0, wb_next = 0;
 
   // K/V tile staging: T::kPasses 16-byte chunks of each tile per thread (rows
   // r0 + pass * T::kRpp, chunk tid % T::kCpr). Offsets within a tile are fixed per
@@ -179,6 +190,7 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
 
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -188,7 +200,10 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, q_row, entries[e + 1] & 0xffff, S);
+    }
 
     if (kind != 0) {
       const uint16_t* kt_lds = smem + (2 * buf) * T::kElems;
@@ -206,10 +221,15 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
       // st[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4 (raw
       // scores; scale_log2 > 0, so the row maximum commutes with the scaling).
       if constexpr (CM) {
-        // log2 units; on partial slices the caller's mask adds its bias (or -inf)
+        // log2 units; partial slices take -inf from the mask's bits (kind 2) or
+        // add the mask's bias element by element (kind 3)
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) st[kh] *= scale_log2;
         if (kind == 2) {
+          const uint64_t w = wb >> (4 * h);
+          apply_bits(st[0], static_cast<uint32_t>(w));
+          apply_bits(st[1], static_cast<uint32_t>(w >> 32));
+        } else if (kind == 3) {
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -293,6 +313,7 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
         }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -388,7 +409,7 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 #pragma unroll
       for (int d = 0; d < D; ++d) acc = fmaf(q[d], kt_lds[j * D + d], acc);
       if constexpr (CM) {
-        if (kind == 2) acc += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
+        if (kind >= 2) acc += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
       } else {
         if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
       }
@@ -553,9 +574,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
   const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
   const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
 
-  int e0, e1;
+  int e0, e1, mrow = 0;
   if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + kb;
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + kb;
     e0 = row * ax.cap;
     e1 = e0 + ax.cnt[row];
   } else {
@@ -612,8 +634,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     dvt[dt] = f32x16{};
   }
 
+  uint64_t wb = 0, wb_next = 0;  // caller's mask: allowed-query bits of this key, two tiles
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, key, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -623,7 +647,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     const int qt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, key, entries[e + 1] & 0xffff, S);
+    }
 
     if (kind != 0) {
       const uint16_t* q_lds = smem + (2 * buf) * T::kElems;
@@ -644,6 +671,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
         if constexpr (CM) {
           s *= scale_log2;
           if (kind == 2) {
+            apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
+          } else if (kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
@@ -665,12 +694,14 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
           const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat[buf][0][32 * qh + 8 * g + 4 * h]);
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][32 * qh + 8 * g + 4 * h]);
           const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+          uint32_t kq = 0;
+          if constexpr (DR) kq = keep_quad(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h, key, l32 & 3);
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int j = 4 * g + t;
             const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
             if constexpr (DR) {
-              const float z = drop1(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h + t, key);
+              const float z = ((kq >> (4 * t)) & 1u) ? ax.keep_scale : 0.f;
               s[j] = pj * z;
               dp[j] = pj * (z * dp[j] - dv4[t]);
             } else {
@@ -696,6 +727,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
       }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -752,9 +784,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
   const float dl = delta[static_cast<int64_t>(bh) * S + min(q_row, S - 1)];
   const uint16_t* Kbh = K + b * ksb + hd * ksh;
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
-  int e0, e1;
+  int e0, e1, mrow = 0;
   if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + qb;
     e0 = row * ax.cap;
     e1 = e0 + ax.cnt[row];
   } else {
@@ -802,8 +835,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
 #pragma unroll
   for (int dt = 0; dt < T::kDt; ++dt) dqt[dt] = f32x16{};
 
+  uint64_t wb = 0, wb_next = 0;  // caller's mask: allowed-key bits of this row, two tiles
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -813,7 +848,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, q_row, entries[e + 1] & 0xffff, S);
+    }
 
     if (kind != 0) {
       const uint16_t* k_lds = smem + (2 * buf) * T::kElems;
@@ -837,6 +875,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) s[kh] *= scale_log2;
         if (kind == 2) {
+          const uint64_t w = wb >> (4 * h);
+          apply_bits(s[0], static_cast<uint32_t>(w));
+          apply_bits(s[1], static_cast<uint32_t>(w >> 32));
+        } else if (kind == 3) {
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -882,6 +924,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
       }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -993,6 +1036,13 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
     __syncthreads();
     const int kind = (ent >> (16 + 2 * sub)) & 3;
     if (kind == 0) continue;
+    uint64_t keep = ~0ull;  // dropout: keep bits of the tile's 64 keys
+    if constexpr (DR) {
+      keep = 0;
+#pragma unroll 1
+      for (int g = 0; g < 16; ++g)
+        keep |= static_cast<uint64_t>(keep4(ax, bh, q_row, kt * 64 + 4 * g)) << (4 * g);
+    }
     for (int j = 0; j < 64; ++j) {
       float sj = 0.f, dp = 0.f;
 #pragma unroll
@@ -1001,13 +1051,13 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
         dp = fmaf(g[d], vt_lds[j * D + d], dp);
       }
       if constexpr (CM) {
-        if (kind == 2) sj += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
+        if (kind >= 2) sj += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
       }
       float pj = __builtin_amdgcn_exp2f(sj - l2);
       if constexpr (!CM) {
         if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
       }
-      if constexpr (DR) dp *= drop1(ax, bh, q_row, kt * 64 + j);
+      if constexpr (DR) dp *= ((keep >> j) & 1) ? ax.keep_scale : 0.f;
       const float ds = pj * (dp - dl);
 #pragma unroll
       for (int d = 0; d < D; ++d) dq[d] = fmaf(ds, kt_lds[j * D + d], dq[d]);
@@ -1120,7 +1170,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
       dpp += __shfl_xor(dpp, 32);
       float sl = sp * scale_log2;
       if constexpr (CM) {
-        if (kind == 2) sl += mask_bias(ax, b, hd, qt * 64 + i, key, S) * kLog2e;
+        if (kind >= 2) sl += mask_bias(ax, b, hd, qt * 64 + i, key, S) * kLog2e;
       }
       float pi = __builtin_amdgcn_exp2f(sl - l2_lds[i]);
       if constexpr (!CM) {
@@ -1156,50 +1206,82 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
 // 1. wattn_mask_kinds_kernel: one workgroup per (mask row mr, 128x128 square
 //    (query block i, key block j)); wave w reads the square's 32 query rows
 //    32w..32w+31, lane l the keys l and 64 + l of each, so every mask byte (or
-//    float) is read once, 64 consecutive keys per wave load. Each 32x32
-//    sub-block gets (any allowed, all allowed with bias 0). From them:
-//      kinds_q[(mr * n_b + i) * n_t + t]  for the key tiles t = 2j, 2j + 1,
+//    float) is read once, 64 consecutive keys per wave load. It writes
+//    - the allowed-pair bitmaps: bits_q word (mr, query q, key tile t) has bit
+//      i for key 64t + i (one ballot per row and tile), bits_kv word (mr, key k,
+//      query tile u) bit i for query 64u + i (each lane gathers 32 rows of its
+//      key, and two waves fill the two halves of a word);
+//    - for each 32x32 sub-block three flags: some pair allowed, every pair
+//      allowed with bias 0, some allowed pair with a nonzero bias; from them
+//      kinds_q[(mr * n_b + i) * n_t + t] for the key tiles t = 2j, 2j + 1 and
 //      kinds_kv[(mr * n_b + j) * n_t + u] for the query tiles u = 2i, 2i + 1,
-//    2 bits per 32-wide slice of the block (query slices for the query-major
-//    lists, key slices for the key-major ones): 0 nothing allowed, 1 all
-//    allowed with bias 0, 2 otherwise. Positions at or past S count as masked.
+//      2 bits per 32-wide slice of the block (query slices for the query-major
+//      lists, key slices for the key-major ones): 0 nothing allowed, 1 all
+//      allowed with bias 0, 2 some allowed and all of those with bias 0 (the
+//      kernels mask from the bitmap), 3 some nonzero bias (the kernels read it).
+//    Positions at or past S count as masked.
 // 2. wattn_mask_compact_kernel: one wave per list row (query-major rows, then
 //    key-major rows): entries[row * n_t + c] = t | kinds << 16 for the tiles t
 //    with a nonzero kind, t ascending, and cnt[row] = their number. Wave 0 also
 //    writes the identity launch order of the blocks.
 __global__ __launch_bounds__(256) void wattn_mask_kinds_kernel(AttnX ax, int S, int n_b, int n_t,
                                                                uint8_t* __restrict__ kinds_q,
-                                                               uint8_t* __restrict__ kinds_kv) {
-  __shared__ uint32_t flags[4];  // per wave: (any, all) bits of its four 32x32 sub-blocks
+                                                               uint8_t* __restrict__ kinds_kv,
+                                                               uint64_t* __restrict__ bits_q,
+                                                               uint32_t* __restrict__ bits_kv) {
+  __shared__ uint32_t flags[4];  // per wave: (any, all, nonzero) bits of its four sub-blocks
   const int j = blockIdx.x, i = blockIdx.y, mr = blockIdx.z;
   const int bm = mr / ax.MH, hm = mr - bm * ax.MH;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  bool any0 = false, all0 = true, any1 = false, all1 = true;
+  const int64_t rows = static_cast<int64_t>(n_b) * 128;  // bitmap rows per mask row
+  bool any0 = false, all0 = true, nz0 = false, any1 = false, all1 = true, nz1 = false;
+  uint32_t col0 = 0, col1 = 0;    // this lane's keys: allowed bits of the 32 rows
+  uint64_t row0 = 0, row1 = 0;    // lane r < 32: allowed bits of row r, key tiles 2j, 2j + 1
   const int k0 = j * 128 + lane, k1 = k0 + 64;
 #pragma unroll 8
   for (int r = 0; r < 32; ++r) {
     const int q = i * 128 + 32 * wave + r;
     const float v0 = mask_bias(ax, bm, hm, q, k0, S);
     const float v1 = mask_bias(ax, bm, hm, q, k1, S);
-    any0 |= !(v0 == -INFINITY);
+    const bool a0 = !(v0 == -INFINITY), a1 = !(v1 == -INFINITY);
+    any0 |= a0;
     all0 &= (v0 == 0.f);
-    any1 |= !(v1 == -INFINITY);
+    nz0 |= a0 & (v0 != 0.f);
+    any1 |= a1;
     all1 &= (v1 == 0.f);
+    nz1 |= a1 & (v1 != 0.f);
+    col0 |= static_cast<uint32_t>(a0) << r;
+    col1 |= static_cast<uint32_t>(a1) << r;
+    const uint64_t w0 = __ballot(a0), w1 = __ballot(a1);
+    if (lane == r) {
+      row0 = w0;
+      row1 = w1;
+    }
+  }
+  // bitmaps
+  const int t0 = 2 * j, u = 2 * i + (wave >> 1);
+  if (lane < 32) {
+    uint64_t* dst = bits_q + (mr * rows + i * 128 + 32 * wave + lane) * n_t + t0;
+    dst[0] = row0;
+    if (t0 + 1 < n_t) dst[1] = row1;
+  }
+  if (u < n_t) {
+    // the 32-bit half (wave & 1) of word (mr, key, u)
+    bits_kv[2 * ((mr * rows + k0) * n_t + u) + (wave & 1)] = col0;
+    bits_kv[2 * ((mr * rows + k1) * n_t + u) + (wave & 1)] = col1;
   }
   // sub-block c (key columns 32c..32c+31 of the square) of this wave's 32 rows
-  const uint64_t ba0 = __ballot(any0), bl0 = __ballot(all0);
-  const uint64_t ba1 = __ballot(any1), bl1 = __ballot(all1);
+  const uint64_t ba0 = __ballot(any0), bl0 = __ballot(all0), bn0 = __ballot(nz0);
+  const uint64_t ba1 = __ballot(any1), bl1 = __ballot(all1), bn1 = __ballot(nz1);
   if (lane == 0) {
+    auto lo = [](uint64_t m) { return static_cast<uint32_t>(m & 0xffffffffull); };
+    auto hi = [](uint64_t m) { return static_cast<uint32_t>(m >> 32); };
     uint32_t f = 0;
-    f |= (static_cast<uint32_t>(ba0 & 0xffffffffull) != 0) << 0;
-    f |= (static_cast<uint32_t>(ba0 >> 32) != 0) << 1;
-    f |= (static_cast<uint32_t>(ba1 & 0xffffffffull) != 0) << 2;
-    f |= (static_cast<uint32_t>(ba1 >> 32) != 0) << 3;
-    f |= (static_cast<uint32_t>(bl0 & 0xffffffffull) == 0xffffffffu) << 4;
-    f |= (static_cast<uint32_t>(bl0 >> 32) == 0xffffffffu) << 5;
-    f |= (static_cast<uint32_t>(bl1 & 0xffffffffull) == 0xffffffffu) << 6;
-    f |= (static_cast<uint32_t>(bl1 >> 32) == 0xffffffffu) << 7;
+    f |= (lo(ba0) != 0) << 0 | (hi(ba0) != 0) << 1 | (lo(ba1) != 0) << 2 | (hi(ba1) != 0) << 3;
+    f |= (lo(bl0) == ~0u) << 4 | (hi(bl0) == ~0u) << 5 | (lo(bl1) == ~0u) << 6 |
+         (hi(bl1) == ~0u) << 7;
+    f |= (lo(bn0) != 0) << 8 | (hi(bn0) != 0) << 9 | (lo(bn1) != 0) << 10 | (hi(bn1) != 0) << 11;
     flags[wave] = f;
   }
   __syncthreads();
@@ -1209,24 +1291,26 @@ __global__ __launch_bounds__(256) void wattn_mask_kinds_kernel(AttnX ax, int S, 
     const int h = tid & 1;
     uint32_t kb = 0;
     for (int sl = 0; sl < 4; ++sl) {
-      bool any, all;
+      bool any, all, nz;
       if (tid < 2) {  // query slice sl, sub-blocks (sl, 2h), (sl, 2h + 1)
         const uint32_t f = flags[sl];
         any = ((f >> (2 * h)) & 3) != 0;
         all = ((f >> (4 + 2 * h)) & 3) == 3;
+        nz = ((f >> (8 + 2 * h)) & 3) != 0;
       } else {  // key slice sl, sub-blocks (2h, sl), (2h + 1, sl)
         const uint32_t f0 = flags[2 * h], f1 = flags[2 * h + 1];
         any = ((f0 >> sl) & 1) | ((f1 >> sl) & 1);
         all = ((f0 >> (4 + sl)) & 1) & ((f1 >> (4 + sl)) & 1);
+        nz = ((f0 >> (8 + sl)) & 1) | ((f1 >> (8 + sl)) & 1);
       }
-      kb |= static_cast<uint32_t>(!any ? 0 : (all ? 1 : 2)) << (2 * sl);
+      kb |= static_cast<uint32_t>(!any ? 0 : (all ? 1 : (nz ? 3 : 2))) << (2 * sl);
     }
     if (tid < 2) {
       const int t = 2 * j + h;
       if (t < n_t) kinds_q[(static_cast<int64_t>(mr) * n_b + i) * n_t + t] = static_cast<uint8_t>(kb);
     } else {
-      const int u = 2 * i + h;
-      if (u < n_t) kinds_kv[(static_cast<int64_t>(mr) * n_b + j) * n_t + u] = static_cast<uint8_t>(kb);
+      const int uu = 2 * i + h;
+      if (uu < n_t) kinds_kv[(static_cast<int64_t>(mr) * n_b + j) * n_t + uu] = static_cast<uint8_t>(kb);
     }
   }
 }
@@ -1260,7 +1344,7 @@ __global__ __launch_bounds__(256) void wattn_mask_compact_kernel(
 // launch order; the tile kinds, query-major rows then key-major rows; the
 // entries, same order; the counts, same order.
 struct MaskWs {
-  size_t order, kinds_q, kinds_kv, ent_q, ent_kv, cnt_q, cnt_kv, total;
+  size_t order, kinds_q, kinds_kv, ent_q, ent_kv, cnt_q, cnt_kv, bits_q, bits_kv, total;
   int64_t rows;  // list rows of each orientation: mask rows x blocks
 };
 inline MaskWs mask_ws_layout(int S, int mask_batch, int mask_heads) {
@@ -1276,7 +1360,11 @@ inline MaskWs mask_ws_layout(int S, int mask_batch, int mask_heads) {
   w.ent_kv = w.ent_q + rows * n_t * 4;
   w.cnt_q = w.ent_q + up(2 * rows * n_t * 4);
   w.cnt_kv = w.cnt_q + rows * 4;
-  w.total = w.cnt_q + up(2 * rows * 4);
+  // bitmaps: one 64-bit word per (mask row, position padded to 128, tile)
+  const size_t words = static_cast<size_t>(mask_batch) * mask_heads * n_b * 128 * n_t;
+  w.bits_q = w.cnt_q + up(2 * rows * 4);
+  w.bits_kv = w.bits_q + words * 8;
+  w.total = w.bits_kv + words * 8;
   return w;
 }
 
@@ -1320,6 +1408,7 @@ int make_attn_x(const tmac_attn_opts* o, int B, int H, int S, AttnX* x, int* fea
     x->MH = o->mask_heads;
     x->cnt = reinterpret_cast<const int32_t*>(static_cast<const char*>(o->d_mask_ws) + w.cnt_q);
     x->cap = (S + 63) / 64;
+    x->bits = reinterpret_cast<const uint64_t*>(static_cast<const char*>(o->d_mask_ws) + w.bits_q);
   }
   return TMAC_OK;
 }
@@ -1501,6 +1590,7 @@ int setup_lists(AttnLaunch& a, const tmac_attn_opts* opts, int window, int n_per
     const MaskWs w = mask_ws_layout(a.S, opts->mask_batch, opts->mask_heads);
     const char* ws = static_cast<const char*>(opts->d_mask_ws);
     a.ax_kv.cnt = reinterpret_cast<const int32_t*>(ws + w.cnt_kv);
+    a.ax_kv.bits = reinterpret_cast<const uint64_t*>(ws + w.bits_kv);
     a.entries = reinterpret_cast<const int32_t*>(ws + w.ent_q);
     a.entries_kv = reinterpret_cast<const int32_t*>(ws + w.ent_kv);
     a.order = a.order_kv = reinterpret_cast<const int32_t*>(ws + w.order);
@@ -1620,7 +1710,9 @@ extern "C" int tmac_wattn_mask_lists(const tmac_attn_opts* opts, int S, void* st
   auto* kinds_q = reinterpret_cast<uint8_t*>(ws + w.kinds_q);
   hipLaunchKernelGGL(wattn_mask_kinds_kernel, dim3(n_b, n_b, static_cast<unsigned>(n_mr)),
                      dim3(256), 0, s, x, S, n_b, n_t, kinds_q,
-                     reinterpret_cast<uint8_t*>(ws + w.kinds_kv));
+                     reinterpret_cast<uint8_t*>(ws + w.kinds_kv),
+                     reinterpret_cast<uint64_t*>(ws + w.bits_q),
+                     reinterpret_cast<uint32_t*>(ws + w.bits_kv));
   const int64_t n_rows = 2 * w.rows;  // query-major rows, then key-major rows
   hipLaunchKernelGGL(wattn_mask_compact_kernel, dim3(static_cast<unsigned>((n_rows + 3) / 4)),
                      dim3(256), 0, s, kinds_q, static_cast<int>(n_rows), n_t, n_b,
