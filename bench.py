@@ -142,6 +142,33 @@ def setup_spmm(dev):
                 bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu, keep=(X, V, Y, idx))
 
 
+def setup_bell_f32(dev):
+    """The fp32 Block-ELL path (fp32 MFMA): forward at config 2's shape, dX and SDDMM at
+    config 4's, fp32 inputs and outputs."""
+    from titans_core.kernels import block_ell as kbe
+    out = {}
+    c = CFG2
+    pat = BlockELLPattern.sample(c["seed"], c["n_brow"], c["n_bcol"], c["width"])
+    X = gen((c["M"], BS * c["n_brow"]), c["seed"] + 1, dtype=torch.float32).to(dev)
+    V = gen((c["n_brow"], c["width"], BS, BS), c["seed"] + 2, 0.02, dtype=torch.float32).to(dev)
+    idx = pat.device_index(dev)
+    out["fwd"] = lambda: kbe._bell_fwd(X, V, idx["col_idx"], idx["t_ptr"], idx["t_row"],
+                                       idx["t_vblk"], idx["order"], None, False)
+    out["fwd_flops"] = 2 * c["M"] * c["n_brow"] * c["width"] * BS * BS
+    c4 = CFG4
+    pat4 = BlockELLPattern.sample(c4["seed"], c4["n_brow"], c4["n_bcol"], c4["width"])
+    X4 = gen((c4["M"], BS * c4["n_brow"]), c4["seed"] + 1, dtype=torch.float32).to(dev)
+    dY4 = gen((c4["M"], BS * c4["n_bcol"]), c4["seed"] + 2, dtype=torch.float32).to(dev)
+    V4 = gen((c4["n_brow"], c4["width"], BS, BS), c4["seed"] + 3, 0.02, dtype=torch.float32).to(dev)
+    idx4 = pat4.device_index(dev)
+    out["dx"] = lambda: kbe._bell_dx(dY4, V4, idx4["col_idx"], c4["n_bcol"])
+    out["sddmm"] = lambda: kbe._bell_sddmm(X4, dY4, idx4["col_idx"], c4["n_brow"], c4["width"],
+                                           torch.float32)
+    out["bwd_flops"] = 2 * c4["M"] * c4["n_brow"] * c4["width"] * BS * BS
+    out["keep"] = (X, V, idx, X4, dY4, V4, idx4)
+    return out
+
+
 def setup_attn(dev, S=None, pattern=None, block_size=64):
     """Windowed attention forward at config 3's shape (S overridable; the pattern
     defaults to the band of WindowedAttention)."""
@@ -693,6 +720,7 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 measurement of roofline.traffic (null)")
     ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "attn_ex", "dx",
+                                                     "bell_f32",
                                                      "sddmm", "conv",
                                                      "norm", "mac", "mac_ttm", "memupd", "copy",
                                                      "traffic"])
@@ -786,6 +814,15 @@ def main() -> int:
             ms = timed(bw["sddmm"], K, W, stream)
             out["sddmm"] = dict(ms=ms, tflops=bw["flops"] / ms / 1e9, gbs=bw["sd_bytes"] / ms / 1e6)
 
+    if args.mode in ("all", "bell_f32"):
+        wl = setup_bell_f32(dev)
+        f_ms = timed(wl["fwd"], K, W, stream)
+        dx_ms = timed(wl["dx"], K, W, stream)
+        sd_ms = timed(wl["sddmm"], K, W, stream)
+        out["bell_f32"] = dict(fwd_ms=f_ms, fwd_tflops=wl["fwd_flops"] / f_ms / 1e9, dx_ms=dx_ms,
+                               dx_tflops=wl["bwd_flops"] / dx_ms / 1e9, sddmm_ms=sd_ms,
+                               sddmm_tflops=wl["bwd_flops"] / sd_ms / 1e9)
+        del wl
     for mode, setup in (("conv", setup_conv), ("norm", setup_norm)):
         if args.mode in ("all", mode):
             wl = setup(dev)
@@ -857,6 +894,11 @@ def main() -> int:
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
             "attn_bwd_speedup_vs_dense": round(out["attn_bwd"]["dense_bwd_ms"] / out["attn_bwd"]["ms"], 2),
+            "bell_fwd_cfg2_fp32_ms": round(out["bell_f32"]["fwd_ms"], 5),
+            "bell_fwd_cfg2_fp32_tflops": round(out["bell_f32"]["fwd_tflops"], 2),
+            "bell_dx_cfg4_fp32_ms": round(out["bell_f32"]["dx_ms"], 5),
+            "bell_sddmm_cfg4_fp32_ms": round(out["bell_f32"]["sddmm_ms"], 5),
+            "bell_fp32_peak_tflops": 157.3,
             "windowed_attn_fwd_caller_mask_ms": round(out["attn_ex"]["mask"]["fwd_ms"], 5),
             "windowed_attn_bwd_caller_mask_ms": round(out["attn_ex"]["mask"]["bwd_ms"], 5),
             "windowed_attn_mask_lists_us": round(out["attn_ex"]["lists_ms"] * 1e3, 2),

@@ -113,9 +113,10 @@ int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int wi
  * MLPBlock.forward (blocks/mlp.py:58,64; bias from nn.Linear, :36,39) and, with
  * epi = TMAC_EPI_GELU, also the erf GELU between them (blocks/mlp.py:42,61).
  * X, Y row-major with leading dimensions ldx, ldy; bias (nullable) has N
- * entries of the same dtype. dtype: TMAC_BF16 or TMAC_F16.
- * K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary (M <= 64 runs a few-row
- * kernel that splits each block-column's list over four waves).
+ * entries of the same dtype. dtype: TMAC_BF16 or TMAC_F16 (16-bit MFMA), or
+ * TMAC_F32 (fp32 MFMA, for fp32 modules outside autocast; ldx, ldy multiples
+ * of 4). K = 64*n_brow, N = 64*n_bcol; M >= 1 arbitrary (16-bit with M <= 64
+ * runs a few-row kernel that splits each block-column's list over four waves).
  * t_ptr/t_row/t_vblk/order: device copies of tmac_bell_transpose's output. */
 int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
                   const int32_t* d_t_ptr, const int32_t* d_t_row,
@@ -128,7 +129,7 @@ int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
  * Replaces autograd's grad_input of F.linear in the MLP backward
  * (loss.backward() at train_titanmac_nested.py:462 through blocks/mlp.py:58,64).
  * For block-row r: dX[:, 64r:64r+64] = Σ_s dY[:, 64·col_idx[r][s] + :] · W[r,s]ᵀ.
- * d_col_idx: device copy of the row-major index. */
+ * d_col_idx: device copy of the row-major index. dtype as for tmac_bell_fwd. */
 int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
                  const int32_t* d_col_idx, void* d_dX, int64_t lddx,
                  int M, int n_brow, int n_bcol, int width, int dtype, void* stream);
@@ -142,7 +143,8 @@ int tmac_bell_sddmm_workspace(int M, int n_brow, int n_bcol, int width,
  * Replaces autograd's grad_weight = dYᵀ·X of F.linear (blocks/mlp.py:58,64),
  * restricted to the Block-ELL pattern. The M reduction is split across
  * workgroups and summed in a fixed order, so results are deterministic.
- * dvals_dtype: TMAC_F32, TMAC_BF16 or TMAC_F16 (inputs: TMAC_BF16 or TMAC_F16). */
+ * dvals_dtype: TMAC_F32, TMAC_BF16 or TMAC_F16 (inputs, dtype: TMAC_BF16,
+ * TMAC_F16 or TMAC_F32). */
 int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, int64_t lddy,
                     const int32_t* d_col_idx, void* d_dvals, int dvals_dtype,
                     void* d_ws, size_t ws_bytes,

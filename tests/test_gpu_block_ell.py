@@ -2,7 +2,8 @@
 
 Tolerance for 16-bit outputs against the fp64 oracle on the same (16-bit
 rounded) inputs: |got - want| <= 2e-2 + 1e-2 |want| (bf16 bar; fp16 is
-tighter in practice). fp32 SDDMM output: rtol 1e-4 of the block's scale.
+tighter in practice). fp32 SDDMM output: rtol 1e-4 of the block's scale. The
+fp32 path (fp32 inputs, fp32 MFMA): within 1e-4 of the largest entry.
 """
 import numpy as np
 import pytest
@@ -62,6 +63,88 @@ def test_fwd_dx_sddmm_parity(dev, dtype, M, n_brow, n_bcol, width):
     close(dx.float().cpu(), ob.dx(dYn, pat.col_idx, Vn, n_bcol))
     want = ob.sddmm(Xn, dYn, pat.col_idx)
     close(dv.cpu(), want, atol=1e-4 * max(1.0, np.abs(want).max()), rtol=1e-4)
+
+
+def close_rel(got, want, rtol=1e-4, what=""):
+    """fp32 bar: |got - want| <= rtol * max(1, max |want|) elementwise."""
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    sc = max(1.0, float(np.abs(want).max())) if want.size else 1.0
+    err = np.abs(got - want).max() / sc if want.size else 0.0
+    assert err <= rtol, f"{what} max err {err:.3g} (scale {sc:.3g})"
+
+
+@pytest.mark.parametrize("M,n_brow,n_bcol,width", SHAPES)
+def test_fwd_dx_sddmm_parity_fp32(dev, M, n_brow, n_bcol, width):
+    """fp32 path (fp32 MFMA, no autocast) against the fp64 oracle on the same fp32
+    inputs: within 1e-4 of the largest entry (relative)."""
+    pat, X, V, dY, b = data(M, n_brow, n_bcol, width, torch.float32, seed=M + width)
+    Xn, Vn, dYn, bn = (t.double().numpy() for t in (X, V, dY, b))
+    idx = pat.device_index(dev)
+    Xd, Vd, dYd, bd = (t.to(dev) for t in (X, V, dY, b))
+    y = kb.block_ell_mm(Xd, Vd, pat)
+    yb = kb.block_ell_mm(Xd, Vd, pat, bd)
+    yg = kb.block_ell_mm(Xd, Vd, pat, bd, activation="gelu")
+    dx = kb.bell_dx(dYd, Vd, idx["col_idx"], n_bcol)
+    dv = kb.bell_sddmm(Xd, dYd, idx["col_idx"], n_brow, width, torch.float32)
+    torch.cuda.synchronize()
+    assert y.dtype == dx.dtype == dv.dtype == torch.float32
+    ref = ob.fwd(Xn, pat.col_idx, Vn, n_bcol)
+    close_rel(y.cpu(), ref, what="y")
+    close_rel(yb.cpu(), ref + bn, what="y + b")
+    close_rel(yg.cpu(), ob.gelu_erf(ref + bn), what="gelu(y + b)")
+    close_rel(dx.cpu(), ob.dx(dYn, pat.col_idx, Vn, n_bcol), what="dx")
+    close_rel(dv.cpu(), ob.sddmm(Xn, dYn, pat.col_idx), what="dW")
+
+
+def test_fp32_config4_shape_and_determinism(dev):
+    """Config 4's shape (M = 32768, 640 -> 2560 at 50%) in fp32: dX on sampled rows
+    and dW on all 200 blocks against the fp64 oracle; reruns bit-identical."""
+    M, n_brow, n_bcol, width = 32768, 10, 40, 20
+    pat, X, V, dY, _ = data(M, n_brow, n_bcol, width, torch.float32, seed=4)
+    idx = pat.device_index(dev)
+    Xd, Vd, dYd = X.to(dev), V.to(dev), dY.to(dev)
+    dx = kb.bell_dx(dYd, Vd, idx["col_idx"], n_bcol)
+    dv = kb.bell_sddmm(Xd, dYd, idx["col_idx"], n_brow, width, torch.float32)
+    y = kb.block_ell_mm(Xd, Vd, pat)
+    assert torch.equal(dx, kb.bell_dx(dYd, Vd, idx["col_idx"], n_bcol))
+    assert torch.equal(dv, kb.bell_sddmm(Xd, dYd, idx["col_idx"], n_brow, width, torch.float32))
+    assert torch.equal(y, kb.block_ell_mm(Xd, Vd, pat))
+    rows = np.random.default_rng(0).choice(M, 256, replace=False)
+    rows = np.unique(np.concatenate([rows, [0, 1, 127, 128, M - 1]]))
+    Xn, Vn, dYn = X.double().numpy(), V.double().numpy(), dY.double().numpy()
+    close_rel(dx.cpu().numpy()[rows], ob.dx(dYn[rows], pat.col_idx, Vn, n_bcol), what="dx")
+    close_rel(y.cpu().numpy()[rows], ob.fwd(Xn[rows], pat.col_idx, Vn, n_bcol), what="y")
+    close_rel(dv.cpu(), ob.sddmm(Xn, dYn, pat.col_idx), what="dW")
+
+
+def test_mlp_block_ell_fp32_training_matches_dense_fp64(dev):
+    """An fp32 Block-ELL MLP (fc2(gelu(fc1(x)))) trains without autocast: output and the
+    gradients of x, both layers' stored blocks and biases against fp64 autograd of the
+    same dense weights on the CPU, within 1e-4 of each tensor's largest entry."""
+    from titans_core.blocks.mlp import MLPBlock
+    torch.manual_seed(3)
+    mlp = MLPBlock(192, 384, block_ell=True, density=0.5).to(dev)
+    assert mlp.fc1.values.dtype == torch.float32
+    x = torch.randn(2, 77, 192, device=dev, requires_grad=True)
+    y = mlp(x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    W1 = mlp.fc1.to_dense_weight().detach().double().cpu().requires_grad_(True)
+    W2 = mlp.fc2.to_dense_weight().detach().double().cpu().requires_grad_(True)
+    b1 = mlp.fc1.bias.detach().double().cpu().requires_grad_(True)
+    b2 = mlp.fc2.bias.detach().double().cpu().requires_grad_(True)
+    xd = x.detach().double().cpu().requires_grad_(True)
+    F = torch.nn.functional
+    yd = F.linear(F.gelu(F.linear(xd, W1, b1)), W2, b2)
+    yd.backward(gy.double().cpu())
+    close_rel(y.detach().cpu(), yd.detach(), what="y")
+    close_rel(x.grad.cpu(), xd.grad, what="dx")
+    close_rel(mlp.fc1.bias.grad.cpu(), b1.grad, what="db1")
+    close_rel(mlp.fc2.bias.grad.cpu(), b2.grad, what="db2")
+    for lin, W in ((mlp.fc1, W1), (mlp.fc2, W2)):
+        want = ob.from_dense(W.grad.t().contiguous().numpy(), lin.col_idx.cpu().numpy())
+        close_rel(lin.values.grad.cpu(), want, what="dvalues")
 
 
 @pytest.mark.parametrize("M", [70, 20])

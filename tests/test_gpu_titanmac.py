@@ -298,6 +298,27 @@ def test_titanmac_bf16_block_ell_mlp_matches_oracle(dev):
     assert abs(out["memory_loss"].float().item() - wloss) <= 5e-2 * abs(wloss)
 
 
+def test_titanmac_fp32_block_ell_mlp_matches_oracle(dev):
+    """An fp32 TitanMAC with the Block-ELL MLP, no autocast (the fp32 Block-ELL kernels):
+    MAC, block-sparse attention, read-only memory; logits within 1e-4 of the largest."""
+    torch.manual_seed(15)
+    cfg = tc.TitanMACConfig(vocab_size=97, d_model=128, n_heads=2, n_layers=2, d_ff=256,
+                            max_seq_len=256, window_size=64, n_persistent=4, use_neural_memory=True,
+                            segment_size=64, n_memory_tokens=8, mlp_block_ell=True,
+                            mlp_density=0.5)
+    m = tc.TitanMAC(cfg).to(dev).eval()
+    assert m.layers[0].mlp.fc1.values.dtype == torch.float32
+    ids = torch.randint(0, 97, (2, 150), generator=torch.Generator().manual_seed(16))
+    with torch.no_grad():
+        out = m(ids.to(dev))
+    want, wloss, _ = ot.forward(_oracle_params(m), dict(
+        vocab_size=97, d_model=128, n_heads=2, n_layers=2, window_size=64, n_persistent=4,
+        use_neural_memory=True, segment_size=64, n_memory_tokens=8, block_size=64),
+        ids.numpy(), update=False)
+    close_rel(out["logits"], want, 1e-4, "logits")
+    assert abs(out["memory_loss"].item() - wloss) <= 1e-4 * abs(wloss)
+
+
 def test_titanmac_mac_training_step_runs_on_hip(dev):
     """A training step of the MAC model: sequential segments with memory updates, backward
     through every HIP op; gradients finite, memory parameters moved."""

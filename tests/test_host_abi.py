@@ -195,8 +195,10 @@ def test_bell_fwd_argument_errors(lib):
     assert lib.tmac_bell_fwd(*[None if i == 0 else a for i, a in enumerate(ok)]) == -1
     bad = list(ok); bad[13] = 161
     assert lib.tmac_bell_fwd(*bad) == -2          # width > n_bcol
-    bad = list(ok); bad[14] = 0
-    assert lib.tmac_bell_fwd(*bad) == -4          # fp32 not supported by the MFMA kernel
+    bad = list(ok); bad[14] = 9
+    assert lib.tmac_bell_fwd(*bad) == -4          # unknown dtype
+    bad = list(ok); bad[14] = 0; bad[1] = 2562
+    assert lib.tmac_bell_fwd(*bad) == -5          # fp32: ldx in whole 16-byte vectors
     bad = list(ok); bad[15] = 7
     assert lib.tmac_bell_fwd(*bad) == -8          # unknown epilogue
     bad = list(ok); bad[1] = 2000
@@ -209,7 +211,8 @@ def test_bell_fwd_argument_errors(lib):
 
 def test_bell_dx_and_sddmm_argument_errors(lib):
     assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 0, 10, 40, 20, 1, None) == -2
-    assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 100, 10, 40, 20, 0, None) == -4
+    assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 100, 10, 40, 20, 3, None) == -4
+    assert lib.tmac_bell_dx(FAKE, 2562, FAKE, FAKE, FAKE, 640, 100, 10, 40, 20, 0, None) == -5
     ws = ctypes.c_size_t(0)
     assert lib.tmac_bell_sddmm_workspace(32768, 10, 40, 20, ctypes.byref(ws)) == 0 and ws.value > 0
     args = [FAKE, 640, FAKE, 2560, FAKE, FAKE, 0, FAKE, ws.value - 1, 32768, 10, 40, 20, 1, None]

@@ -549,6 +549,227 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
       }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 path (fp32 modules without autocast): the same three products on
+// v_mfma_f32_32x32x2_f32, fp32 products and fp32 accumulation.
+//
+// Gather GEMM (forward and dX): a workgroup owns a 128-row by 64-column output
+// tile and walks the same list as the 16-bit kernel. Per list entry it stages
+// the 128x64 activation tile (row-major) and the weight block as Bᵀ ([n][k]:
+// transposed while staging for the forward, as stored for dX) in LDS, rows
+// padded to 68 floats so the 16-byte reads of 16 consecutive rows hit all 64
+// banks once; the next entry's tiles are prefetched into registers during the
+// current entry's math. Wave w computes output rows 32w..32w+31 against both
+// 32-column halves. An MFMA step sums k = 4u + q (lanes 0-31) and 32 + 4u + q
+// (lanes 32-63), so each lane's operands for four steps are one 16-byte read
+// of its own row.
+constexpr int kBMf = 128;  // output rows per fp32 workgroup (4 waves x 32)
+constexpr int kPf = 68;    // LDS row pitch of the fp32 tiles, floats
+
+__device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <bool FWD>
+__global__ __launch_bounds__(256, 2) void bell_gemm_f32_kernel(
+    const float* __restrict__ A, int64_t lda, const float* __restrict__ vals,
+    const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ in_blk,
+    const int32_t* __restrict__ t_vblk, const int32_t* __restrict__ order,
+    const float* __restrict__ bias, int epi, float* __restrict__ Y, int64_t ldy, int M, int n_out,
+    int width, int n_mtiles, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) float xs[kBMf * kPf];  // activation tile [m][k]
+  __shared__ __attribute__((aligned(16))) float ws[64 * kPf];    // weight block as Bᵀ [n][k]
+
+  const int logical = xcd_logical_id(per_xcd);
+  if (logical >= n_mtiles * n_out) return;
+  const int mtile = logical / n_out;
+  const int oi = logical - mtile * n_out;
+  const int ob = FWD ? order[oi] : oi;
+  const int e0 = FWD ? t_ptr[ob] : ob * width;
+  const int e1 = FWD ? t_ptr[ob + 1] : e0 + width;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int m0 = mtile * kBMf;
+
+  // Staging: activation rows 16p + tid/16 (p = 0..7), 16-byte chunk tid % 16 (16
+  // threads per 256-byte row); weight block: dX rows 16p + tid/16 as they are,
+  // forward rows kk = tid % 64 with chunk tid/64 + 4p, written transposed.
+  const int srow = tid >> 4, schunk = tid & 15;
+  int64_t xoff[8];
+#pragma unroll
+  for (int p = 0; p < 8; ++p)
+    xoff[p] = static_cast<int64_t>(min(m0 + 16 * p + srow, M - 1)) * lda + 4 * schunk;
+  f32x4 px[8], pw[4];
+  auto gload = [&](int e) __attribute__((always_inline)) {
+    const float* xb = A + static_cast<int64_t>(in_blk[e]) * 64;
+    const float* wb = vals + static_cast<int64_t>(FWD ? t_vblk[e] : e) * 4096;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) px[p] = *reinterpret_cast<const f32x4*>(xb + xoff[p]);
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (FWD)
+        pw[p] = *reinterpret_cast<const f32x4*>(wb + (tid & 63) * 64 + 4 * ((tid >> 6) + 4 * p));
+      else
+        pw[p] = *reinterpret_cast<const f32x4*>(wb + (16 * p + srow) * 64 + 4 * schunk);
+    }
+  };
+  auto sstore = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      *reinterpret_cast<f32x4*>(xs + (16 * p + srow) * kPf + 4 * schunk) = px[p];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      if constexpr (FWD) {
+        const int kk = tid & 63, n0 = 4 * ((tid >> 6) + 4 * p);
+        ws[(n0 + 0) * kPf + kk] = pw[p].x;
+        ws[(n0 + 1) * kPf + kk] = pw[p].y;
+        ws[(n0 + 2) * kPf + kk] = pw[p].z;
+        ws[(n0 + 3) * kPf + kk] = pw[p].w;
+      } else {
+        *reinterpret_cast<f32x4*>(ws + (16 * p + srow) * kPf + 4 * schunk) = pw[p];
+      }
+    }
+  };
+
+  f32x16 acc[2];
+  acc[0] = f32x16{};
+  acc[1] = f32x16{};
+  if (e0 < e1) gload(e0);
+  const float* xa = xs + (32 * wave + l32) * kPf + 32 * h;
+  const float* wa0 = ws + l32 * kPf + 32 * h;
+  const float* wa1 = ws + (32 + l32) * kPf + 32 * h;
+  for (int e = e0; e < e1; ++e) {
+    __syncthreads();  // the previous entry's reads of xs / ws are done
+    sstore();
+    __syncthreads();
+    if (e + 1 < e1) gload(e + 1);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(xa + 4 * u);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(wa0 + 4 * u);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(wa1 + 4 * u);
+      acc[0] = mfma_f32(a.x, b0.x, acc[0]);
+      acc[1] = mfma_f32(a.x, b1.x, acc[1]);
+      acc[0] = mfma_f32(a.y, b0.y, acc[0]);
+      acc[1] = mfma_f32(a.y, b1.y, acc[1]);
+      acc[0] = mfma_f32(a.z, b0.z, acc[0]);
+      acc[1] = mfma_f32(a.z, b1.z, acc[1]);
+      acc[0] = mfma_f32(a.w, b0.w, acc[0]);
+      acc[1] = mfma_f32(a.w, b1.w, acc[1]);
+    }
+  }
+
+  // acc[ct][j] = out[m0 + 32w + 8(j/4) + 4h + j%4][64 ob + 32 ct + l32]
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int col = 64 * ob + 32 * ct + l32;
+    const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int row = m0 + 32 * wave + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (row >= M) continue;
+      float v = acc[ct][j] + bv;
+      if (epi == TMAC_EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
+      Y[static_cast<int64_t>(row) * ldy + col] = v;
+    }
+  }
+}
+
+// fp32 SDDMM: the work split of bell_sddmm_kernel (a workgroup per M-range,
+// block-row r and four slots, wave w on slot 4 sg + w). Per 32-row step the
+// workgroup stages X[m:m+32, 64r:+64] and each wave its own dY[m:m+32, 64c:+64]
+// in LDS (rows past the range are zero); the wave's 64x64 block is four 32x32
+// MFMA tiles, an MFMA step summing rows m + 2s (lanes 0-31) and m + 2s + 1
+// (lanes 32-63). Partial sums go to the workspace as in the 16-bit kernel.
+__global__ __launch_bounds__(256, 2) void bell_sddmm_f32_kernel(
+    const float* __restrict__ X, int64_t ldx, const float* __restrict__ dY, int64_t lddy,
+    const int32_t* __restrict__ col_idx, float* __restrict__ part, int M, int n_brow, int width,
+    int n_sgroups, int rows_per_split, int n_splits, int per_xcd) {
+  __shared__ __attribute__((aligned(16))) float xs[32 * 64];
+  __shared__ __attribute__((aligned(16))) float ds[4][32 * 64];
+
+  const int per_split = n_brow * n_sgroups;
+  const int logical = xcd_logical_id(per_xcd);
+  if (logical >= n_splits * per_split) return;
+  const int split = logical / per_split;
+  const int rem = logical - split * per_split;
+  const int r = rem / n_sgroups;
+  const int sg = rem - r * n_sgroups;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int s = sg * 4 + wave;
+  const bool active = s < width;
+  const int c = col_idx[r * width + min(s, width - 1)];  // inactive waves stage a valid tile
+  const int m_lo = split * rows_per_split;
+  const int m_hi = min(M, m_lo + rows_per_split);
+
+  // X: rows tid/16 and 16 + tid/16, chunk tid % 16; dY: the wave's lanes, rows
+  // 4p + lane/16 (p = 0..7), chunk lane % 16.
+  const int xr = tid >> 4, xc = tid & 15, dr = lane >> 4, dc = lane & 15;
+  f32x4 px[2], pd[8];
+  auto gload = [&](int m) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const int row = m + 16 * p + xr;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(
+          X + static_cast<int64_t>(min(row, M - 1)) * ldx + 64 * r + 4 * xc);
+      px[p] = row < m_hi ? v : f32x4{};
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int row = min(m + 4 * p + dr, M - 1);
+      pd[p] = *reinterpret_cast<const f32x4*>(dY + static_cast<int64_t>(row) * lddy + 64 * c + 4 * dc);
+    }
+  };
+  auto sstore = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < 2; ++p) *reinterpret_cast<f32x4*>(xs + (16 * p + xr) * 64 + 4 * xc) = px[p];
+#pragma unroll
+    for (int p = 0; p < 8; ++p)
+      *reinterpret_cast<f32x4*>(ds[wave] + (4 * p + dr) * 64 + 4 * dc) = pd[p];
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b) acc[a][b] = f32x16{};
+  if (m_lo < m_hi) gload(m_lo);
+  for (int m = m_lo; m < m_hi; m += 32) {
+    __syncthreads();
+    sstore();
+    __syncthreads();
+    if (m + 32 < m_hi) gload(m + 32);
+    const float* dsw = ds[wave];
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const int row = 2 * st + h;
+      const float a0 = xs[row * 64 + l32], a1 = xs[row * 64 + 32 + l32];
+      const float b0 = dsw[row * 64 + l32], b1 = dsw[row * 64 + 32 + l32];
+      acc[0][0] = mfma_f32(a0, b0, acc[0][0]);
+      acc[0][1] = mfma_f32(a0, b1, acc[0][1]);
+      acc[1][0] = mfma_f32(a1, b0, acc[1][0]);
+      acc[1][1] = mfma_f32(a1, b1, acc[1][1]);
+    }
+  }
+
+  if (!active) return;
+  float* dst = part + (static_cast<int64_t>(split) * n_brow * width + r * width + s) * 4096;
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int kk = 32 * a + 8 * (j >> 2) + 4 * h + (j & 3);
+        dst[kk * 64 + 32 * b + l32] = acc[a][b][j];
+      }
+}
+
 // dvals[i] = Σ_split part[split][i], splits added in ascending order.
 template <int OUT>
 __global__ __launch_bounds__(256) void bell_sddmm_reduce_kernel(const float* __restrict__ part,
@@ -605,13 +826,26 @@ extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
   if (!d_X || !d_vals || !d_t_ptr || !d_t_row || !d_t_vblk || !d_order || !d_Y) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
   if (epi != TMAC_EPI_NONE && epi != TMAC_EPI_GELU) return TMAC_ERR_VALUE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (ldx < K || ldy < N) return TMAC_ERR_SHAPE;
-  if (!aligned16(d_X) || !aligned16(d_vals) || !aligned16(d_Y) || (ldx % 8) || (ldy % 8))
+  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16 bytes
+  if (!aligned16(d_X) || !aligned16(d_vals) || !aligned16(d_Y) || (ldx % vec) || (ldy % vec))
     return TMAC_ERR_ALIGN;
   if (d_bias && !aligned16(d_bias)) return TMAC_ERR_ALIGN;
+  if (dtype == TMAC_F32) {
+    const int n_mt = (M + kBMf - 1) / kBMf;
+    const int64_t tot = static_cast<int64_t>(n_mt) * n_bcol;
+    if (tot > (1ll << 30)) return TMAC_ERR_SHAPE;
+    const int pxcd = static_cast<int>((tot + 7) / 8);
+    hipLaunchKernelGGL((bell_gemm_f32_kernel<true>), dim3(8 * pxcd), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const float*>(d_X), ldx,
+                       static_cast<const float*>(d_vals), d_t_ptr, d_t_row, d_t_vblk, d_order,
+                       static_cast<const float*>(d_bias), epi, static_cast<float*>(d_Y), ldy, M,
+                       n_bcol, width, n_mt, pxcd);
+    return launch_status();
+  }
   const int n_mtiles = (M + kBM - 1) / kBM;
   const int64_t total = static_cast<int64_t>(n_mtiles) * n_bcol;
   if (total > (1ll << 30)) return TMAC_ERR_SHAPE;
@@ -647,11 +881,23 @@ extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
   if (!d_dY || !d_vals || !d_col_idx || !d_dX) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (lddy < N || lddx < K) return TMAC_ERR_SHAPE;
-  if (!aligned16(d_dY) || !aligned16(d_vals) || !aligned16(d_dX) || (lddy % 8) || (lddx % 8))
+  const int vec = dtype == TMAC_F32 ? 4 : 8;
+  if (!aligned16(d_dY) || !aligned16(d_vals) || !aligned16(d_dX) || (lddy % vec) || (lddx % vec))
     return TMAC_ERR_ALIGN;
+  if (dtype == TMAC_F32) {
+    const int n_mt = (M + kBMf - 1) / kBMf;
+    const int64_t tot = static_cast<int64_t>(n_mt) * n_brow;
+    if (tot > (1ll << 30)) return TMAC_ERR_SHAPE;
+    const int pxcd = static_cast<int>((tot + 7) / 8);
+    hipLaunchKernelGGL((bell_gemm_f32_kernel<false>), dim3(8 * pxcd), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), static_cast<const float*>(d_dY), lddy,
+                       static_cast<const float*>(d_vals), nullptr, d_col_idx, nullptr, nullptr,
+                       nullptr, 0, static_cast<float*>(d_dX), lddx, M, n_brow, width, n_mt, pxcd);
+    return launch_status();
+  }
   const int n_mtiles = (M + kBM - 1) / kBM;
   const int64_t total = static_cast<int64_t>(n_mtiles) * n_brow;
   if (total > (1ll << 30)) return TMAC_ERR_SHAPE;
@@ -689,12 +935,13 @@ extern "C" int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, i
   if (!d_X || !d_dY || !d_col_idx || !d_dvals) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
   if (dvals_dtype != TMAC_F32 && dvals_dtype != TMAC_BF16 && dvals_dtype != TMAC_F16)
     return TMAC_ERR_DTYPE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
   if (ldx < K || lddy < N) return TMAC_ERR_SHAPE;
-  if (!aligned16(d_X) || !aligned16(d_dY) || !aligned16(d_dvals) || (ldx % 8) || (lddy % 8))
+  const int vec = dtype == TMAC_F32 ? 4 : 8;
+  if (!aligned16(d_X) || !aligned16(d_dY) || !aligned16(d_dvals) || (ldx % vec) || (lddy % vec))
     return TMAC_ERR_ALIGN;
   int n_splits, rows_per_split;
   sddmm_split(M, n_brow, width, &n_splits, &rows_per_split);
@@ -708,7 +955,11 @@ extern "C" int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, i
   const auto* X = static_cast<const uint16_t*>(d_X);
   const auto* dY = static_cast<const uint16_t*>(d_dY);
   float* part = static_cast<float*>(d_ws);
-  if (dtype == TMAC_BF16)
+  if (dtype == TMAC_F32)
+    hipLaunchKernelGGL(bell_sddmm_f32_kernel, dim3(8 * per_xcd), dim3(256), 0, s,
+                       static_cast<const float*>(d_X), ldx, static_cast<const float*>(d_dY), lddy,
+                       d_col_idx, part, M, n_brow, width, n_sg, rows_per_split, n_splits, per_xcd);
+  else if (dtype == TMAC_BF16)
     hipLaunchKernelGGL((bell_sddmm_kernel<TMAC_BF16>), dim3(8 * per_xcd), dim3(256), 0, s, X, ldx,
                        dY, lddy, d_col_idx, part, M, n_brow, width, n_sg, rows_per_split, n_splits,
                        per_xcd);

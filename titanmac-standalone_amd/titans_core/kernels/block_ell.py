@@ -125,8 +125,8 @@ def _rows(t: torch.Tensor, features: int) -> Tuple[torch.Tensor, int]:
 def _check_values(values: torch.Tensor, what: str) -> None:
     if values.dim() != 4 or values.shape[2:] != (BLOCK, BLOCK):
         raise ValueError(f"{what}: values must be [n_brow, width, 64, 64], got {tuple(values.shape)}")
-    if values.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"{what}: the MFMA kernels take bfloat16 or float16, got {values.dtype}")
+    if values.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise TypeError(f"{what}: the kernels take bfloat16, float16 or float32, got {values.dtype}")
 
 
 def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
@@ -288,8 +288,9 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
     activation: None or "gelu" (erf form, as nn.GELU()). The GELU is fused into
     the kernel's store when no gradient is required; otherwise it is applied as
     a separate op so autograd can differentiate it. The kernels compute in
-    bfloat16 / float16 (fp32 accumulation); under torch.autocast the inputs are
-    cast to the autocast dtype first, as for nn.Linear.
+    bfloat16 / float16 (fp32 accumulation) or float32 (fp32 MFMA); under
+    torch.autocast the inputs are cast to the autocast dtype first, as for
+    nn.Linear.
     """
     if activation not in (None, "gelu"):
         raise ValueError(f"unsupported activation {activation!r}")
