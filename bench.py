@@ -717,6 +717,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-dense", action="store_true",
+                    help="with --mode attn_bwd: skip the dense baseline (profiling runs)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 measurement of roofline.traffic (null)")
     ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "attn_ex", "dx",
@@ -790,7 +792,8 @@ def main() -> int:
         ms = timed(bwd["launch"], K, W, stream)
         out["attn_bwd"] = dict(ms=ms, tokens_per_s=bwd["tokens"] / ms * 1e3,
                                tflops=bwd["flops"] / ms / 1e9)
-        out["attn_bwd"]["dense_bwd_ms"] = dense_attention_bwd_baseline(att, bwd, K, stream)
+        if not args.no_dense:
+            out["attn_bwd"]["dense_bwd_ms"] = dense_attention_bwd_baseline(att, bwd, K, stream)
     if args.mode in ("all", "attn_ex"):
         if args.mode == "attn_ex":
             att = setup_attn(dev)

@@ -245,8 +245,9 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
  * Replaces the autograd backward of the masked SDPA call in
  * WindowedAttention.forward (attn/windowed_attention.py:318-323) and of
  * BlockSparseAttention's per-block matmul/softmax loop
- * (attn/block_sparse_attention.py:277-334). Three launches on `stream`
- * (row sums, then dK/dV, then dQ), no atomics: results are deterministic.
+ * (attn/block_sparse_attention.py:277-334). Launches on `stream`, no atomics:
+ * results are deterministic (16-bit: dQ, which also writes the row sums, then
+ * dK/dV; fp32: row sums, dK/dV, dQ).
  * Q, K, V, O, dO, dQ, dK, dV: [B, H, S, dh] addressed by strides as in
  * tmac_wattn_fwd; dQ, dK, dV must not overlap each other or the inputs.
  * lse: fp32 [B, H, S] from tmac_wattn_fwd of the same Q, K, V and mask.

@@ -455,42 +455,12 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 // Backward (16-bit MFMA path). With P = softmax(S) recomputed from the
 // forward's log-sum-exp, Δ = rowsum(dO ⊙ O):
 //   dV = Pᵀ·dO,  dS = P ⊙ (dO·Vᵀ − Δ),  dK = scale·dSᵀ·Q,  dQ = scale·dS·K.
-// Two kernels, no atomics (results are deterministic): wattn_bwd_kv_kernel
-// owns 128 keys and walks the query tiles that touch them (key-major work
-// list, tmac_wattn_schedule_kv); wattn_bwd_q_kernel owns 128 queries and walks
-// the forward's work list. Both recompute S and dP with MFMAs.
+// Two kernels, no atomics (results are deterministic): wattn_bwd_q_kernel owns
+// 128 queries, walks the forward's work list and also writes Δ of its rows;
+// then wattn_bwd_kv_kernel owns 128 keys and walks the query tiles that touch
+// them (key-major work list, tmac_wattn_schedule_kv). Both recompute S and dP
+// with MFMAs.
 // ---------------------------------------------------------------------------
-
-// Δ[b, h, q] = Σ_d dO[b, h, q, d] · O[b, h, q, d] in fp32: D/8 lanes per row,
-// 2048/D rows per workgroup.
-template <int DT, int D>
-__global__ __launch_bounds__(256) void wattn_bwd_delta_kernel(
-    const uint16_t* __restrict__ O, const uint16_t* __restrict__ dO, float* __restrict__ delta,
-    int64_t osb, int64_t osh, int64_t oss, int64_t gsb, int64_t gsh, int64_t gss, int H, int S,
-    int64_t n_rows) {
-  constexpr int kLpr = D / 8;  // lanes per row
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / kLpr) + threadIdx.x / kLpr;
-  const int ch = threadIdx.x % kLpr;
-  float acc = 0.f;
-  if (row < n_rows) {
-    const int64_t bh = row / S;
-    const int q = static_cast<int>(row - bh * S);
-    const int b = static_cast<int>(bh / H), hd = static_cast<int>(bh - static_cast<int64_t>(b) * H);
-    const u32x4 o = ldg16(O + b * osb + hd * osh + static_cast<int64_t>(q) * oss + 8 * ch);
-    const u32x4 g = ldg16(dO + b * gsb + hd * gsh + static_cast<int64_t>(q) * gss + 8 * ch);
-    const uint32_t ow[4] = {o.x, o.y, o.z, o.w}, gw[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] & 0xffff)),
-                 Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] & 0xffff)), acc);
-      acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] >> 16)),
-                 Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] >> 16)), acc);
-    }
-  }
-#pragma unroll
-  for (int o = 1; o < kLpr; o <<= 1) acc += __shfl_xor(acc, o);
-  if (row < n_rows && ch == 0) delta[row] = acc;
-}
 
 // Packs accumulator values v[j0 + 2t], v[j0 + 2t + 1] (t = 0..3) into one
 // 16-bit MFMA operand (eight values, in the permuted key/query order of the
@@ -747,7 +717,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
 template <int DT, int D, int FEAT = 0>
 __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
-    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O, int64_t osb, int64_t osh,
+    int64_t oss, const float* __restrict__ lse, float* __restrict__ delta,
     uint16_t* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
     int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
@@ -781,7 +752,29 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     }
   }
   const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + min(q_row, S - 1)]);
-  const float dl = delta[static_cast<int64_t>(bh) * S + min(q_row, S - 1)];
+  // Δ = rowsum(dO ⊙ O) of this row in fp32: this lane's half of the head dims
+  // (the dO chunks it holds), then lane ^ 32's half. Written for the dK/dV
+  // kernel, which runs after this one.
+  float dl;
+  {
+    const uint16_t* op = O + b * osb + hd * osh + static_cast<int64_t>(min(q_row, S - 1)) * oss + 8 * h;
+    float acc = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) {
+      const u32x4 o = ldg16(op + 16 * kk);
+      const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+      const uint32_t gw[4] = {gf[kk].x, gf[kk].y, gf[kk].z, gf[kk].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] & 0xffff)),
+                   Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] & 0xffff)), acc);
+        acc = fmaf(Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] >> 16)),
+                   Mfma<DT>::to_f32(static_cast<uint16_t>(gw[i] >> 16)), acc);
+      }
+    }
+    dl = xor32_add(acc);
+    if (h == 0 && q_row < S) delta[static_cast<int64_t>(bh) * S + q_row] = dl;
+  }
   const uint16_t* Kbh = K + b * ksb + hd * ksh;
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
   int e0, e1, mrow = 0;
@@ -856,50 +849,39 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     if (kind != 0) {
       const uint16_t* k_lds = smem + (2 * buf) * T::kElems;
       const uint16_t* v_lds = smem + (2 * buf + 1) * T::kElems;
-      f32x16 s[2], dp[2];
+      // One 32-key half at a time (s, dp: 32 VGPRs instead of 64).
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
-        s[kh] = f32x16{};
-        dp[kh] = f32x16{};
+        f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int kk = 0; kk < T::kKk; ++kk) {
           const u32x4 ka = lds16(k_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
           const u32x4 va = lds16(v_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
-          s[kh] = Mfma<DT>::run(ka, qf[kk], s[kh]);
-          dp[kh] = Mfma<DT>::run(va, gf[kk], dp[kh]);
+          s = Mfma<DT>::run(ka, qf[kk], s);
+          dp = Mfma<DT>::run(va, gf[kk], dp);
         }
-      }
-      // s[kh][j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4; the
-      // span bounds move to this lane's origin (kt*64 + 4h).
-      if constexpr (CM) {
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) s[kh] *= scale_log2;
-        if (kind == 2) {
-          const uint64_t w = wb >> (4 * h);
-          apply_bits(s[0], static_cast<uint32_t>(w));
-          apply_bits(s[1], static_cast<uint32_t>(w >> 32));
-        } else if (kind == 3) {
-#pragma unroll
-          for (int kh = 0; kh < 2; ++kh)
+        // s[j] = S[q_row][key], key = kt*64 + 32kh + 8(j/4) + 4h + j%4; the span
+        // bounds move to this lane's origin (kt*64 + 4h).
+        if constexpr (CM) {
+          s *= scale_log2;
+          if (kind == 2) {
+            apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * kh)));
+          } else if (kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
-              s[kh][j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
+              s[j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
             }
-        }
-      } else if (kind == 2) {
-        const int base = kt * 64 + 4 * h;
-        const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
+          }
+        } else if (kind == 2) {
+          const int base = kt * 64 + 4 * h;
+          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
 #pragma unroll
           for (int j = 0; j < 16; ++j) {
             const int off = 32 * kh + 8 * (j >> 2) + (j & 3);
-            s[kh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[kh][j] : -INFINITY;
+            s[j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[j] : -INFINITY;
           }
-      }
-#pragma unroll
-      for (int kh = 0; kh < 2; ++kh)
+        }
 #pragma unroll
         for (int jg = 0; jg < 4; ++jg) {
           float z[4] = {1.f, 1.f, 1.f, 1.f};
@@ -907,19 +889,21 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int j = 4 * jg + t;
-            const float pj = __builtin_amdgcn_exp2f(fmaf(s[kh][j], sc, -l2));
-            dp[kh][j] = DR ? pj * (z[t] * dp[kh][j] - dl) : pj * (dp[kh][j] - dl);
+            const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -l2));
+            dp[j] = DR ? pj * (z[t] * dp[j] - dl) : pj * (dp[j] - dl);
           }
         }
-      // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
+        // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 db = pack8<DT>(dp[ks >> 1], 8 * (ks & 1));
+        for (int k2 = 0; k2 < 2; ++k2) {
+          const int ks = 2 * kh + k2;
+          const u32x4 db = pack8<DT>(dp, 8 * k2);
 #pragma unroll
-        for (int dt = 0; dt < T::kDt; ++dt) {
-          const u32x4 ka = lds_read_tr4x2<T::kP>(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
-                                                 32 * dt + 16 * grp, lane);
-          dqt[dt] = Mfma<DT>::run(ka, db, dqt[dt]);
+          for (int dt = 0; dt < T::kDt; ++dt) {
+            const u32x4 ka = lds_read_tr4x2<T::kP>(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
+                                                   32 * dt + 16 * grp, lane);
+            dqt[dt] = Mfma<DT>::run(ka, db, dqt[dt]);
+          }
         }
       }
     }
@@ -1474,7 +1458,7 @@ void launch_fwd(const AttnLaunch& a) {
   }
 }
 
-// Backward, 16-bit MFMA kernels: row sums, then dK/dV, then dQ.
+// Backward, 16-bit MFMA kernels: dQ (which also writes the row sums Δ), then dK/dV.
 template <int DT, int D, int FEAT>
 void launch_bwd_mfma(const AttnLaunch& a) {
   const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os, *gs = a.gs, *dqs = a.dqs,
@@ -1484,21 +1468,17 @@ void launch_bwd_mfma(const AttnLaunch& a) {
   const auto* V = static_cast<const uint16_t*>(a.V);
   const auto* O = static_cast<const uint16_t*>(a.O);
   const auto* G = static_cast<const uint16_t*>(a.dO);
-  const int64_t n_rows = static_cast<int64_t>(a.B) * a.H * a.S;
-  const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);  // 2048/D rows each
-  hipLaunchKernelGGL((wattn_bwd_delta_kernel<DT, D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
-                     a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
+  hipLaunchKernelGGL((wattn_bwd_q_kernel<DT, D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V,
+                     G, O, os[0], os[1], os[2], a.lse, a.delta, static_cast<uint16_t*>(a.dQ),
+                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
+                     gs[2], dqs[0], dqs[1], dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr,
+                     a.entries, a.order, a.wm_q, a.ax_q);
   hipLaunchKernelGGL((wattn_bwd_kv_kernel<DT, D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
                      V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
                      static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
                      vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0],
                      dvs[1], dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
                      a.order_kv, a.wm_kv, a.ax_kv);
-  hipLaunchKernelGGL((wattn_bwd_q_kernel<DT, D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V,
-                     G, a.lse, a.delta, static_cast<uint16_t*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
-                     ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
-                     dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
-                     a.wm_q, a.ax_q);
 }
 
 // Backward, fp32 FMA kernels.
