@@ -50,17 +50,23 @@ def threshold(p: float) -> int:
 
 
 def keep_mask(bh: int, rows: np.ndarray, cols: np.ndarray, seed: int, p: float) -> np.ndarray:
-    """bool [len(rows), len(cols)]: whether pair (bh, q, k) survives dropout p."""
+    """bool [len(rows), len(cols)]: whether pair (bh, q, k) survives dropout p.
+
+    One Philox call per (row, key group k // 4) that the columns touch; key k takes
+    word k % 4 of its group's draw."""
     rows = np.asarray(rows, dtype=np.int64)
     cols = np.asarray(cols, dtype=np.int64)
-    ctr = np.zeros((rows.size, cols.size, 4), dtype=np.uint32)
-    ctr[..., 0] = (cols // 4)[None, :]
+    t = threshold(p)
+    if t >= 2**32:
+        return np.zeros((rows.size, cols.size), bool)
+    groups, inv = np.unique(cols // 4, return_inverse=True)
+    ctr = np.zeros((rows.size, groups.size, 4), dtype=np.uint32)
+    ctr[..., 0] = groups[None, :]
     ctr[..., 1] = rows[:, None]
     ctr[..., 2] = bh
-    out = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))
-    word = np.take_along_axis(out, np.broadcast_to((cols % 4)[None, :, None],
-                                                   (rows.size, cols.size, 1)), axis=-1)[..., 0]
-    return word >= np.uint32(threshold(p)) if threshold(p) < 2**32 else np.zeros(word.shape, bool)
+    out = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))  # [rows, groups, 4]
+    words = out[:, inv, cols % 4]  # [rows, cols]
+    return words >= np.uint32(t)
 
 
 def drop_factors(B: int, H: int, S: int, seed: int, p: float, rows=None) -> np.ndarray:

@@ -295,3 +295,50 @@ def test_block_sparse_module_dropout_trains(dev):
     x = torch.randn(2, 300, 256, device=dev, dtype=torch.bfloat16, requires_grad=True)
     m(x).float().square().mean().backward()
     assert torch.isfinite(x.grad).all()
+
+
+def test_config3_size_caller_mask_and_dropout_sampled(dev):
+    """Config 3's shape (B=8, H=10, S=4096, dh 64, bf16) with a caller's bool [S, S] mask and
+    dropout 0.1: the band + persistent mask with 10% of its pairs removed, 0.3% random pairs
+    added everywhere (so nearly every tile is partial) and one fully masked row. Forward and
+    dQ on sampled rows of all 80 (b, h) pairs (boundary rows included), dK/dV on sampled keys
+    of three pairs (from every query row that attends to them), against the oracle with the
+    same Philox decisions; the 16-bit bar, Δ from the stored output."""
+    import sampled
+    B, H, S, dh, p, seed = 8, 10, 4096, 64, 0.1, 20261202
+    rng = np.random.default_rng(3)
+    mask = om.band_mask(S, 512, 16)
+    mask &= rng.random((S, S)) >= 0.1
+    mask |= rng.random((S, S)) < 0.003
+    mask[100, :] = False
+    q, k, v, do = tensors((B, H, S, dh), torch.bfloat16, seed=33)
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = windowed_attention(qd, kd, vd, 0, 0, attn_mask=torch.from_numpy(mask).to(dev),
+                           dropout_p=p, seed=seed)
+    o.backward(do.to(dev))
+    torch.cuda.synchronize()
+    o_np = o.detach().float().cpu().numpy()
+    dq, dk, dv = (t.grad.float().cpu().numpy() for t in (qd, kd, vd))
+    assert np.all(o_np[:, :, 100] == 0) and np.all(dq[:, :, 100] == 0)
+    qn, kn, vn, gn = (t.float().numpy() for t in (q, k, v, do))
+    bias = np.where(mask, 0.0, -np.inf)
+    cols = np.arange(S)
+    for bh in range(B * H):
+        b, h = divmod(bh, H)
+        rows = sampled.sample_rows(S, 16, 512, rng, n_random=4)
+        rows = np.unique(np.concatenate([rows, [100]]))
+        z = od.keep_mask(bh, rows, cols, seed, p) / (1.0 - float(np.float32(p)))
+        want = oa.biased_attention(qn[b, h, rows], kn[b, h], vn[b, h], bias[rows], 0.125, z)
+        close(o_np[b, h, rows], want, what=f"out (b,h)={b, h}")
+        gq, _, _ = oa.biased_attention_grads(qn[b, h, rows], kn[b, h], vn[b, h], gn[b, h, rows],
+                                             bias[rows], 0.125, z, out=o_np[b, h, rows])
+        close(dq[b, h, rows], gq, what=f"dq (b,h)={b, h}")
+    for bh in (0, 37, 79):
+        b, h = divmod(bh, H)
+        keys = np.array(sorted({0, 15, 16, 17, 511, 512, 2047, 4095} | set(rng.choice(S, 4).tolist())))
+        qrows = np.nonzero(mask[:, keys].any(axis=1))[0]
+        z = od.keep_mask(bh, qrows, cols, seed, p) / (1.0 - float(np.float32(p)))
+        _, gk, gv = oa.biased_attention_grads(qn[b, h, qrows], kn[b, h], vn[b, h], gn[b, h, qrows],
+                                              bias[qrows], 0.125, z, out=o_np[b, h, qrows])
+        close(dk[b, h, keys], gk[keys], what=f"dk (b,h)={b, h}")
+        close(dv[b, h, keys], gv[keys], what=f"dv (b,h)={b, h}")
