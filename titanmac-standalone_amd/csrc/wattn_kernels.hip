@@ -53,6 +53,13 @@ __device__ __forceinline__ void apply_bits(f32x16& v, uint32_t w) {
   for (int j = 0; j < 16; ++j) v[j] = ((w >> (8 * (j >> 2) + (j & 3))) & 1u) ? v[j] : -INFINITY;
 }
 
+// Register operands loaded once before a tile loop (this lane's Q, K or V rows)
+// are handed through an empty asm statement, so the compiler waits for their
+// loads there, once. Otherwise the loop's entry state (these loads pending) and
+// back edge (the next tile's prefetch pending) merge, and it waits for the
+// prefetch before the first MFMA of every tile.
+__device__ __forceinline__ void settle(u32x4& v) { asm volatile("" : "+v"(v)); }
+
 template <bool CM>
 __device__ __forceinline__ float lse_log2(float lse) {
   const float l2 = lse * kLog2e;
@@ -120,6 +127,8 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
     const uint16_t* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < T::kKk; ++kk) qf[kk] = ldg16(qp + 16 * kk);
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) settle(qf[kk]);
   }
 
   int e0, e1, mrow = 0;
@@ -538,6 +547,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
       kf[kk] = ldg16(kp + 16 * kk);
       vf[kk] = ldg16(vp + 16 * kk);
     }
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) {
+      settle(kf[kk]);
+      settle(vf[kk]);
+    }
   }
   const uint16_t* Qbh = Q + b * qsb + hd * qsh;
   const uint16_t* Gbh = dO + b * gsb + hd * gsh;
@@ -582,10 +596,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
         pre[T::kPasses + p] = ldg16(Gbh + qr * gss + c8);
       }
     }
-    if (tid < 128) {
-      const int qr = min(qt * 64 + (tid & 63), S - 1);
-      st_pre = tid < 64 ? lse_log2<CM>(lse_bh[qr]) : dl_bh[qr];
-    }
+    // LSE (threads 0-63) and Δ (64-127) of the tile's queries, loaded raw by every
+    // thread (threads 128-255 repeat them): an unconditional load that nothing
+    // consumes until sstore, so no wait lands here.
+    st_pre = ((tid & 64) ? dl_bh : lse_bh)[min(qt * 64 + (tid & 63), S - 1)];
   };
   auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
@@ -594,7 +608,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
       sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
       sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
     }
-    if (tid < 128) stat[buf][tid >> 6][tid & 63] = st_pre;
+    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<CM>(st_pre) : st_pre;
   };
 
   f32x16 dkt[T::kDt], dvt[T::kDt];
@@ -749,6 +763,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
     for (int kk = 0; kk < T::kKk; ++kk) {
       qf[kk] = ldg16(qp + 16 * kk);
       gf[kk] = ldg16(gp + 16 * kk);
+    }
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) {
+      settle(qf[kk]);
+      settle(gf[kk]);
     }
   }
   const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + min(q_row, S - 1)]);
