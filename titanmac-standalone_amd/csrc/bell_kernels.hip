@@ -257,6 +257,15 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   // staging tile and store 128-byte row segments.
   uint16_t* stage = smem0 + wave * kTileElems;
   const int64_t col0 = static_cast<int64_t>(ob) * 64;
+  // the bias values of this lane's 32 columns, all eight loads in flight at once
+  u32x2 bb[2][4] = {};
+  if (bias) {
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg)
+        bb[ni][jg] = *reinterpret_cast<const u32x2*>(bias + col0 + 32 * ni + 8 * jg + 4 * h);
+  }
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -268,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] = acc[mi][ni][4 * jg + t];
         if (bias) {
-          const u32x2 b2 = *reinterpret_cast<const u32x2*>(bias + col0 + n_loc);
+          const u32x2 b2 = bb[ni][jg];
           v[0] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x & 0xffff));
           v[1] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x >> 16));
           v[2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
@@ -406,6 +415,15 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
   // stage-1 memory, which no wave touches any more).
   uint16_t* stage = &st1[0][0];
   const int64_t col0 = static_cast<int64_t>(ob) * 64;
+  // the bias values of this lane's 32 columns, all eight loads in flight at once
+  u32x2 bb[2][4] = {};
+  if (bias) {
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+      for (int jg = 0; jg < 4; ++jg)
+        bb[ni][jg] = *reinterpret_cast<const u32x2*>(bias + col0 + 32 * ni + 8 * jg + 4 * h);
+  }
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -417,7 +435,7 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
 #pragma unroll
         for (int t = 0; t < 4; ++t) v[t] = acc[mi][ni][4 * jg + t];
         if (bias) {
-          const u32x2 b2 = *reinterpret_cast<const u32x2*>(bias + col0 + n_loc);
+          const u32x2 b2 = bb[ni][jg];
           v[0] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x & 0xffff));
           v[1] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x >> 16));
           v[2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
