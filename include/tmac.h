@@ -144,7 +144,8 @@ int tmac_bell_sddmm_workspace(int M, int n_brow, int n_bcol, int width,
  * restricted to the Block-ELL pattern. The M reduction is split across
  * workgroups and summed in a fixed order, so results are deterministic.
  * dvals_dtype: TMAC_F32, TMAC_BF16 or TMAC_F16 (inputs, dtype: TMAC_BF16,
- * TMAC_F16 or TMAC_F32). */
+ * TMAC_F16 or TMAC_F32). ws_bytes >= tmac_bell_sddmm_workspace(...) (else
+ * TMAC_ERR_WORKSPACE); 16-bit inputs need ldx, lddy <= 2^25 (else TMAC_ERR_SHAPE). */
 int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, int64_t lddy,
                     const int32_t* d_col_idx, void* d_dvals, int dvals_dtype,
                     void* d_ws, size_t ws_bytes,

@@ -33,11 +33,12 @@
 // workgroup per block-column whose four waves split the column's list.
 //
 // SDDMM: a workgroup owns one block-row r, four of its slots (one per wave)
-// and a contiguous range of M. Per 64-row step it stages X[m, 64r:+64] and the
-// four dY[m, 64c:+64] tiles in LDS and reads both MFMA operands with transpose
-// reads (the reduction runs over M, the rows). Partial sums per M-range go to a
-// workspace and a second kernel adds them in a fixed order, so the result is
-// deterministic.
+// and a contiguous range of M. Per 32-row step it needs X[m, 64r:+64] and the
+// four dY[m, 64c:+64] tiles (20 KB), copied HBM/L2 -> LDS with global_load_lds
+// into a four-stage ring three steps ahead of the math (one barrier per step),
+// and reads both MFMA operands with transpose reads (the reduction runs over M,
+// the rows). Partial sums per M-range go to a workspace and a second kernel
+// adds them in a fixed order, so the result is deterministic.
 
 #include "tmac_device.h"
 
@@ -457,13 +458,46 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
   }
 }
 
+// LDS address (byte offset in the workgroup's LDS) of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+// HBM/L2 -> LDS copy of 1 KB as in dma16, from base + voff (base wave-uniform,
+// in SGPRs; voff this lane's byte offset), written as assembly so the compiler
+// does not track it: the kernel waits for these copies itself with exact
+// vmcnt values, and the compiler's own waits (which would cover every copy in
+// flight) stay out of the loop.
+__device__ __forceinline__ void dma16_nowait(const void* base, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_byte), "v"(voff),
+               "s"(base)
+               : "memory", "m0");
+}
+
+// s_waitcnt vmcnt(n) for n in {0, 5, 10}; the other counters are left alone.
+__device__ __forceinline__ void wait_vm(int n) {
+  if (n >= 10)
+    asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+  else if (n >= 5)
+    asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+constexpr int kSdRows = 32;            // M rows per SDDMM step
+constexpr int kSdStages = 4;           // LDS ring depth (three steps of copies in flight)
+constexpr int kSdTile = kSdRows * 64;  // one 32x64 tile, 16-bit elements
+constexpr int kSdStage = 5 * kSdTile;  // X tile + four dY tiles (20 KB)
+
 template <int DT>
 __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
     const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ dY, int64_t lddy,
     const int32_t* __restrict__ col_idx, float* __restrict__ part, int M, int n_brow, int width,
     int n_sgroups, int rows_per_split, int n_splits, int per_xcd) {
-  // Tile 0: X[m0:m0+64, 64r:64r+64]; tiles 1..4: dY[m0:m0+64, 64c_w:64c_w+64].
-  __shared__ __attribute__((aligned(16))) uint16_t smem[5 * kTileElems];
+  // Ring of four stages; stage = X[m:m+32, 64r:+64] then dY[m:m+32, 64c_w:+64]
+  // for w = 0..3, each tile 32 rows of 64 elements, chunks swizzled as wswz.
+  __shared__ __attribute__((aligned(16))) uint16_t ring[kSdStages * kSdStage];
 
   const int per_split = n_brow * n_sgroups;
   const int logical = xcd_logical_id(per_xcd);
@@ -474,48 +508,48 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
   const int sg = rem - r * n_sgroups;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int l32 = lane & 31, h = lane >> 5;
-  const int grp = (lane >> 4) & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int h = lane >> 5, grp = (lane >> 4) & 1, l32 = lane & 31;
   const int s = sg * 4 + wave;
   const bool active = s < width;
-
-  // Block-columns of the four staged dY tiles; slots past the row's width
-  // repeat the last valid one (loaded, never used).
-  int cblk[4];
-#pragma unroll
-  for (int w = 0; w < 4; ++w) cblk[w] = col_idx[r * width + min(sg * 4 + w, width - 1)];
+  // this wave's block-column; a slot past the row's width repeats the last one
+  // (copied, never used)
+  const int cw = col_idx[r * width + min(s, width - 1)];
 
   const int m_begin = split * rows_per_split;
   const int m_end = min(M, m_begin + rows_per_split);
+  const int n_steps = (m_end - m_begin + kSdRows - 1) / kSdRows;
 
-  // 5 tiles x 64 rows x 8 chunks of 16 bytes = 10 chunks per thread; chunk
-  // p of this thread belongs to tile p/2, row (tid/8) + 32*(p%2), column chunk tid%8.
-  u32x4 pre[10];
-  auto gload = [&](int m0) {
-#pragma unroll
-    for (int p = 0; p < 10; ++p) {
-      const int t = p >> 1;
-      const int row = (tid >> 3) + 32 * (p & 1);
-      const int ch = tid & 7;
-      const int m = m0 + row;
-      if (m < m_end) {
-        const uint16_t* src = (t == 0)
-                                  ? X + static_cast<int64_t>(m) * ldx + 64 * r + ch * 8
-                                  : dY + static_cast<int64_t>(m) * lddy + 64 * cblk[t - 1] + ch * 8;
-        pre[p] = ldg16(src);
-      } else {
-        pre[p] = u32x4{0u, 0u, 0u, 0u};  // rows past the range contribute zero
-      }
-    }
+  // Copies per step and wave: its own dY tile (four 8-row instructions) and
+  // rows 8w..8w+7 of the X tile. Lane L of an instruction covering rows
+  // R..R+7 fills chunk position L & 7 of row R + L / 8 and fetches the global
+  // chunk the swizzle stores there; the eight lanes of a row read 128
+  // contiguous bytes. A lane's byte offsets from the step's first row are the
+  // same for every step; rows past M (last step of the matrix only) read row
+  // M-1, valid memory, and are zeroed in LDS once the copies have landed.
+  const int drow = lane >> 3, dpos = lane & 7;
+  auto swz_chunk = [](int row, int pos) {
+    const int a = (row >> 1) & 7;
+    return pos ^ (((a & 1) << 2) | (a >> 1));
   };
-  auto sstore = [&]() {
+  const int xrow = 8 * wave + drow;
+  const uint32_t xcol = 2u * (64 * r + 8 * swz_chunk(xrow, dpos));
+  uint32_t ycol[4];
 #pragma unroll
-    for (int p = 0; p < 10; ++p) {
-      const int t = p >> 1;
-      const int row = (tid >> 3) + 32 * (p & 1);
-      sts16(smem + t * kTileElems + row * kPitch + (tid & 7) * 8, pre[p]);
-    }
+  for (int j = 0; j < 4; ++j) ycol[j] = 2u * (64 * cw + 8 * swz_chunk(8 * j + drow, dpos));
+  const uint32_t ring0 = lds_offset(ring);
+  auto issue = [&](int step) {
+    const int m0 = m_begin + step * kSdRows;
+    const uint32_t st = ring0 + static_cast<uint32_t>((step % kSdStages) * kSdStage * 2);
+    const uint16_t* xb = X + static_cast<int64_t>(m0) * ldx;
+    const uint16_t* yb = dY + static_cast<int64_t>(m0) * lddy;
+    const int lim = M - 1 - m0;  // rows beyond this one read it instead
+    dma16_nowait(xb, static_cast<uint32_t>(min(xrow, lim)) * static_cast<uint32_t>(2 * ldx) + xcol,
+                 st + 8 * wave * 128);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      dma16_nowait(yb, static_cast<uint32_t>(min(8 * j + drow, lim)) * static_cast<uint32_t>(2 * lddy) + ycol[j],
+                   st + (1 + wave) * kSdTile * 2 + 8 * j * 128);
   };
 
   f32x16 acc[2][2];
@@ -524,33 +558,42 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[ki][ni] = f32x16{};
 
-  const uint16_t* xt = smem;
-  const uint16_t* dyt = smem + (1 + wave) * kTileElems;
-
-  gload(m_begin);
-  sstore();
-  __syncthreads();
-  for (int m0 = m_begin; m0 < m_end; m0 += 64) {
-    const bool more = m0 + 64 < m_end;
-    if (more) gload(m0 + 64);
-    if (active) {
+  for (int i = 0; i < kSdStages - 1 && i < n_steps; ++i) issue(i);
+  for (int i = 0; i < n_steps; ++i) {
+    // this wave's copies of step i have landed when at most those of the
+    // (up to two) later steps already issued are outstanding
+    wait_vm(5 * min(2, n_steps - 1 - i));
+    const int m0 = m_begin + i * kSdRows;
+    uint16_t* st = ring + (i % kSdStages) * kSdStage;
+    if (m0 + kSdRows > m_end) {
+      // rows past the range contribute zero: each wave clears the rows it copied
+      const int valid = m_end - m0;
+      if (xrow >= valid) sts16(st + xrow * 64 + 8 * dpos, u32x4{0u, 0u, 0u, 0u});
 #pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
+      for (int j = 0; j < 4; ++j)
+        if (8 * j + drow >= valid)
+          sts16(st + (1 + wave) * kSdTile + (8 * j + drow) * 64 + 8 * dpos, u32x4{0u, 0u, 0u, 0u});
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    // every wave's copies of step i are in LDS, and every wave is done reading
+    // the stage the next copies overwrite (step i-1's)
+    asm volatile("s_barrier" ::: "memory");
+    if (i + kSdStages - 1 < n_steps) issue(i + kSdStages - 1);
+    if (active) {
+      const uint16_t* xt = st;
+      const uint16_t* dyt = st + (1 + wave) * kSdTile;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
         u32x4 af[2], bf[2];
 #pragma unroll
-        for (int ki = 0; ki < 2; ++ki) af[ki] = lds_read_tr8(xt, 16 * ms + 8 * h, 32 * ki + 16 * grp, lane);
+        for (int ki = 0; ki < 2; ++ki) af[ki] = lds_read_tr8_wswz(xt, 16 * ks + 8 * h, 32 * ki + 16 * grp, lane);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) bf[ni] = lds_read_tr8(dyt, 16 * ms + 8 * h, 32 * ni + 16 * grp, lane);
+        for (int ni = 0; ni < 2; ++ni) bf[ni] = lds_read_tr8_wswz(dyt, 16 * ks + 8 * h, 32 * ni + 16 * grp, lane);
 #pragma unroll
         for (int ki = 0; ki < 2; ++ki)
 #pragma unroll
           for (int ni = 0; ni < 2; ++ni) acc[ki][ni] = Mfma<DT>::run(af[ki], bf[ni], acc[ki][ni]);
       }
-    }
-    __syncthreads();
-    if (more) {
-      sstore();
-      __syncthreads();
     }
   }
 
@@ -820,18 +863,29 @@ int launch_status() {
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }
 
-// Split of the SDDMM reduction over M: enough workgroups to cover the chip
-// about twice, rows per split a multiple of 64.
-void sddmm_split(int M, int n_brow, int width, int* n_splits, int* rows_per_split) {
+// Split of the SDDMM reduction over M, rows per split a multiple of 64. The
+// 16-bit kernel (two workgroups per CU) takes as many splits as fit the 512
+// slots of one wave of workgroups, so no workgroup waits for a second round;
+// the fp32 kernel (four per CU) about 512 workgroups or a few more.
+void sddmm_split(int M, int n_brow, int width, bool f32, int* n_splits, int* rows_per_split) {
   const int n_sg = (width + 3) / 4;
   const int base = n_brow * n_sg;
   const int m_steps = (M + 63) / 64;
-  int want = (512 + base - 1) / base;
+  int want = f32 ? (512 + base - 1) / base : 512 / base;
   if (want < 1) want = 1;
   if (want > m_steps) want = m_steps;
   const int steps_per = (m_steps + want - 1) / want;
   *rows_per_split = steps_per * 64;
   *n_splits = (M + *rows_per_split - 1) / *rows_per_split;
+}
+
+// Workspace of tmac_bell_sddmm: the partial sums of the larger of the two
+// kernels' splits (one size for every dtype).
+size_t sddmm_ws_bytes(int M, int n_brow, int width) {
+  int n32, n16, rows_per_split;
+  sddmm_split(M, n_brow, width, true, &n32, &rows_per_split);
+  sddmm_split(M, n_brow, width, false, &n16, &rows_per_split);
+  return static_cast<size_t>(n32 > n16 ? n32 : n16) * n_brow * width * 4096 * sizeof(float);
 }
 
 }  // namespace
@@ -940,9 +994,7 @@ extern "C" int tmac_bell_sddmm_workspace(int M, int n_brow, int n_bcol, int widt
   if (!ws_bytes) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
-  int n_splits, rows_per_split;
-  sddmm_split(M, n_brow, width, &n_splits, &rows_per_split);
-  *ws_bytes = static_cast<size_t>(n_splits) * n_brow * width * 4096 * sizeof(float);
+  *ws_bytes = sddmm_ws_bytes(M, n_brow, width);
   return TMAC_OK;
 }
 
@@ -962,10 +1014,11 @@ extern "C" int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, i
   if (!aligned16(d_X) || !aligned16(d_dY) || !aligned16(d_dvals) || (ldx % vec) || (lddy % vec))
     return TMAC_ERR_ALIGN;
   int n_splits, rows_per_split;
-  sddmm_split(M, n_brow, width, &n_splits, &rows_per_split);
-  const size_t need = static_cast<size_t>(n_splits) * n_brow * width * 4096 * sizeof(float);
-  if (!d_ws || ws_bytes < need) return TMAC_ERR_WORKSPACE;
+  sddmm_split(M, n_brow, width, dtype == TMAC_F32, &n_splits, &rows_per_split);
+  if (!d_ws || ws_bytes < sddmm_ws_bytes(M, n_brow, width)) return TMAC_ERR_WORKSPACE;
   if (!aligned16(d_ws)) return TMAC_ERR_ALIGN;
+  // the 16-bit kernel addresses 32 rows of X and dY with 32-bit byte offsets
+  if (dtype != TMAC_F32 && (ldx > (1ll << 25) || lddy > (1ll << 25))) return TMAC_ERR_SHAPE;
   const int n_sg = (width + 3) / 4;
   const int64_t total = static_cast<int64_t>(n_splits) * n_brow * n_sg;
   const int per_xcd = static_cast<int>((total + 7) / 8);
