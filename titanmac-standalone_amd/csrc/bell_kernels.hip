@@ -53,31 +53,18 @@ constexpr int kBM = 256;        // output rows per gather-GEMM workgroup (4 wave
 //   activation tile (kBM rows): chunk c of row r at c ^ ((r >> 1) & 7), so a
 //     16-lane phase of the operand reads (16 consecutive rows, one chunk each)
 //     covers all 64 banks once;
-//   weight block (64 rows): chunk c of row r at c ^ w(r >> 1), w(a) =
-//     ((a & 1) << 2) | ((a >> 1) & 3): conflict-free both for the forward's
-//     transpose reads (4 consecutive rows x 64 bytes per 32-lane phase) and for
-//     dX's 16-byte row reads (16 consecutive rows per phase).
+//   weight block (64 rows): swz64 (tmac_device.h), conflict-free both for the
+//     forward's transpose reads and for dX's 16-byte row reads.
 // Every 16-lane phase of the tile stores writes 256 contiguous bytes.
 __device__ __forceinline__ int xswz(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 1) & 7)) << 3);
 }
-__device__ __forceinline__ int wswz(int row, int chunk) {
-  const int a = (row >> 1) & 7;
-  return row * 64 + ((chunk ^ (((a & 1) << 2) | (a >> 1))) << 3);
-}
 
 // Transpose read of rows r0..r0+7 (r0 a multiple of 8) x 16 columns of a
-// wswz tile: lane (lane % 16) of each 16-lane group receives column
+// swz64 tile: lane (lane % 16) of each 16-lane group receives column
 // c0 + lane % 16 of those rows, as one MFMA operand (see lds_read_tr8).
-__device__ __forceinline__ u32x4 lds_read_tr8_wswz(const uint16_t* tile, int r0, int c0, int lane) {
-  const int i = lane & 15;
-  const int col = c0 + 4 * (i & 3);
-  const int ra = r0 + (i >> 2), rb = ra + 4;
-  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + wswz(ra, col >> 3) + (col & 7)));
-  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(tile + wswz(rb, col >> 3) + (col & 7)));
-  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
-  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
-  return u32x4{l2.x, l2.y, h2.x, h2.y};
+__device__ __forceinline__ u32x4 lds_read_tr8_swz64(const uint16_t* tile, int r0, int c0, int lane) {
+  return lds_read_tr4x2_swz64(tile, r0, r0 + 4, c0, lane);
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -96,7 +83,7 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
     const uint16_t* __restrict__ bias, int epi, uint16_t* __restrict__ Y, int64_t ldy, int M,
     int n_out, int width, int n_mtiles, int per_xcd) {
   // Two buffers, each the activation tile (kBM x 64, xswz) and the weight
-  // block (64 x 64, wswz); the epilogue's four per-wave 64x64 staging tiles
+  // block (64 x 64, swz64); the epilogue's four per-wave 64x64 staging tiles
   // (pitch kPitch) reuse the same memory.
   // The buffers are separate arrays so the compiler can tell that copies into
   // one do not alias reads of the other (and does not wait for them).
@@ -188,9 +175,9 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
       if constexpr (FWD)
-        wf[ni] = lds_read_tr8_wswz(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+        wf[ni] = lds_read_tr8_swz64(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
       else
-        wf[ni] = lds16(wt + wswz(32 * ni + l32, 2 * kk + h));
+        wf[ni] = lds16(wt + swz64(32 * ni + l32, 2 * kk + h));
     }
   };
   // The reads of k-step kk+1 are issued before the MFMAs of k-step kk, and
@@ -321,7 +308,7 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
     const int32_t* __restrict__ t_vblk, const uint16_t* __restrict__ bias, int epi,
     uint16_t* __restrict__ Y, int64_t ldy, int M) {
   // Per wave and stage: activation tile (64 x 64, xswz) then weight block
-  // (64 x 64, wswz). Separate arrays per stage, so the compiler can tell the
+  // (64 x 64, swz64). Separate arrays per stage, so the compiler can tell the
   // copies into one stage from the reads of the other.
   __shared__ __attribute__((aligned(16))) uint16_t st0[4][8192];
   __shared__ __attribute__((aligned(16))) uint16_t st1[4][8192];
@@ -366,7 +353,7 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) xa[mi] = lds16(buf + xswz(32 * mi + l32, 2 * kk + h));
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni) wf[ni] = lds_read_tr8_wswz(buf + 4096, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+      for (int ni = 0; ni < 2; ++ni) wf[ni] = lds_read_tr8_swz64(buf + 4096, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -458,23 +445,6 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
   }
 }
 
-// LDS address (byte offset in the workgroup's LDS) of a __shared__ pointer.
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
-}
-
-// HBM/L2 -> LDS copy of 1 KB as in dma16, from base + voff (base wave-uniform,
-// in SGPRs; voff this lane's byte offset), written as assembly so the compiler
-// does not track it: the kernel waits for these copies itself with exact
-// vmcnt values, and the compiler's own waits (which would cover every copy in
-// flight) stay out of the loop.
-__device__ __forceinline__ void dma16_nowait(const void* base, uint32_t voff, uint32_t lds_byte) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_byte), "v"(voff),
-               "s"(base)
-               : "memory", "m0");
-}
-
 // s_waitcnt vmcnt(n) for n in {0, 5, 10}; the other counters are left alone.
 __device__ __forceinline__ void wait_vm(int n) {
   if (n >= 10)
@@ -496,7 +466,7 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
     const int32_t* __restrict__ col_idx, float* __restrict__ part, int M, int n_brow, int width,
     int n_sgroups, int rows_per_split, int n_splits, int per_xcd) {
   // Ring of four stages; stage = X[m:m+32, 64r:+64] then dY[m:m+32, 64c_w:+64]
-  // for w = 0..3, each tile 32 rows of 64 elements, chunks swizzled as wswz.
+  // for w = 0..3, each tile 32 rows of 64 elements, chunks swizzled as swz64.
   __shared__ __attribute__((aligned(16))) uint16_t ring[kSdStages * kSdStage];
 
   const int per_split = n_brow * n_sgroups;
@@ -544,11 +514,11 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
     const uint16_t* xb = X + static_cast<int64_t>(m0) * ldx;
     const uint16_t* yb = dY + static_cast<int64_t>(m0) * lddy;
     const int lim = M - 1 - m0;  // rows beyond this one read it instead
-    dma16_nowait(xb, static_cast<uint32_t>(min(xrow, lim)) * static_cast<uint32_t>(2 * ldx) + xcol,
+    dma_lds16(xb, static_cast<uint32_t>(min(xrow, lim)) * static_cast<uint32_t>(2 * ldx) + xcol,
                  st + 8 * wave * 128);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      dma16_nowait(yb, static_cast<uint32_t>(min(8 * j + drow, lim)) * static_cast<uint32_t>(2 * lddy) + ycol[j],
+      dma_lds16(yb, static_cast<uint32_t>(min(8 * j + drow, lim)) * static_cast<uint32_t>(2 * lddy) + ycol[j],
                    st + (1 + wave) * kSdTile * 2 + 8 * j * 128);
   };
 
@@ -586,9 +556,9 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
       for (int ks = 0; ks < 2; ++ks) {
         u32x4 af[2], bf[2];
 #pragma unroll
-        for (int ki = 0; ki < 2; ++ki) af[ki] = lds_read_tr8_wswz(xt, 16 * ks + 8 * h, 32 * ki + 16 * grp, lane);
+        for (int ki = 0; ki < 2; ++ki) af[ki] = lds_read_tr8_swz64(xt, 16 * ks + 8 * h, 32 * ki + 16 * grp, lane);
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) bf[ni] = lds_read_tr8_wswz(dyt, 16 * ks + 8 * h, 32 * ni + 16 * grp, lane);
+        for (int ni = 0; ni < 2; ++ni) bf[ni] = lds_read_tr8_swz64(dyt, 16 * ks + 8 * h, 32 * ni + 16 * grp, lane);
 #pragma unroll
         for (int ki = 0; ki < 2; ++ki)
 #pragma unroll

@@ -136,6 +136,55 @@ __device__ __forceinline__ void sts16(uint16_t* p, u32x4 v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// Element offset of 16-byte chunk `chunk` of row `row` in an LDS tile of 64
+// 16-bit values (128 bytes) per row, chunks XOR-swizzled: chunk c of row r at
+// c ^ w((r >> 1) & 7), w(a) = ((a & 1) << 2) | (a >> 1). Conflict-free for the
+// 64 four-byte banks both for transpose reads (4 consecutive rows x 64 bytes
+// per 32-lane phase) and for 16-byte row reads (16 consecutive rows per phase).
+__device__ __forceinline__ int swz64(int row, int chunk) {
+  const int a = (row >> 1) & 7;
+  return row * 64 + ((chunk ^ (((a & 1) << 2) | (a >> 1))) << 3);
+}
+
+// lds_read_tr4x2 for a swz64 tile: rows r0..r0+3 and r1..r1+3 (multiples of
+// 4) at column c0 + lane%16 of the 16-lane group.
+__device__ __forceinline__ u32x4 lds_read_tr4x2_swz64(const uint16_t* tile, int r0, int r1, int c0,
+                                                      int lane) {
+  const int i = lane & 15;
+  const int col = c0 + 4 * (i & 3);
+  const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(tile + swz64(r0 + (i >> 2), col >> 3) + (col & 7)));
+  const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(tile + swz64(r1 + (i >> 2), col >> 3) + (col & 7)));
+  const u32x2 l2 = __builtin_bit_cast(u32x2, lo);
+  const u32x2 h2 = __builtin_bit_cast(u32x2, hi);
+  return u32x4{l2.x, l2.y, h2.x, h2.y};
+}
+
+// LDS address (byte offset in the workgroup's LDS) of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)(p)));
+}
+
+// HBM/L2 -> LDS copies with global_load_lds: lane L moves the bytes at
+// base + voff (base wave-uniform, in SGPRs; voff this lane's byte offset) to
+// LDS byte lds_byte + size * L (lds_byte wave-uniform). 16 bytes per lane
+// (1 KB per wave instruction) or 4 (256 bytes). Written as assembly so the
+// compiler does not track them: a kernel using these waits for them itself
+// with exact vmcnt values (loads complete in issue order), and the compiler's
+// own waits, which would cover every copy in flight, stay out of its loop.
+__device__ __forceinline__ void dma_lds16(const void* base, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds_byte), "v"(voff),
+               "s"(base)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* base, uint32_t voff, uint32_t lds_byte) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, %2" ::"s"(lds_byte), "v"(voff),
+               "s"(base)
+               : "memory", "m0");
+}
+
 // Workgroup id remapped so that consecutive logical ids run on the same XCD:
 // the hardware hands workgroup b to XCD b % 8, so logical = (b % 8) * per_xcd +
 // b / 8 keeps each XCD on one contiguous slice of the logical work order (and

@@ -500,6 +500,59 @@ __device__ __forceinline__ void store_row(uint16_t* rowp, const f32x16 (&acc)[ND
     }
 }
 
+// The vector-ALU and dV/dK part of one 32-query half of a listed tile, for
+// the wave's 32 keys (both dK/dV kernels). s and dp hold S (scaled to log2
+// units by sc) and dP of the half, element j for query q0 + 8(j/4) + j%4 with
+// q0 = qbase + 32qh + 4h; lse_l and dl_l hold LSE·log2e and Δ of the tile's 64
+// queries. Forms P and dS in place (with kFeatDrop, P ⊙ Z for dV and
+// P ⊙ (Z ⊙ dP − Δ)), then dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, dOᵀ and Qᵀ taken by
+// tr(tile, r0, r1, c0), a transpose read of rows r0..r0+3 and r1..r1+3 at
+// column c0 of the staged tile, in the accumulator's permuted query order.
+template <int DT, int D, bool DR, class TrRead>
+__device__ __forceinline__ void kv_half_update(f32x16& s, f32x16& dp, float sc, const float* lse_l,
+                                               const float* dl_l, int qh, int qbase, int h,
+                                               int grp, int lane, int key, int bh,
+                                               const AttnX& ax, const uint16_t* q_lds,
+                                               const uint16_t* g_lds, f32x16 (&dkt)[D / 32],
+                                               f32x16 (&dvt)[D / 32], TrRead tr) {
+  // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e and Δ as one 16-byte read each
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse_l + 32 * qh + 8 * g + 4 * h);
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl_l + 32 * qh + 8 * g + 4 * h);
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+    uint32_t kq = 0;
+    if constexpr (DR) kq = keep_quad(ax, bh, qbase + 32 * qh + 8 * g + 4 * h, key, lane & 3);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int j = 4 * g + t;
+      const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
+      if constexpr (DR) {
+        const float z = ((kq >> (4 * t)) & 1u) ? ax.keep_scale : 0.f;
+        s[j] = pj * z;
+        dp[j] = pj * (z * dp[j] - dv4[t]);
+      } else {
+        s[j] = pj;
+        dp[j] = pj * (dp[j] - dv4[t]);
+      }
+    }
+  }
+  // dVᵀ[d][key] += Σ_q dO[q][d] P[q][key]; dKᵀ[d][key] += Σ_q Q[q][d] dS[q][key].
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const u32x4 pb = pack8<DT>(s, 8 * ks);
+    const u32x4 db = pack8<DT>(dp, 8 * ks);
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) {
+      const int rr = 32 * qh + 16 * ks + 4 * h;
+      const u32x4 ga = tr(g_lds, rr, rr + 8, 32 * dt + 16 * grp);
+      const u32x4 qa = tr(q_lds, rr, rr + 8, 32 * dt + 16 * grp);
+      dvt[dt] = Mfma<DT>::run(ga, pb, dvt[dt]);
+      dkt[dt] = Mfma<DT>::run(qa, db, dkt[dt]);
+    }
+  }
+}
+
 // dK, dV. Workgroup = (b, h, 128 keys); wave w owns keys 32w..32w+31 of the
 // block, held in registers as the B operands of S = Q·Kᵀ and dP = dO·Vᵀ
 // (lane = key). Per listed 64-query tile, Q and dO (plus LSE and Δ of those
@@ -672,48 +725,202 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
             s[j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[j] : -INFINITY;
           }
         }
-        // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e and Δ as one 16-byte read each
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat[buf][0][32 * qh + 8 * g + 4 * h]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat[buf][1][32 * qh + 8 * g + 4 * h]);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-          uint32_t kq = 0;
-          if constexpr (DR) kq = keep_quad(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h, key, l32 & 3);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int j = 4 * g + t;
-            const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
-            if constexpr (DR) {
-              const float z = ((kq >> (4 * t)) & 1u) ? ax.keep_scale : 0.f;
-              s[j] = pj * z;
-              dp[j] = pj * (z * dp[j] - dv4[t]);
-            } else {
-              s[j] = pj;
-              dp[j] = pj * (dp[j] - dv4[t]);
-            }
-          }
-        }
-        // dVᵀ[d][key] += Σ_q dO[q][d] P[q][key]; dKᵀ[d][key] += Σ_q Q[q][d] dS[q][key].
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 pb = pack8<DT>(s, 8 * ks);
-          const u32x4 db = pack8<DT>(dp, 8 * ks);
-#pragma unroll
-          for (int dt = 0; dt < T::kDt; ++dt) {
-            const int rr = 32 * qh + 16 * ks + 4 * h;
-            const u32x4 ga = lds_read_tr4x2<T::kP>(g_lds, rr, rr + 8, 32 * dt + 16 * grp, lane);
-            const u32x4 qa = lds_read_tr4x2<T::kP>(q_lds, rr, rr + 8, 32 * dt + 16 * grp, lane);
-            dvt[dt] = Mfma<DT>::run(ga, pb, dvt[dt]);
-            dkt[dt] = Mfma<DT>::run(qa, db, dkt[dt]);
-          }
-        }
+        kv_half_update<DT, D, DR>(s, dp, sc, &stat[buf][0][0], &stat[buf][1][0], qh, qt * 64, h,
+                                  grp, lane, key, bh, ax, q_lds, g_lds, dkt, dvt,
+                                  [&](const uint16_t* t, int r0, int r1, int c0) {
+                                    return lds_read_tr4x2<T::kP>(t, r0, r1, c0, lane);
+                                  });
       }
     }
     if (more) sstore(buf ^ 1);
     if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
+  }
+
+  if (key >= S) return;
+  store_row<DT, T::kDt>(dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss, dkt, scale, h);
+  store_row<DT, T::kDt>(dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss, dvt, 1.f, h);
+}
+
+// dK, dV at head dimension 64 without a caller's mask (FEAT 0 or kFeatDrop):
+// the work of wattn_bwd_kv_kernel, with the query tiles copied HBM/L2 -> LDS by
+// global_load_lds into a ring of four stages, three tiles ahead of the math,
+// one barrier per tile. Stage = Q and dO tiles (64 rows of 128 bytes, chunks
+// swizzled by swz64: conflict-free for the S/dP operands' 16-byte row reads and
+// the dK/dV operands' transpose reads), then LSE·log2e and Δ of the 64 queries.
+// Wave w copies Q and dO rows 16w..16w+15 (two 8-row instructions each); wave 2
+// also copies the 64 LSE values (and converts them in place once they have
+// landed), wave 3 the 64 Δ values. Rows past S read row S-1 (always masked).
+constexpr int kKvStages = 4;
+constexpr int kKvTileB = 64 * 128;             // one 64x64 16-bit tile, bytes
+constexpr int kKvStageB = 2 * kKvTileB + 512;  // Q, dO, LSE·log2e, Δ
+
+template <int DT, int FEAT = 0>
+__global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
+    const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
+    const uint16_t* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    uint16_t* __restrict__ dK, uint16_t* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
+    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
+    int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
+    int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
+  static_assert((FEAT & kFeatMask) == 0, "caller masks take wattn_bwd_kv_kernel");
+  constexpr int D = 64;
+  constexpr bool DR = (FEAT & kFeatDrop) != 0;
+  using T = Tile<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t ring[kKvStages * kKvStageB / 2];
+
+  int bh, kb;
+  if (!work_item(wm, order, bh, kb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;  // uniform
+  const int l32 = lane & 31, h = lane >> 5;
+  const int grp = (lane >> 4) & 1;
+  const int key = kb * 128 + wave * 32 + l32;  // this lane's key
+  const Span span = mask_col_span(mp, key);     // the queries that see it (partial tiles only)
+
+  u32x4 kf[T::kKk], vf[T::kKk];
+  {
+    const int kc = min(key, S - 1);
+    const uint16_t* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + 8 * h;
+    const uint16_t* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + 8 * h;
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) {
+      kf[kk] = ldg16(kp + 16 * kk);
+      vf[kk] = ldg16(vp + 16 * kk);
+    }
+#pragma unroll
+    for (int kk = 0; kk < T::kKk; ++kk) {
+      settle(kf[kk]);
+      settle(vf[kk]);
+    }
+  }
+  const uint16_t* Qbh = Q + b * qsb + hd * qsh;
+  const uint16_t* Gbh = dO + b * gsb + hd * gsh;
+  const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
+  const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
+  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  const int n = e1 - e0;
+
+  // Copies: this wave's rows of Q and dO, chunk positions as for swz64 (lane L
+  // of an instruction covering rows R..R+7 fills chunk position L & 7 of row
+  // R + L / 8 with the global chunk the swizzle stores there).
+  const int drow = lane >> 3, dpos = lane & 7;
+  int crow[2];
+  uint32_t cchunk[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    crow[j] = 16 * wave + 8 * j + drow;
+    const int a = (crow[j] >> 1) & 7;
+    cchunk[j] = 16u * static_cast<uint32_t>(dpos ^ (((a & 1) << 2) | (a >> 1)));
+  }
+  const uint32_t ring0 = lds_offset(ring);
+  auto issue = [&](int idx) __attribute__((always_inline)) {
+    const int qt = entries[e0 + idx] & 0xffff;
+    const uint32_t st = ring0 + static_cast<uint32_t>((idx % kKvStages) * kKvStageB);
+    const int lim = S - 1 - qt * 64;  // rows beyond this one read it instead
+    const uint16_t* qb = Qbh + static_cast<int64_t>(qt) * 64 * qss;
+    const uint16_t* gb = Gbh + static_cast<int64_t>(qt) * 64 * gss;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t r = static_cast<uint32_t>(min(crow[j], lim));
+      dma_lds16(qb, r * static_cast<uint32_t>(2 * qss) + cchunk[j], st + (16 * wave + 8 * j) * 128);
+      dma_lds16(gb, r * static_cast<uint32_t>(2 * gss) + cchunk[j],
+                st + kKvTileB + (16 * wave + 8 * j) * 128);
+    }
+    if (wave >= 2) {
+      const float* sb = wave == 2 ? lse_bh : dl_bh;
+      dma_lds4(sb, 4u * static_cast<uint32_t>(min(qt * 64 + lane, S - 1)),
+               st + 2 * kKvTileB + (wave - 2) * 256);
+    }
+  };
+
+  f32x16 dkt[T::kDt], dvt[T::kDt];
+#pragma unroll
+  for (int dt = 0; dt < T::kDt; ++dt) {
+    dkt[dt] = f32x16{};
+    dvt[dt] = f32x16{};
+  }
+
+  for (int i = 0; i < kKvStages - 1 && i < n; ++i) issue(i);
+  for (int i = 0; i < n; ++i) {
+    // this wave's copies of tile i have landed when at most those of the (up
+    // to kKvStages - 2) later tiles already issued are outstanding: four copies
+    // per tile for waves 0-1, five for waves 2-3
+    const int later = min(kKvStages - 2, n - 1 - i);
+    if (wave >= 2) {
+      if (later == 2) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+      else if (later == 1) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    } else {
+      if (later == 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+      else if (later == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    const uint16_t* st = ring + (i % kKvStages) * (kKvStageB / 2);
+    float* lse2 = reinterpret_cast<float*>(const_cast<uint16_t*>(st) + 2 * (kKvTileB / 2));
+    if (wave == 2) {
+      // LSE -> LSE·log2e, in place (this wave's copy has landed)
+      lse2[lane] = lse_log2<false>(lse2[lane]);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    // every wave's copies of tile i are in LDS (and converted), and every wave
+    // is done reading the stage the next copies overwrite (tile i-1's)
+    asm volatile("s_barrier" ::: "memory");
+    if (i + kKvStages - 1 < n) issue(i + kKvStages - 1);
+
+    const int ent = entries[e0 + i];
+    const int qt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    if (kind != 0) {
+      const uint16_t* q_lds = st;
+      const uint16_t* g_lds = st + kKvTileB / 2;
+      const float* lse_l = lse2;
+      const float* dl_l = lse2 + 64;
+      // S and dP of both 32-query halves first: the second half's MFMAs run
+      // while the first half's softmax is on the vector ALU.
+      f32x16 s2[2], dp2[2];
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        s2[qh] = f32x16{};
+        dp2[qh] = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < T::kKk; ++kk) {
+          const u32x4 qa = lds16(q_lds + swz64(32 * qh + l32, 2 * kk + h));
+          const u32x4 ga = lds16(g_lds + swz64(32 * qh + l32, 2 * kk + h));
+          s2[qh] = Mfma<DT>::run(qa, kf[kk], s2[qh]);
+          dp2[qh] = Mfma<DT>::run(ga, vf[kk], dp2[qh]);
+        }
+      }
+      // s2[qh][j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4
+      if (kind == 2) {
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          const int base = qt * 64 + 32 * qh + 4 * h;
+          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
+#pragma unroll
+          for (int j = 0; j < 16; ++j) {
+            const int off = 8 * (j >> 2) + (j & 3);
+            s2[qh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s2[qh][j] : -INFINITY;
+          }
+        }
+      }
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        f32x16& s = s2[qh];
+        f32x16& dp = dp2[qh];
+        kv_half_update<DT, D, DR>(s, dp, scale_log2, lse_l, dl_l, qh, qt * 64, h, grp, lane, key,
+                                  bh, ax, q_lds, g_lds, dkt, dvt,
+                                  [&](const uint16_t* t, int r0, int r1, int c0) {
+                                    return lds_read_tr4x2_swz64(t, r0, r1, c0, lane);
+                                  });
+      }
+    }
   }
 
   if (key >= S) return;
@@ -1492,6 +1699,18 @@ void launch_bwd_mfma(const AttnLaunch& a) {
                      qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
                      gs[2], dqs[0], dqs[1], dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr,
                      a.entries, a.order, a.wm_q, a.ax_q);
+  // The copy-ring kernel addresses 64 rows of Q and dO with 32-bit byte offsets.
+  if constexpr (D == 64 && (FEAT & kFeatMask) == 0) {
+    if (qs[2] <= (1ll << 25) && gs[2] <= (1ll << 25)) {
+      hipLaunchKernelGGL((wattn_bwd_kv64_kernel<DT, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
+                         K, V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
+                         static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
+                         vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0],
+                         dvs[1], dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr,
+                         a.entries_kv, a.order_kv, a.wm_kv, a.ax_kv);
+      return;
+    }
+  }
   hipLaunchKernelGGL((wattn_bwd_kv_kernel<DT, D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
                      V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
                      static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
