@@ -531,8 +531,8 @@ __global__ __launch_bounds__(256, 2) void bell_sddmm_kernel(
   for (int i = 0; i < kSdStages - 1 && i < n_steps; ++i) issue(i);
   for (int i = 0; i < n_steps; ++i) {
     // this wave's copies of step i have landed when at most those of the
-    // (up to two) later steps already issued are outstanding
-    wait_vm(5 * min(2, n_steps - 1 - i));
+    // (up to kSdStages - 2) later steps already issued are outstanding
+    wait_vm(5 * min(kSdStages - 2, n_steps - 1 - i));
     const int m0 = m_begin + i * kSdRows;
     uint16_t* st = ring + (i % kSdStages) * kSdStage;
     if (m0 + kSdRows > m_end) {
