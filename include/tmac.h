@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 4
+#define TMAC_ABI_VERSION 5
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -124,6 +124,35 @@ int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
                   const void* d_bias, void* d_Y, int64_t ldy,
                   int M, int n_brow, int n_bcol, int width,
                   int dtype, int epi, void* stream);
+
+/* Forward of fc1 with the erf GELU in training: Y = gelu(Z) and Z = X·W + bias
+ * (the pre-activation, kept for tmac_bell_gelu_bwd), both written by the
+ * forward kernel's epilogue, so the activation costs no pass of its own.
+ * Replaces `self.fc1(x)` followed by `self.activation(hidden)` of
+ * MLPBlock.forward when gradients are recorded (blocks/mlp.py:58,61). As
+ * tmac_bell_fwd with epi = TMAC_EPI_GELU, plus Z [M, N] with leading dimension
+ * ldz; dtype TMAC_BF16 or TMAC_F16. */
+int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
+                           const int32_t* d_t_ptr, const int32_t* d_t_row,
+                           const int32_t* d_t_vblk, const int32_t* d_order,
+                           const void* d_bias, void* d_Y, int64_t ldy, void* d_Z, int64_t ldz,
+                           int M, int n_brow, int n_bcol, int width, int dtype, void* stream);
+
+/* Bytes of device workspace tmac_bell_gelu_bwd needs for the bias gradient. */
+int tmac_bell_gelu_bwd_workspace(int M, int N, size_t* ws_bytes);
+
+/* GELU backward and bias gradient of fc1, one pass over the gradient:
+ * gZ = gA ⊙ GELU'(Z) (erf form) for [M, N] row-major 16-bit operands with
+ * leading dimensions (N and the pitches multiples of 8), and with d_dbias
+ * non-null dbias[n] = Σ_m gZ[m][n] in fp32 (of the stored 16-bit gZ, summed in
+ * a fixed order: deterministic; 0 when M = 0). Replaces autograd's backward of
+ * nn.GELU and the bias gradient of fc1 in MLPBlock's backward
+ * (blocks/mlp.py:58,61). d_ws: tmac_bell_gelu_bwd_workspace bytes (needed with
+ * d_dbias only; the row operands may be null when M = 0). dtype: TMAC_BF16 or
+ * TMAC_F16. */
+int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_Z, int64_t ldz, void* d_gZ,
+                       int64_t ldgz, float* d_dbias, void* d_ws, size_t ws_bytes, int M, int N,
+                       int dtype, void* stream);
 
 /* Input gradient: dX[M, K] = dY[M, N] · Wᵀ, fp32 accumulation.
  * Replaces autograd's grad_input of F.linear in the MLP backward

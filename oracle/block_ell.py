@@ -137,6 +137,14 @@ def gelu_erf(x: np.ndarray) -> np.ndarray:
     return 0.5 * x * (1.0 + erf(x / math.sqrt(2.0)))
 
 
+def gelu_erf_grad(x: np.ndarray) -> np.ndarray:
+    """d/dx of gelu_erf: Φ(x) + x φ(x), the derivative autograd applies for
+    nn.GELU() in MLPBlock's backward (blocks/mlp.py:42,61)."""
+    erf = np.vectorize(math.erf, otypes=[np.float64])
+    x = np.asarray(x, dtype=np.float64)
+    return 0.5 * (1.0 + erf(x / math.sqrt(2.0))) + x * np.exp(-0.5 * x * x) / math.sqrt(2.0 * math.pi)
+
+
 def fwd(X: np.ndarray, col_idx: np.ndarray, values: np.ndarray, n_bcol: int,
         bias: np.ndarray | None = None, gelu: bool = False, dtype=np.float64) -> np.ndarray:
     """Y = X · to_dense(W) (+ bias) (then GELU), accumulated in `dtype`."""

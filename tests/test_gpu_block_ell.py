@@ -325,3 +325,71 @@ def test_row_pitch_inputs_and_padded_outputs(dev, M):
     assert (Yw[:, :8] == sentinel).all() and (Yw[:, 8 + N:] == sentinel).all()
     assert torch.equal(dXw[:, 16:16 + K], dx)
     assert (dXw[:, :16] == sentinel).all() and (dXw[:, 16 + K:] == sentinel).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [50, 300])  # few-row kernel, gather GEMM
+def test_fwd_gelu_aux_outputs_bit_exact(dev, dtype, M):
+    """tmac_bell_fwd_gelu_aux writes gelu(z) and z: bit-identical to the plain
+    forward with and without its fused GELU (same kernel, same sums)."""
+    pat, X, V, _, b = data(M, 4, 6, 3, dtype, seed=M)
+    i = pat.device_index(dev)
+    args = (X.to(dev), V.to(dev), i["col_idx"], i["t_ptr"], i["t_row"], i["t_vblk"], i["order"], b.to(dev))
+    a, z = kb._bell_fwd_gelu(*args)
+    assert torch.equal(z, kb._bell_fwd(*args, False))
+    assert torch.equal(a, kb._bell_fwd(*args, True))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N", [(0, 64), (1, 64), (257, 192), (5000, 2560)])
+def test_gelu_bwd_and_bias_grad(dev, dtype, M, N):
+    """gz = ga ⊙ GELU'(z) against the fp64 oracle (16-bit bar); the bias gradient is
+    the column sum of the stored gz (fp32, fixed order: rerun bit-identical)."""
+    g = torch.Generator().manual_seed(M + N)
+    ga = torch.randn(M, N, generator=g).to(dtype)
+    z = (torch.randn(M, N, generator=g) * 3).to(dtype)
+    gz, db = kb._bell_gelu_bwd(ga.to(dev), z.to(dev), True)
+    want = ga.double().numpy() * ob.gelu_erf_grad(z.double().numpy())
+    close(gz.float().cpu(), want)
+    colsum = gz.double().cpu().numpy().sum(0)
+    assert np.abs(db.cpu().numpy() - colsum).max() <= 1e-5 * (1.0 + np.abs(gz.double().cpu().numpy()).sum(0).max())
+    gz2, db2 = kb._bell_gelu_bwd(ga.to(dev), z.to(dev), True)
+    assert torch.equal(gz, gz2) and torch.equal(db, db2)
+    gz3, db3 = kb._bell_gelu_bwd(ga.to(dev), z.to(dev), False)
+    assert torch.equal(gz3, gz) and db3.numel() == 0
+
+
+def test_mlp_block_ell_bf16_training_fused_gelu(dev):
+    """A bf16 Block-ELL MLP in training (fc1 + GELU through the kernel that also stores
+    the pre-activation; GELU' and fc1's bias gradient in one pass): output and the
+    gradients of x, both layers' blocks and biases against an fp64 oracle that rounds
+    to bf16 where the kernels store (z, gelu(z), the fc2 input gradient, gz)."""
+    from titans_core.blocks.mlp import MLPBlock
+    torch.manual_seed(4)
+    mlp = MLPBlock(128, 384, block_ell=True, density=0.5, seed=5).to(dev, torch.bfloat16).train()
+    x = torch.randn(3, 100, 128, device=dev).to(torch.bfloat16).requires_grad_(True)
+    y = mlp(x)
+    gy = torch.randn_like(y)
+    y.backward(gy)
+    r16 = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).double().numpy()  # noqa: E731
+    f1, f2 = mlp.fc1, mlp.fc2
+    c1, c2 = f1.col_idx.cpu().numpy(), f2.col_idx.cpu().numpy()
+    V1 = f1.values.detach().double().cpu().numpy()
+    V2 = f2.values.detach().double().cpu().numpy()
+    b1 = f1.bias.detach().double().cpu().numpy()
+    b2 = f2.bias.detach().double().cpu().numpy()
+    X = x.detach().double().cpu().numpy().reshape(-1, 128)
+    G = gy.double().cpu().numpy().reshape(-1, 128)
+    zf = ob.fwd(X, c1, V1, 6, b1)
+    z = r16(zf)
+    a = r16(ob.gelu_erf(zf))
+    close(y.detach().float().cpu().reshape(-1, 128), ob.fwd(a, c2, V2, 2, b2))
+    ga = r16(ob.dx(G, c2, V2, 2))
+    gz = r16(ga * ob.gelu_erf_grad(z))
+    close(x.grad.float().cpu().reshape(-1, 128), ob.dx(gz, c1, V1, 6))
+    close(f1.bias.grad.float().cpu(), gz.sum(0), atol=0.1)
+    close(f2.bias.grad.float().cpu(), G.sum(0), atol=0.1)
+    w1 = ob.sddmm(X, gz, c1)
+    close(f1.values.grad.float().cpu(), w1, atol=1e-2 * np.abs(w1).max())
+    w2 = ob.sddmm(a, G, c2)
+    close(f2.values.grad.float().cpu(), w2, atol=1e-2 * np.abs(w2).max())

@@ -209,6 +209,39 @@ def test_bell_fwd_argument_errors(lib):
     assert lib.tmac_bell_fwd(*bad) == -5          # ldx not a multiple of 8
 
 
+def test_fused_gelu_argument_errors(lib):
+    """tmac_bell_fwd_gelu_aux and tmac_bell_gelu_bwd reject bad arguments before
+    any launch (no GPU needed)."""
+    ok = [FAKE, 2560, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, 10240, FAKE, 10240, 8192, 40, 160, 40,
+          1, None]
+    bad = list(ok); bad[10] = None
+    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -1        # Z required
+    bad = list(ok); bad[16] = 0
+    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -4        # 16-bit only
+    bad = list(ok); bad[11] = 10200
+    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -2        # ldz < N
+    bad = list(ok); bad[10] = MISALIGNED
+    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -5
+    ws = ctypes.c_size_t(0)
+    assert lib.tmac_bell_gelu_bwd_workspace(32768, 2560, ctypes.byref(ws)) == 0
+    assert ws.value == 256 * 2560 * 4                    # 256 row parts of fp32 column sums
+    assert lib.tmac_bell_gelu_bwd_workspace(-1, 2560, ctypes.byref(ws)) == -2
+    g = [FAKE, 2560, FAKE, 2560, FAKE, 2560, FAKE, FAKE, ws.value, 32768, 2560, 1, None]
+    bad = list(g); bad[0] = None
+    assert lib.tmac_bell_gelu_bwd(*bad) == -1
+    bad = list(g); bad[7] = None
+    assert lib.tmac_bell_gelu_bwd(*bad) == -1            # bias gradient needs the workspace
+    bad = list(g); bad[10] = 2564
+    assert lib.tmac_bell_gelu_bwd(*bad) == -2            # N % 8
+    bad = list(g); bad[11] = 0
+    assert lib.tmac_bell_gelu_bwd(*bad) == -4
+    bad = list(g); bad[8] = ws.value - 1
+    assert lib.tmac_bell_gelu_bwd(*bad) == -6
+    bad = list(g); bad[1] = 2568
+    bad[4] = MISALIGNED
+    assert lib.tmac_bell_gelu_bwd(*bad) == -5
+
+
 def test_bell_dx_and_sddmm_argument_errors(lib):
     assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 0, 10, 40, 20, 1, None) == -2
     assert lib.tmac_bell_dx(FAKE, 2560, FAKE, FAKE, FAKE, 640, 100, 10, 40, 20, 3, None) == -4

@@ -159,3 +159,19 @@ def test_dense_round_trip_and_bias_gelu():
     X = rng.standard_normal((4, 192))
     b = rng.standard_normal(320)
     assert np.allclose(ob.fwd(X, ci, V, 5, b, gelu=True), ob.gelu_erf(X @ W + b))
+
+
+def test_gelu_grad_against_autograd_and_closed_form():
+    """The oracle's GELU derivative is torch autograd's for the exact-erf GELU
+    (fp64), and at 0 it is 1/2 (Φ(0) = 1/2, the x φ(x) term vanishes); far out
+    it tends to 1 (x >> 0) and 0 (x << 0)."""
+    import torch
+    x = np.linspace(-8.0, 8.0, 1601)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    torch.nn.functional.gelu(xt).sum().backward()
+    assert np.allclose(ob.gelu_erf_grad(x), xt.grad.numpy(), rtol=1e-13, atol=1e-15)
+    assert float(ob.gelu_erf_grad(np.array([0.0]))[0]) == 0.5
+    assert math.isclose(float(ob.gelu_erf_grad(np.array([1.0]))[0]),
+                        0.8413447460685429 + 0.24197072451914337, rel_tol=1e-12)
+    assert abs(float(ob.gelu_erf_grad(np.array([10.0]))[0]) - 1.0) < 1e-12
+    assert abs(float(ob.gelu_erf_grad(np.array([-10.0]))[0])) < 1e-12

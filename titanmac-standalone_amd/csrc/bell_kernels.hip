@@ -80,8 +80,8 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
     const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ in_blk,
     const int32_t* __restrict__ t_vblk, const int32_t* __restrict__ order,
-    const uint16_t* __restrict__ bias, int epi, uint16_t* __restrict__ Y, int64_t ldy, int M,
-    int n_out, int width, int n_mtiles, int per_xcd) {
+    const uint16_t* __restrict__ bias, int epi, uint16_t* __restrict__ Y, int64_t ldy,
+    uint16_t* __restrict__ Z, int64_t ldz, int M, int n_out, int width, int n_mtiles, int per_xcd) {
   // Two buffers, each the activation tile (kBM x 64, xswz) and the weight
   // block (64 x 64, swz64); the epilogue's four per-wave 64x64 staging tiles
   // (pitch kPitch) reuse the same memory.
@@ -242,8 +242,10 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   }
 
   // Epilogue: bias, activation, conversion, then pack through this wave's LDS
-  // staging tile and store 128-byte row segments.
+  // staging tile and store 128-byte row segments. With Z (forward only), the
+  // pre-activation goes to Z as well, through a second staging tile.
   uint16_t* stage = smem0 + wave * kTileElems;
+  uint16_t* stage_z = smem1 + wave * kTileElems;
   const int64_t col0 = static_cast<int64_t>(ob) * 64;
   // the bias values of this lane's 32 columns, all eight loads in flight at once
   u32x2 bb[2][4] = {};
@@ -271,6 +273,12 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
           v[2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
           v[3] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y >> 16));
         }
+        if (Z) {
+          u32x2 pz;
+          pz.x = Mfma<DT>::pack2(v[0], v[1]);
+          pz.y = Mfma<DT>::pack2(v[2], v[3]);
+          *reinterpret_cast<u32x2*>(stage_z + (32 * mi + l32) * kPitch + n_loc) = pz;
+        }
         if (epi == TMAC_EPI_GELU) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) v[t] = gelu_erf(v[t]);
@@ -285,7 +293,10 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   for (int it = 0; it < 8; ++it) {
     const int row = it * 8 + (lane >> 3), ch = lane & 7;
     const int grow = m_base + row;
-    if (grow < M) stg16(Y + static_cast<int64_t>(grow) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+    if (grow < M) {
+      stg16(Y + static_cast<int64_t>(grow) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+      if (Z) stg16(Z + static_cast<int64_t>(grow) * ldz + col0 + ch * 8, lds16(stage_z + row * kPitch + ch * 8));
+    }
   }
 }
 
@@ -306,7 +317,7 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
     const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ t_row,
     const int32_t* __restrict__ t_vblk, const uint16_t* __restrict__ bias, int epi,
-    uint16_t* __restrict__ Y, int64_t ldy, int M) {
+    uint16_t* __restrict__ Y, int64_t ldy, uint16_t* __restrict__ Z, int64_t ldz, int M) {
   // Per wave and stage: activation tile (64 x 64, xswz) then weight block
   // (64 x 64, swz64). Separate arrays per stage, so the compiler can tell the
   // copies into one stage from the reads of the other.
@@ -399,9 +410,10 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
 #pragma unroll
         for (int j = 0; j < 16; ++j) acc[mi][ni][j] += red[(w * 64 + (mi * 2 + ni) * 16 + j) * 64 + lane];
 
-  // Epilogue as in bell_gemm_kernel, for wave 0's 64 rows (staging tile in
+  // Epilogue as in bell_gemm_kernel, for wave 0's 64 rows (staging tiles in
   // stage-1 memory, which no wave touches any more).
   uint16_t* stage = &st1[0][0];
+  uint16_t* stage_z = &st1[1][0];
   const int64_t col0 = static_cast<int64_t>(ob) * 64;
   // the bias values of this lane's 32 columns, all eight loads in flight at once
   u32x2 bb[2][4] = {};
@@ -429,6 +441,12 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
           v[2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
           v[3] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y >> 16));
         }
+        if (Z) {
+          u32x2 pz;
+          pz.x = Mfma<DT>::pack2(v[0], v[1]);
+          pz.y = Mfma<DT>::pack2(v[2], v[3]);
+          *reinterpret_cast<u32x2*>(stage_z + (32 * mi + l32) * kPitch + n_loc) = pz;
+        }
         if (epi == TMAC_EPI_GELU) {
 #pragma unroll
           for (int t = 0; t < 4; ++t) v[t] = gelu_erf(v[t]);
@@ -441,7 +459,10 @@ __global__ __launch_bounds__(256) void bell_fwd_small_kernel(
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int row = it * 8 + (lane >> 3), ch = lane & 7;
-    if (row < M) stg16(Y + static_cast<int64_t>(row) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+    if (row < M) {
+      stg16(Y + static_cast<int64_t>(row) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+      if (Z) stg16(Z + static_cast<int64_t>(row) * ldz + col0 + ch * 8, lds16(stage_z + row * kPitch + ch * 8));
+    }
   }
 }
 
@@ -820,6 +841,81 @@ __global__ __launch_bounds__(256) void bell_sddmm_reduce_kernel(const float* __r
   }
 }
 
+// GELU backward with the bias gradient's partial sums (fc1 of an MLP in
+// training): gZ = gA ⊙ gelu_erf_grad(Z) for [M, N] 16-bit rows (N a multiple
+// of 8), and with part non-null part[p][n] = the sum of the stored (rounded)
+// gZ[m][n] over the rows of part p (rows p·R .. p·R + R - 1). Workgroup = 512
+// columns x 4 waves: each wave reads 1 KB of one row per instruction (lane =
+// 8 columns) and walks rows w, w + 4, ... of the part; the 4 waves' sums are
+// added through LDS in a fixed order, and column_sum_kernel adds the parts in
+// a fixed order: deterministic for given (M, N). Grid (ceil(N / 512), parts).
+constexpr int kGeluParts = 256;  // at most this many row parts
+
+template <int DT>
+__global__ __launch_bounds__(256) void bell_gelu_bwd_kernel(
+    const uint16_t* __restrict__ gA, int64_t lda, const uint16_t* __restrict__ Z, int64_t ldz,
+    uint16_t* __restrict__ gZ, int64_t ldg, float* __restrict__ part, int M, int N,
+    int rows_per_part) {
+  __shared__ float red[4][512];
+  const int cg = threadIdx.x & 63, rl = threadIdx.x >> 6;
+  const int col = blockIdx.x * 512 + cg * 8;
+  const int r0 = blockIdx.y * rows_per_part;
+  const int r1 = min(M, r0 + rows_per_part);
+  float acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+  if (col < N) {
+    // four rows per pass, their eight loads issued together (rows past the
+    // part read its last row, valid memory, and are computed but neither
+    // stored nor summed)
+    for (int r = r0 + rl; r < r1; r += 16) {
+      u32x4 a[4], z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rr = min(r + 4 * u, r1 - 1);
+        a[u] = ldg16(gA + static_cast<int64_t>(rr) * lda + col);
+        z[u] = ldg16(Z + static_cast<int64_t>(rr) * ldz + col);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool valid = r + 4 * u < r1;
+        const uint32_t aw[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+        const uint32_t zw[4] = {z[u].x, z[u].y, z[u].z, z[u].w};
+        uint32_t ow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float g0 = Mfma<DT>::to_f32(static_cast<uint16_t>(aw[i] & 0xffff)) *
+                           gelu_erf_grad(Mfma<DT>::to_f32(static_cast<uint16_t>(zw[i] & 0xffff)));
+          const float g1 = Mfma<DT>::to_f32(static_cast<uint16_t>(aw[i] >> 16)) *
+                           gelu_erf_grad(Mfma<DT>::to_f32(static_cast<uint16_t>(zw[i] >> 16)));
+          ow[i] = Mfma<DT>::pack2(g0, g1);
+          acc[2 * i] += valid ? Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] & 0xffff)) : 0.f;
+          acc[2 * i + 1] += valid ? Mfma<DT>::to_f32(static_cast<uint16_t>(ow[i] >> 16)) : 0.f;
+        }
+        if (valid) stg16(gZ + static_cast<int64_t>(r + 4 * u) * ldg + col, u32x4{ow[0], ow[1], ow[2], ow[3]});
+      }
+    }
+  }
+  if (!part) return;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) red[rl][cg * 8 + k] = acc[k];
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int cl = threadIdx.x + 256 * h;
+    const int c = blockIdx.x * 512 + cl;
+    if (c < N) part[static_cast<int64_t>(blockIdx.y) * N + c] = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+  }
+}
+
+// Row parts of bell_gelu_bwd_kernel: about 128 rows each, at most kGeluParts.
+void gelu_parts(int M, int* n_parts, int* rows_per_part) {
+  int p = (M + 127) / 128;
+  p = p < 1 ? 1 : (p > kGeluParts ? kGeluParts : p);
+  *n_parts = p;
+  *rows_per_part = (M + p - 1) / p;
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 int check_bell_shape(int M, int n_brow, int n_bcol, int width) {
@@ -860,22 +956,25 @@ size_t sddmm_ws_bytes(int M, int n_brow, int width) {
 
 }  // namespace
 
-extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
-                             const int32_t* d_t_ptr, const int32_t* d_t_row,
-                             const int32_t* d_t_vblk, const int32_t* d_order, const void* d_bias,
-                             void* d_Y, int64_t ldy, int M, int n_brow, int n_bcol, int width,
-                             int dtype, int epi, void* stream) {
+namespace {
+
+// tmac_bell_fwd, and with d_Z (16-bit, epi GELU) tmac_bell_fwd_gelu_aux.
+int bell_fwd_impl(const void* d_X, int64_t ldx, const void* d_vals, const int32_t* d_t_ptr,
+                  const int32_t* d_t_row, const int32_t* d_t_vblk, const int32_t* d_order,
+                  const void* d_bias, void* d_Y, int64_t ldy, void* d_Z, int64_t ldz, int M,
+                  int n_brow, int n_bcol, int width, int dtype, int epi, void* stream) {
   if (!d_X || !d_vals || !d_t_ptr || !d_t_row || !d_t_vblk || !d_order || !d_Y) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
   if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
   if (epi != TMAC_EPI_NONE && epi != TMAC_EPI_GELU) return TMAC_ERR_VALUE;
   const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
-  if (ldx < K || ldy < N) return TMAC_ERR_SHAPE;
+  if (ldx < K || ldy < N || (d_Z && ldz < N)) return TMAC_ERR_SHAPE;
   const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16 bytes
   if (!aligned16(d_X) || !aligned16(d_vals) || !aligned16(d_Y) || (ldx % vec) || (ldy % vec))
     return TMAC_ERR_ALIGN;
   if (d_bias && !aligned16(d_bias)) return TMAC_ERR_ALIGN;
+  if (d_Z && (!aligned16(d_Z) || (ldz % vec))) return TMAC_ERR_ALIGN;
   if (dtype == TMAC_F32) {
     const int n_mt = (M + kBMf - 1) / kBMf;
     const int64_t tot = static_cast<int64_t>(n_mt) * n_bcol;
@@ -897,24 +996,48 @@ extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
   const auto* V = static_cast<const uint16_t*>(d_vals);
   const auto* b = static_cast<const uint16_t*>(d_bias);
   auto* Y = static_cast<uint16_t*>(d_Y);
+  auto* Z = static_cast<uint16_t*>(d_Z);
   if (M <= kSmallM) {
     if (dtype == TMAC_BF16)
       hipLaunchKernelGGL((bell_fwd_small_kernel<TMAC_BF16>), dim3(n_bcol), dim3(256), 0, s, X, ldx, V,
-                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, M);
+                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, Z, ldz, M);
     else
       hipLaunchKernelGGL((bell_fwd_small_kernel<TMAC_F16>), dim3(n_bcol), dim3(256), 0, s, X, ldx, V,
-                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, M);
+                         d_t_ptr, d_t_row, d_t_vblk, b, epi, Y, ldy, Z, ldz, M);
     return launch_status();
   }
   if (dtype == TMAC_BF16)
     hipLaunchKernelGGL((bell_gemm_kernel<TMAC_BF16, true>), dim3(8 * per_xcd), dim3(256), 0, s, X,
-                       ldx, V, d_t_ptr, d_t_row, d_t_vblk, d_order, b, epi, Y, ldy, M, n_bcol, width,
-                       n_mtiles, per_xcd);
+                       ldx, V, d_t_ptr, d_t_row, d_t_vblk, d_order, b, epi, Y, ldy, Z, ldz, M, n_bcol,
+                       width, n_mtiles, per_xcd);
   else
     hipLaunchKernelGGL((bell_gemm_kernel<TMAC_F16, true>), dim3(8 * per_xcd), dim3(256), 0, s, X,
-                       ldx, V, d_t_ptr, d_t_row, d_t_vblk, d_order, b, epi, Y, ldy, M, n_bcol, width,
-                       n_mtiles, per_xcd);
+                       ldx, V, d_t_ptr, d_t_row, d_t_vblk, d_order, b, epi, Y, ldy, Z, ldz, M, n_bcol,
+                       width, n_mtiles, per_xcd);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
+                             const int32_t* d_t_ptr, const int32_t* d_t_row,
+                             const int32_t* d_t_vblk, const int32_t* d_order, const void* d_bias,
+                             void* d_Y, int64_t ldy, int M, int n_brow, int n_bcol, int width,
+                             int dtype, int epi, void* stream) {
+  return bell_fwd_impl(d_X, ldx, d_vals, d_t_ptr, d_t_row, d_t_vblk, d_order, d_bias, d_Y, ldy,
+                       nullptr, 0, M, n_brow, n_bcol, width, dtype, epi, stream);
+}
+
+extern "C" int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
+                                      const int32_t* d_t_ptr, const int32_t* d_t_row,
+                                      const int32_t* d_t_vblk, const int32_t* d_order,
+                                      const void* d_bias, void* d_Y, int64_t ldy, void* d_Z,
+                                      int64_t ldz, int M, int n_brow, int n_bcol, int width,
+                                      int dtype, void* stream) {
+  if (!d_Z) return TMAC_ERR_NULL;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  return bell_fwd_impl(d_X, ldx, d_vals, d_t_ptr, d_t_row, d_t_vblk, d_order, d_bias, d_Y, ldy,
+                       d_Z, ldz, M, n_brow, n_bcol, width, dtype, TMAC_EPI_GELU, stream);
 }
 
 extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
@@ -950,12 +1073,12 @@ extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
   auto* dX = static_cast<uint16_t*>(d_dX);
   if (dtype == TMAC_BF16)
     hipLaunchKernelGGL((bell_gemm_kernel<TMAC_BF16, false>), dim3(8 * per_xcd), dim3(256), 0, s,
-                       dY, lddy, V, nullptr, d_col_idx, nullptr, nullptr, nullptr, 0, dX, lddx, M,
-                       n_brow, width, n_mtiles, per_xcd);
+                       dY, lddy, V, nullptr, d_col_idx, nullptr, nullptr, nullptr, 0, dX, lddx, nullptr,
+                       0, M, n_brow, width, n_mtiles, per_xcd);
   else
     hipLaunchKernelGGL((bell_gemm_kernel<TMAC_F16, false>), dim3(8 * per_xcd), dim3(256), 0, s,
-                       dY, lddy, V, nullptr, d_col_idx, nullptr, nullptr, nullptr, 0, dX, lddx, M,
-                       n_brow, width, n_mtiles, per_xcd);
+                       dY, lddy, V, nullptr, d_col_idx, nullptr, nullptr, nullptr, 0, dX, lddx, nullptr,
+                       0, M, n_brow, width, n_mtiles, per_xcd);
   return launch_status();
 }
 
@@ -1022,4 +1145,55 @@ extern "C" int tmac_bell_sddmm(const void* d_X, int64_t ldx, const void* d_dY, i
     hipLaunchKernelGGL((bell_sddmm_reduce_kernel<TMAC_F16>), dim3(grid), dim3(256), 0, s, part,
                        d_dvals, n_elem, n_splits);
   return launch_status();
+}
+
+extern "C" int tmac_bell_gelu_bwd_workspace(int M, int N, size_t* ws_bytes) {
+  if (!ws_bytes) return TMAC_ERR_NULL;
+  if (M < 0 || N <= 0) return TMAC_ERR_SHAPE;
+  int n_parts, rows;
+  gelu_parts(M, &n_parts, &rows);
+  *ws_bytes = static_cast<size_t>(n_parts) * N * sizeof(float);
+  return TMAC_OK;
+}
+
+extern "C" int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_Z, int64_t ldz,
+                                  void* d_gZ, int64_t ldgz, float* d_dbias, void* d_ws,
+                                  size_t ws_bytes, int M, int N, int dtype, void* stream) {
+  // with M = 0 the row operands are not read (empty tensors may pass null)
+  if ((M > 0 && (!d_gA || !d_Z || !d_gZ)) || (d_dbias && !d_ws)) return TMAC_ERR_NULL;
+  if (M < 0 || N <= 0 || (N % 8) || ldga < N || ldz < N || ldgz < N) return TMAC_ERR_SHAPE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (!aligned16(d_gA) || !aligned16(d_Z) || !aligned16(d_gZ) || (ldga % 8) || (ldz % 8) ||
+      (ldgz % 8))
+    return TMAC_ERR_ALIGN;
+  int n_parts, rows;
+  gelu_parts(M, &n_parts, &rows);
+  float* part = nullptr;
+  if (d_dbias) {
+    if (ws_bytes < static_cast<size_t>(n_parts) * N * sizeof(float)) return TMAC_ERR_WORKSPACE;
+    if (!aligned16(d_ws)) return TMAC_ERR_ALIGN;
+    part = static_cast<float*>(d_ws);
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M > 0) {
+    const dim3 grid(static_cast<unsigned>((N + 511) / 512), static_cast<unsigned>(n_parts));
+    const auto* gA = static_cast<const uint16_t*>(d_gA);
+    const auto* Z = static_cast<const uint16_t*>(d_Z);
+    auto* gZ = static_cast<uint16_t*>(d_gZ);
+    if (dtype == TMAC_BF16)
+      hipLaunchKernelGGL((bell_gelu_bwd_kernel<TMAC_BF16>), grid, dim3(256), 0, s, gA, ldga, Z, ldz,
+                         gZ, ldgz, part, M, N, rows);
+    else
+      hipLaunchKernelGGL((bell_gelu_bwd_kernel<TMAC_F16>), grid, dim3(256), 0, s, gA, ldga, Z, ldz,
+                         gZ, ldgz, part, M, N, rows);
+    const int st = launch_status();
+    if (st != TMAC_OK) return st;
+  }
+  if (d_dbias) {
+    // with M = 0 there are no partials: the sums over zero parts are 0
+    hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(256), 0, s,
+                       part, d_dbias, static_cast<int64_t>(N), M > 0 ? n_parts : 0, int64_t{0});
+    return launch_status();
+  }
+  return TMAC_OK;
 }

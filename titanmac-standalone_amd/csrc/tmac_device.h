@@ -492,4 +492,19 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erf_z);
 }
 
+// d/dx of gelu_erf: Φ(x) + x φ(x) = 0.5 (1 + erf(x/√2)) + x exp(-x²/2) / √(2π),
+// with the same erf approximation (the exp2 term is exp(-x²/2) itself).
+__device__ __forceinline__ float gelu_erf_grad(float x) {
+  const float z = x * 0.70710678118654752440f;
+  const float az = fabsf(z);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, az, 1.0f));
+  float poly = fmaf(1.061405429f, t, -1.453152027f);
+  poly = fmaf(poly, t, 1.421413741f);
+  poly = fmaf(poly, t, -0.284496736f);
+  poly = fmaf(poly, t, 0.254829592f) * t;
+  const float e = __builtin_amdgcn_exp2f(-(az * az) * 1.4426950408889634f);
+  const float erf_z = copysignf(fmaf(-poly, e, 1.0f), z);
+  return fmaf(x * 0.39894228040143268f, e, 0.5f * (1.0f + erf_z));
+}
+
 }  // namespace tmac

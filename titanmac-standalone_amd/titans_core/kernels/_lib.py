@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -42,6 +42,10 @@ SIGNATURES = {
     "tmac_bell_validate": [_vp, _i, _i, _i],
     "tmac_bell_transpose": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "tmac_bell_fwd": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _i, _vp],
+    "tmac_bell_fwd_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i, _i, _i,
+                               _i, _i, _vp],
+    "tmac_bell_gelu_bwd_workspace": [_i, _i, ctypes.POINTER(_sz)],
+    "tmac_bell_gelu_bwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _vp],
     "tmac_bell_dx": [_vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_sddmm_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
     "tmac_bell_sddmm": [_vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _sz, _i, _i, _i, _i, _i, _vp],

@@ -169,6 +169,86 @@ def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu):
     return x.new_empty((*x.shape[:-1], BLOCK * n_bcol))
 
 
+def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
+                   t_ptr: torch.Tensor, t_row: torch.Tensor, t_vblk: torch.Tensor,
+                   order: torch.Tensor, bias: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(gelu(z), z) with z = x · W + bias, both from the forward kernel's epilogue
+    (16-bit only): the training form of fc1 + GELU, z kept for the backward."""
+    _check_values(values, "bell_fwd_gelu")
+    if values.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"bell_fwd_gelu: bfloat16 or float16 only, got {values.dtype}")
+    n_brow, width = int(values.shape[0]), int(values.shape[1])
+    n_bcol = int(t_ptr.numel()) - 1
+    K, N = BLOCK * n_brow, BLOCK * n_bcol
+    if x.shape[-1] != K:
+        raise ValueError(f"bell_fwd_gelu: x has {x.shape[-1]} features, W has {K} rows")
+    if x.dtype != values.dtype:
+        raise TypeError(f"bell_fwd_gelu: x dtype {x.dtype} != values dtype {values.dtype}")
+    dev = _lib.require_device(x, values, t_ptr, what="bell_fwd_gelu")
+    x2, ldx = _rows(x, K)
+    M = x2.shape[0]
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
+    z = torch.empty((M, N), dtype=x.dtype, device=dev)
+    if M > 0:
+        if bias is not None:
+            if bias.shape != (N,) or bias.dtype != x.dtype:
+                raise ValueError(f"bell_fwd_gelu: bias must be [{N}] of {x.dtype}")
+            bias = bias.contiguous()
+        with _lib.device_guard(dev):
+            rc = _lib.lib().tmac_bell_fwd_gelu_aux(
+                _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
+                _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M,
+                n_brow, n_bcol, width, _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+        _lib.check(rc, "tmac_bell_fwd_gelu_aux")
+    shape = (*x.shape[:-1], N)
+    return y.reshape(shape), z.reshape(shape)
+
+
+bell_fwd_gelu = torch.library.custom_op("titanmac::bell_fwd_gelu", mutates_args=())(_bell_fwd_gelu)
+
+
+@bell_fwd_gelu.register_fake
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias):
+    shape = (*x.shape[:-1], BLOCK * (t_ptr.shape[0] - 1))
+    return x.new_empty(shape), x.new_empty(shape)
+
+
+def _bell_gelu_bwd(ga: torch.Tensor, z: torch.Tensor, with_bias: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(gz, dbias): gz = ga ⊙ GELU'(z) in z's dtype, and with with_bias the fp32
+    column sums of gz (else an empty tensor), in one pass over ga and z."""
+    N = z.shape[-1]
+    dev = _lib.require_device(ga, z, what="bell_gelu_bwd")
+    if ga.dtype != z.dtype:
+        ga = ga.to(z.dtype)
+    ga2, ldga = _rows(ga, N)
+    z2, ldz = _rows(z, N)
+    M = z2.shape[0]
+    gz = torch.empty((M, N), dtype=z.dtype, device=dev)
+    db = torch.empty((N,) if with_bias else (0,), dtype=torch.float32, device=dev)
+    L = _lib.lib()
+    ws = None
+    if with_bias:
+        import ctypes
+        nb = ctypes.c_size_t(0)
+        _lib.check(L.tmac_bell_gelu_bwd_workspace(M, N, ctypes.byref(nb)), "tmac_bell_gelu_bwd_workspace")
+        ws = torch.empty(max(1, (nb.value + 15) // 16 * 4), dtype=torch.float32, device=dev)
+    with _lib.device_guard(dev):
+        rc = L.tmac_bell_gelu_bwd(_lib.ptr(ga2), ldga, _lib.ptr(z2), ldz, _lib.ptr(gz), N,
+                                  _lib.ptr(db) if with_bias else None, _lib.ptr(ws),
+                                  ws.numel() * 4 if ws is not None else 0, M, N,
+                                  _lib.dtype_code(z.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_bell_gelu_bwd")
+    return gz.reshape(z.shape), db
+
+
+bell_gelu_bwd = torch.library.custom_op("titanmac::bell_gelu_bwd", mutates_args=())(_bell_gelu_bwd)
+
+
+@bell_gelu_bwd.register_fake
+def _(ga, z, with_bias):
+    return z.new_empty(z.shape), z.new_empty((z.shape[-1],) if with_bias else (0,), dtype=torch.float32)
+
+
 def _bell_dx(dy: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, n_bcol: int) -> torch.Tensor:
     """dX = dY · Wᵀ; dy [..., 64*n_bcol] -> dx [..., 64*n_brow]."""
     _check_values(values, "bell_dx")
@@ -281,13 +361,47 @@ def _fwd_backward(ctx, gy):
 bell_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
 
 
+def _fwd_gelu_setup_context(ctx, inputs, output):
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias = inputs
+    ctx.mark_non_differentiable(output[1])
+    ctx.set_materialize_grads(False)  # no zero-filled gradient for the pre-activation output
+    ctx.save_for_backward(x, values, col_idx, output[1])
+    ctx.n_bcol = int(t_ptr.shape[0]) - 1
+    ctx.has_bias = bias is not None
+    ctx.bias_dtype = bias.dtype if bias is not None else None
+
+
+def _fwd_gelu_backward(ctx, ga, _gz_unused):
+    """GELU' and the bias gradient in one pass (bell_gelu_bwd), then dX and the
+    SDDMM on gz."""
+    x, values, col_idx, z = ctx.saved_tensors
+    n_brow, width = int(values.shape[0]), int(values.shape[1])
+    if ga is None:
+        ga = torch.zeros_like(z)
+    want_b = ctx.has_bias and ctx.needs_input_grad[7]
+    gz, db = bell_gelu_bwd(ga, z, want_b)
+    gx = gv = gb = None
+    if ctx.needs_input_grad[0]:
+        gx = bell_dx(gz, values, col_idx, ctx.n_bcol).to(x.dtype)
+    if ctx.needs_input_grad[1]:
+        gv = bell_sddmm(x, gz, col_idx, n_brow, width, values.dtype)
+    if want_b:
+        gb = db.to(ctx.bias_dtype)
+    return gx, gv, None, None, None, None, None, gb
+
+
+bell_fwd_gelu.register_autograd(_fwd_gelu_backward, setup_context=_fwd_gelu_setup_context)
+
+
 def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern,
                  bias: Optional[torch.Tensor] = None, activation: Optional[str] = None) -> torch.Tensor:
     """y = activation(x · W + bias) with W = (pattern, values) in Block-ELL.
 
     activation: None or "gelu" (erf form, as nn.GELU()). The GELU is fused into
-    the kernel's store when no gradient is required; otherwise it is applied as
-    a separate op so autograd can differentiate it. The kernels compute in
+    the kernel's store. When gradients are recorded (16-bit), the kernel also
+    stores the pre-activation, and the backward computes GELU' and the bias
+    gradient in one pass over the gradient (titanmac::bell_fwd_gelu); fp32 runs
+    the GELU as a separate op. The kernels compute in
     bfloat16 / float16 (fp32 accumulation) or float32 (fp32 MFMA); under
     torch.autocast the inputs are cast to the autocast dtype first, as for
     nn.Linear.
@@ -304,6 +418,12 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
     idx = pattern.device_index(values.device)
     fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
         x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
+    if activation == "gelu" and not fuse and values.dtype in (torch.bfloat16, torch.float16):
+        # training: the kernel writes gelu(z) and z; the backward runs GELU' and
+        # the bias gradient in one pass (bell_fwd_gelu's autograd)
+        y, _ = bell_fwd_gelu(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
+                             idx["order"], bias)
+        return y
     op = _bell_fwd if _lib.direct_call(x, values, bias) else bell_fwd
     y = op(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"], idx["order"], bias,
            fuse)
