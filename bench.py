@@ -17,7 +17,9 @@ The same run also times, as secondary figures:
     mask (block 64);
   - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
     masked bf16 backward (five bmm over the full S x S);
-  - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40);
+  - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40), and one
+    bf16 training step (forward + backward) of a Block-ELL MLPBlock 640 -> 2560 -> 640 at
+    that shape;
   - the causal depthwise conv of BlockSparseAttention (B=8, T=4096, 1920 channels,
     4 taps) and TitanBlock's RMSNorm (32768 x 640), forward and backward, in GB/s
     of compulsory HBM traffic;
@@ -38,8 +40,8 @@ PyTorch paths of configs 1, 3 and 4 are timed on the CPU as secondary figures.
 roofline.traffic is measured by the run itself: two rocprofv3 counter passes (FETCH_SIZE,
 WRITE_SIZE) over `--mode traffic` of the current build, scaled by a plain 1 GiB copy.
 
-Modes (for profiling runs): all (default), spmm, attn, attn_bwd, dx, sddmm, conv, norm, mac,
-mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE),
+Modes (for profiling runs): all (default), spmm, attn, attn_bwd, attn_ex, dx, sddmm, bell_f32,
+mlp_train, conv, norm, mac, mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE),
 traffic (the copy then the SpMM, three launches each: what the counter passes profile).
 """
 from __future__ import annotations
@@ -167,6 +169,26 @@ def setup_bell_f32(dev):
     out["bwd_flops"] = 2 * c4["M"] * c4["n_brow"] * c4["width"] * BS * BS
     out["keep"] = (X, V, idx, X4, dY4, V4, idx4)
     return out
+
+
+def setup_mlp_train(dev):
+    """One training step (forward + backward) of a bf16 Block-ELL MLPBlock at config 4's
+    shape: 640 -> 2560 -> 640 at 50% density, 32768 rows; fc1 + GELU through the fused
+    training path (tmac_bell_fwd_gelu_aux, tmac_bell_gelu_bwd)."""
+    from titans_core.blocks.mlp import MLPBlock
+    c4 = CFG4
+    torch.manual_seed(c4["seed"])
+    m = MLPBlock(BS * c4["n_brow"], BS * c4["n_bcol"], block_ell=True, density=0.5,
+                 seed=c4["seed"]).to(dev, torch.bfloat16).train()
+    x = gen((c4["M"], BS * c4["n_brow"]), c4["seed"] + 1).to(dev).requires_grad_(True)
+    gy = gen((c4["M"], BS * c4["n_brow"]), c4["seed"] + 2).to(dev)
+
+    def launch():
+        x.grad = None
+        m.zero_grad(set_to_none=True)
+        m(x).backward(gy)
+    nnz = m.fc1.pattern.nnz_blocks + m.fc2.pattern.nnz_blocks
+    return dict(launch=launch, flops=3 * 2 * c4["M"] * nnz * BS * BS, keep=(m, x, gy))
 
 
 def setup_attn(dev, S=None, pattern=None, block_size=64):
@@ -722,7 +744,7 @@ def main() -> int:
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 measurement of roofline.traffic (null)")
     ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "attn_ex", "dx",
-                                                     "bell_f32",
+                                                     "bell_f32", "mlp_train",
                                                      "sddmm", "conv",
                                                      "norm", "mac", "mac_ttm", "memupd", "copy",
                                                      "traffic"])
@@ -817,6 +839,11 @@ def main() -> int:
             ms = timed(bw["sddmm"], K, W, stream)
             out["sddmm"] = dict(ms=ms, tflops=bw["flops"] / ms / 1e9, gbs=bw["sd_bytes"] / ms / 1e6)
 
+    if args.mode in ("all", "mlp_train"):
+        wl = setup_mlp_train(dev)
+        ms = timed(wl["launch"], K, W, stream)
+        out["mlp_train"] = dict(ms=ms, tflops=wl["flops"] / ms / 1e9)
+        del wl
     if args.mode in ("all", "bell_f32"):
         wl = setup_bell_f32(dev)
         f_ms = timed(wl["fwd"], K, W, stream)
@@ -917,6 +944,8 @@ def main() -> int:
             "bell_sddmm_cfg4_ms": round(out["sddmm"]["ms"], 5),
             "bell_sddmm_cfg4_tflops": round(out["sddmm"]["tflops"], 3),
             "bell_sddmm_cfg4_hbm_gbs_compulsory": round(out["sddmm"]["gbs"], 1),
+            "bell_mlp_train_step_cfg4_ms": round(out["mlp_train"]["ms"], 5),
+            "bell_mlp_train_step_cfg4_tflops": round(out["mlp_train"]["tflops"], 3),
             "dwconv_fwd_ms": round(out["conv"]["fwd_ms"], 5),
             "dwconv_fwd_hbm_gbs_compulsory": round(out["conv"]["fwd_gbs"], 1),
             "dwconv_bwd_ms": round(out["conv"]["bwd_ms"], 5),
