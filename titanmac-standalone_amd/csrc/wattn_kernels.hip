@@ -42,15 +42,29 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
-// Row log-sum-exp in log2 units for the backward. A row that a caller's mask
-// masks fully has lse = -inf (and output 0): it gets +inf, so each of its
-// probabilities exp2(s - l2) is 0 (also for s = -inf).
-// Caller's-mask slices of kind 2 (allowed pairs all have bias 0): v[j] keeps its
-// score where bit 8(j/4) + j%4 of w is set, else -inf. w holds this lane's 32
-// positions of a 32-wide half tile, already shifted to the lane's origin.
+// Masking of a partial 32-wide half tile: v[j] keeps its score where bit
+// 8(j/4) + j%4 of w is set, else -inf. w holds this lane's 32 positions of the
+// half tile, shifted to the lane's origin. The bit, moved to the sign and
+// shifted back, is an all-ones or zero mask that selects between the score and
+// -inf bit by bit (two instructions per element).
 __device__ __forceinline__ void apply_bits(f32x16& v, uint32_t w) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = ((w >> (8 * (j >> 2) + (j & 3))) & 1u) ? v[j] : -INFINITY;
+  for (int j = 0; j < 16; ++j) {
+    const int bit = 8 * (j >> 2) + (j & 3);
+    const uint32_t keep = static_cast<uint32_t>(static_cast<int32_t>(w << (31 - bit)) >> 31);
+    v[j] = __uint_as_float((__float_as_uint(v[j]) & keep) | (0xff800000u & ~keep));
+  }
+}
+
+// Bits [0, n) of a 32-bit word (none for n <= 0, all for n >= 32).
+__device__ __forceinline__ uint32_t below32(int n) {
+  return n <= 0 ? 0u : (n >= 32 ? ~0u : (1u << n) - 1u);
+}
+
+// Bit t (t < 32) set iff position o + t lies in the span: t < np - o, or
+// lo - o <= t <= hi - o. Built once per half tile for apply_bits.
+__device__ __forceinline__ uint32_t span_bits32(const Span& s, int o) {
+  return below32(s.np - o) | (below32(s.hi - o + 1) & ~below32(s.lo - o));
 }
 
 // Register operands loaded once before a tile loop (this lane's Q, K or V rows)
@@ -60,6 +74,9 @@ __device__ __forceinline__ void apply_bits(f32x16& v, uint32_t w) {
 // prefetch before the first MFMA of every tile.
 __device__ __forceinline__ void settle(u32x4& v) { asm volatile("" : "+v"(v)); }
 
+// Row log-sum-exp in log2 units for the backward. A row that a caller's mask
+// masks fully has lse = -inf (and output 0): it gets +inf, so each of its
+// probabilities exp2(s - l2) is 0 (also for s = -inf).
 template <bool CM>
 __device__ __forceinline__ float lse_log2(float lse) {
   const float l2 = lse * kLog2e;
@@ -248,17 +265,10 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
             }
         }
       } else if (kind == 2) {
-        // key - (kt*64 + 4h) is a constant per element, so the span bounds move
-        // to this lane's origin and each test compares a constant with them.
-        const int base = kt * 64 + 4 * h;
-        const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
+        // key - (kt*64 + 32kh + 4h) is 8(j/4) + j%4: the span as bits from this
+        // lane's origin in each half
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int off = 32 * kh + 8 * (j >> 2) + (j & 3);
-            st[kh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? st[kh][j] : -INFINITY;
-          }
+        for (int kh = 0; kh < 2; ++kh) apply_bits(st[kh], span_bits32(span, kt * 64 + 32 * kh + 4 * h));
       }
       float mx = -INFINITY;
 #pragma unroll
@@ -717,13 +727,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
             }
           }
         } else if (kind == 2) {
-          const int base = qt * 64 + 32 * qh + 4 * h;
-          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int off = 8 * (j >> 2) + (j & 3);
-            s[j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[j] : -INFINITY;
-          }
+          apply_bits(s, span_bits32(span, qt * 64 + 32 * qh + 4 * h));
         }
         kv_half_update<DT, D, DR>(s, dp, sc, &stat[buf][0][0], &stat[buf][1][0], qh, qt * 64, h,
                                   grp, lane, key, bh, ax, q_lds, g_lds, dkt, dvt,
@@ -900,15 +904,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
       // s2[qh][j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4
       if (kind == 2) {
 #pragma unroll
-        for (int qh = 0; qh < 2; ++qh) {
-          const int base = qt * 64 + 32 * qh + 4 * h;
-          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int off = 8 * (j >> 2) + (j & 3);
-            s2[qh][j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s2[qh][j] : -INFINITY;
-          }
-        }
+        for (int qh = 0; qh < 2; ++qh) apply_bits(s2[qh], span_bits32(span, qt * 64 + 32 * qh + 4 * h));
       }
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh) {
@@ -1100,13 +1096,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
             }
           }
         } else if (kind == 2) {
-          const int base = kt * 64 + 4 * h;
-          const int np = span.np - base, lo = span.lo - base, hi = span.hi - base;
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            const int off = 32 * kh + 8 * (j >> 2) + (j & 3);
-            s[j] = ((off < np) | ((off >= lo) & (off <= hi))) ? s[j] : -INFINITY;
-          }
+          apply_bits(s, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
         }
 #pragma unroll
         for (int jg = 0; jg < 4; ++jg) {
