@@ -26,8 +26,9 @@ The same run also times, as secondary figures:
   - config 5: the full TitanMAC forward (MAC variant, 16 layers, d_model 640, 10 heads,
     window 512, 16 persistent tokens, 32 memory tokens per 512-token segment, Block-ELL
     MLP at 50%, vocab 50000, random init) on token ids [4, 4096] in bf16, eval, in
-    tokens/s; once with the read-only memory of the default config (segments batched) and
-    once with test-time memory on (segments in order, one memory update each);
+    tokens/s; once with the read-only memory of the default config (segments batched),
+    once with test-time memory on (segments in order, one memory update each), and once
+    more so with each segment's layer stack replayed from a captured HIP graph;
   - the neural-memory update step (norm, clip, momentum, forgetting) over config 5's
     memory MLP (2 x 640 x 640 + biases, fp32) in GB/s of compulsory traffic.
 Inputs are drawn on the CPU from fixed seeds and copied to HBM before timing.
@@ -357,8 +358,9 @@ CFG5 = dict(B=4, T=4096, vocab_size=50000, d_model=640, n_heads=10, n_layers=16,
             n_persistent=16, seed=7)
 
 
-def setup_mac(dev, test_time_memory=False):
-    """Config 5: TitanMAC forward (MAC) with the Block-ELL MLP at 50%, bf16, eval."""
+def setup_mac(dev, test_time_memory=False, graph=False):
+    """Config 5: TitanMAC forward (MAC) with the Block-ELL MLP at 50%, bf16, eval; with graph,
+    the layer stack of each segment replays a captured HIP graph (TitanMAC.capture_block_graph)."""
     sys.path.insert(0, str(ROOT / "titanmac-standalone_amd"))
     import titans_core as tc
     c = CFG5
@@ -369,6 +371,8 @@ def setup_mac(dev, test_time_memory=False):
                             mlp_density=0.5, enable_test_time_memory=test_time_memory)
     torch.manual_seed(c["seed"])
     model = tc.TitanMAC(cfg).to(dev, torch.bfloat16).eval()
+    if graph:
+        model.capture_block_graph(c["B"])
     g = torch.Generator().manual_seed(c["seed"] + 1)
     ids = torch.randint(0, c["vocab_size"], (c["B"], c["T"]), generator=g).to(dev)
     res = {}
@@ -868,9 +872,10 @@ def main() -> int:
         del mu
     # whole-model forwards: a few steps keep the timed region to seconds
     k5, w5 = max(2, min(K, 10)), max(1, min(W, 3))
-    for key, ttm in (("mac", False), ("mac_ttm", True)):
-        if args.mode in ("all", key):
-            wl = setup_mac(dev, ttm)
+    for key, ttm, graph in (("mac", False, False), ("mac_ttm", True, False),
+                            ("mac_ttm_graph", True, True)):
+        if args.mode in ("all", key) or (key == "mac_ttm_graph" and args.mode == "mac_ttm"):
+            wl = setup_mac(dev, ttm, graph)
             ms = timed(wl["launch"], k5, w5, stream)
             out[key] = dict(ms=ms, tokens_per_s=wl["tokens"] / ms * 1e3, steps=k5)
             del wl
@@ -959,6 +964,7 @@ def main() -> int:
             "titanmac_mac_fwd_cfg5_test_time_memory_tokens_per_s": round(
                 out["mac_ttm"]["tokens_per_s"], 1),
             "titanmac_mac_fwd_cfg5_test_time_memory_ms": round(out["mac_ttm"]["ms"], 3),
+            "titanmac_mac_fwd_cfg5_test_time_memory_block_graph_ms": round(out["mac_ttm_graph"]["ms"], 3),
             "neural_memory_update_cfg5_ms": round(out["memupd"]["ms"], 5),
             "neural_memory_update_cfg5_hbm_gbs_compulsory": round(out["memupd"]["gbs"], 1),
         },

@@ -451,3 +451,41 @@ def test_gradient_checkpointing_gives_identical_gradients(dev):
     assert grads[0].keys() == grads[1].keys() and len(grads[0]) > 10
     for n in grads[0]:
         assert torch.equal(grads[0][n], grads[1][n]), n
+
+
+@pytest.mark.parametrize("bsa", [True, False])
+def test_block_graph_replays_match_eager_test_time_memory(dev, bsa):
+    """TitanMAC.capture_block_graph: an eval MAC forward with test-time memory replays the
+    captured layer stack for every full segment. Two models from the same seed, one eager and
+    one with the graph, run three forwards each (the memory changes between them): logits and
+    the memory MLP bit-identical after every call, with eager GPU work between the replays.
+    After a parameter is replaced (not updated in place) the graph no longer applies and the
+    layers run eagerly, still bit-identical."""
+    cfg = dict(MAC_CFG, vocab_size=97, d_model=128, n_heads=2, n_layers=3, d_ff=256,
+               max_seq_len=256, window_size=64, n_persistent=8, block_size=32,
+               segment_size=64, n_memory_tokens=16, use_block_sparse=bsa,
+               enable_test_time_memory=True, titans_variant="MAC", mlp_block_ell=True,
+               mlp_density=0.5)
+    models = []
+    for _ in range(2):
+        torch.manual_seed(11)
+        models.append(tc.TitanMAC(tc.TitanMACConfig(**cfg)).to(dev, torch.bfloat16).eval())
+    eager, graphed = models
+    B = 3
+    graphed.capture_block_graph(B)
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, 97, (B, 200), generator=g).to(dev)  # 3 full segments + a short one
+    with torch.no_grad():
+        for call in range(3):
+            a = eager(ids)["logits"]
+            _ = torch.ones(4096, device=dev).sum()
+            b = graphed(ids)["logits"]
+            assert torch.equal(a, b), f"call {call}"
+        assert graphed._block_graph["replays"] == 3 * 3  # the full segments of three calls
+        fa = eager.neural_memory.memory_mlp.get_flat_params()
+        fb = graphed.neural_memory.memory_mlp.get_flat_params()
+        assert torch.equal(fa, fb)
+        graphed.layers[0].norm_attn.scale = torch.nn.Parameter(graphed.layers[0].norm_attn.scale.clone())
+        assert torch.equal(eager(ids)["logits"], graphed(ids)["logits"])
+        assert graphed._block_graph["replays"] == 9  # replaced parameter: eager layers
+    graphed.release_block_graph()

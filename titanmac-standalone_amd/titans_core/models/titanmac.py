@@ -76,6 +76,7 @@ class TitanMAC(nn.Module):
             self.memory_proj = None
             self.gate_proj = None
         self.gradient_checkpointing = False
+        self._block_graph = None
         self._init_weights()
 
     def _init_weights(self) -> None:
@@ -110,6 +111,67 @@ class TitanMAC(nn.Module):
             else:
                 y = layer(y, attn_mask=None)
         return y
+
+    # ------------------------------------------------------------------ block-stack graph
+
+    def _tensor_ptrs(self):
+        return tuple(t.data_ptr() for t in list(self.parameters()) + list(self.buffers()))
+
+    def capture_block_graph(self, batch: int, seq_len: Optional[int] = None) -> None:
+        """Capture the layer stack for one input shape [batch, seq_len, d_model] in a HIP graph.
+
+        For eval forwards with test-time memory, whose segments run the layers one after
+        another with small batches: there the host's launch rate, not the GPU, sets the pace,
+        and one graph replay replaces a few hundred launches. seq_len defaults to the MAC
+        segment shape, n_persistent + n_memory_tokens + segment_size. Without gradients and
+        outside training, ``forward_mac`` then replays the graph for every input of that
+        shape, dtype and device; other inputs, and any call after a parameter or buffer was
+        replaced (not updated in place, e.g. by ``.to()``), run the layers eagerly again.
+        Results are bit-identical to the eager layers (the same kernels on the same data).
+        Capture again after such changes; ``release_block_graph`` frees the graph.
+        """
+        if seq_len is None:
+            seq_len = self.config.n_persistent + self.config.n_memory_tokens + self.config.segment_size
+        p = next(self.parameters())
+        if not p.is_cuda:
+            raise RuntimeError("capture_block_graph needs the model on a GPU")
+        self.release_block_graph()
+        static_in = torch.zeros(batch, seq_len, self.config.d_model, dtype=p.dtype, device=p.device)
+        was_training = self.training
+        self.eval()
+        try:
+            side = torch.cuda.Stream(device=p.device)
+            side.wait_stream(torch.cuda.current_stream(p.device))
+            with torch.cuda.stream(side), torch.no_grad():
+                for _ in range(2):  # warm-up outside the capture (lazy caches, libraries)
+                    self._blocks(static_in)
+            torch.cuda.current_stream(p.device).wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph), torch.no_grad():
+                static_out = self._blocks(static_in)
+        finally:
+            self.train(was_training)
+        self._block_graph = {"graph": graph, "in": static_in, "out": static_out,
+                             "ptrs": self._tensor_ptrs(), "replays": 0}
+
+    def release_block_graph(self) -> None:
+        self._block_graph = None
+
+    def _graph_blocks(self, parts) -> torch.Tensor:
+        """blocks(cat(parts, dim=1)) through the captured graph when it applies; the result
+        stays valid until the next call (the graph's output buffer)."""
+        gr = self._block_graph
+        if gr is not None and not self.training and not torch.is_grad_enabled():
+            st = gr["in"]
+            if (all(t.dtype == st.dtype and t.device == st.device for t in parts)
+                    and sum(t.shape[1] for t in parts) == st.shape[1]
+                    and all(t.shape[0] == st.shape[0] and t.shape[2] == st.shape[2] for t in parts)
+                    and self._tensor_ptrs() == gr["ptrs"]):
+                torch.cat(parts, dim=1, out=st)
+                gr["graph"].replay()
+                gr["replays"] += 1
+                return gr["out"]
+        return self._blocks(torch.cat(parts, dim=1))
 
     def _memory_step(self, y: torch.Tensor) -> torch.Tensor:
         if self.training or self.config.enable_test_time_memory:
@@ -191,7 +253,7 @@ class TitanMAC(nn.Module):
                 q = xs.mean(dim=1, keepdim=True).expand(B, nl, -1)
                 h = self.memory_proj(self.neural_memory.retrieve(q))
                 parts = [h, xs] if persistent is None else [persistent, h, xs]
-                y = self._blocks(torch.cat(parts, dim=1))
+                y = self._graph_blocks(parts)
                 ys = y[:, Np + nl:]
                 acc = acc + self._memory_step(ys)
                 gate = torch.sigmoid(self.gate_proj(self.neural_memory.retrieve(ys)))
