@@ -290,9 +290,9 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
 
       // Pᵀ as the B operand, 16 keys per MFMA: k-step ks covers keys
       // 16ks..16ks+15 and lane t-th value is key 16ks + 8(t/4) + 4h + t%4. The
-      // row sum stays in fp32, in four chains.
+      // row sum stays in fp32, in four chains started by the first k-step.
       u32x4 pb[4];
-      float r4[4] = {0.f, 0.f, 0.f, 0.f};
+      float r4[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int kh = ks >> 1, j0 = 8 * (ks & 1);
@@ -315,7 +315,7 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
             w[t] = Mfma<DT>::pack2(p0 * z[2 * t], p1 * z[2 * t + 1]);
           else
             w[t] = Mfma<DT>::pack2(p0, p1);
-          r4[t] += p0 + p1;
+          r4[t] = ks == 0 ? p0 + p1 : r4[t] + (p0 + p1);
         }
         pb[ks] = u32x4{w[0], w[1], w[2], w[3]};
       }
@@ -510,40 +510,62 @@ __device__ __forceinline__ void store_row(uint16_t* rowp, const f32x16 (&acc)[ND
     }
 }
 
+// −Δ of the queries of a 32-query half in accumulator order (element j: row
+// 32qh + 8(j/4) + 4h + j%4 of the tile), from the staged −Δ values: the initial
+// dP accumulator, so the MFMAs produce dP − Δ.
+__device__ __forceinline__ f32x16 neg_delta_acc(const float* ndl_l, int qh, int h) {
+  f32x16 r;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndl_l + 32 * qh + 8 * g + 4 * h);
+    r[4 * g] = d4.x;
+    r[4 * g + 1] = d4.y;
+    r[4 * g + 2] = d4.z;
+    r[4 * g + 3] = d4.w;
+  }
+  return r;
+}
+
 // The vector-ALU and dV/dK part of one 32-query half of a listed tile, for
-// the wave's 32 keys (both dK/dV kernels). s and dp hold S (scaled to log2
-// units by sc) and dP of the half, element j for query q0 + 8(j/4) + j%4 with
-// q0 = qbase + 32qh + 4h; lse_l and dl_l hold LSE·log2e and Δ of the tile's 64
-// queries. Forms P and dS in place (with kFeatDrop, P ⊙ Z for dV and
+// the wave's 32 keys (both dK/dV kernels). s holds S of the half (scaled to
+// log2 units by sc), element j for query q0 + 8(j/4) + j%4 with q0 = qbase +
+// 32qh + 4h; lse_l and ndl_l hold LSE·log2e and −Δ of the tile's 64 queries.
+// dp holds dP − Δ (its accumulator started from neg_delta_acc), or, with
+// kFeatDrop, dP. Forms P and dS in place (with kFeatDrop, P ⊙ Z for dV and
 // P ⊙ (Z ⊙ dP − Δ)), then dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, dOᵀ and Qᵀ taken by
 // tr(tile, r0, r1, c0), a transpose read of rows r0..r0+3 and r1..r1+3 at
 // column c0 of the staged tile, in the accumulator's permuted query order.
 template <int DT, int D, bool DR, class TrRead>
 __device__ __forceinline__ void kv_half_update(f32x16& s, f32x16& dp, float sc, const float* lse_l,
-                                               const float* dl_l, int qh, int qbase, int h,
+                                               const float* ndl_l, int qh, int qbase, int h,
                                                int grp, int lane, int key, int bh,
                                                const AttnX& ax, const uint16_t* q_lds,
                                                const uint16_t* g_lds, f32x16 (&dkt)[D / 32],
                                                f32x16 (&dvt)[D / 32], TrRead tr) {
-  // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e and Δ as one 16-byte read each
+  // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e (and −Δ) as one 16-byte read each
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse_l + 32 * qh + 8 * g + 4 * h);
-    const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl_l + 32 * qh + 8 * g + 4 * h);
-    const float lv[4] = {l4.x, l4.y, l4.z, l4.w}, dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-    uint32_t kq = 0;
-    if constexpr (DR) kq = keep_quad(ax, bh, qbase + 32 * qh + 8 * g + 4 * h, key, lane & 3);
+    const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+    if constexpr (DR) {
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndl_l + 32 * qh + 8 * g + 4 * h);
+      const float nd[4] = {d4.x, d4.y, d4.z, d4.w};
+      const uint32_t kq = keep_quad(ax, bh, qbase + 32 * qh + 8 * g + 4 * h, key, lane & 3);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int j = 4 * g + t;
-      const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
-      if constexpr (DR) {
+      for (int t = 0; t < 4; ++t) {
+        const int j = 4 * g + t;
+        const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
         const float z = ((kq >> (4 * t)) & 1u) ? ax.keep_scale : 0.f;
         s[j] = pj * z;
-        dp[j] = pj * (z * dp[j] - dv4[t]);
-      } else {
+        dp[j] = pj * fmaf(z, dp[j], nd[t]);
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int j = 4 * g + t;
+        const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -lv[t]));
         s[j] = pj;
-        dp[j] = pj * (dp[j] - dv4[t]);
+        dp[j] *= pj;
       }
     }
   }
@@ -584,7 +606,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
   constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
-  // [buffer][Q, dO] 64 x D tiles, then [buffer] LSE·log2e and Δ of the 64 queries.
+  // [buffer][Q, dO] 64 x D tiles, then [buffer] LSE·log2e and −Δ of the 64 queries.
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
   __shared__ __attribute__((aligned(16))) float stat[2][2][64];
 
@@ -671,7 +693,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
       sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
       sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
     }
-    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<CM>(st_pre) : st_pre;
+    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<CM>(st_pre) : -st_pre;
   };
 
   f32x16 dkt[T::kDt], dvt[T::kDt];
@@ -704,7 +726,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
       const uint16_t* g_lds = smem + (2 * buf + 1) * T::kElems;
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh) {
-        f32x16 s = f32x16{}, dp = f32x16{};
+        f32x16 s = f32x16{};
+        f32x16 dp = DR ? f32x16{} : neg_delta_acc(&stat[buf][1][0], qh, h);
 #pragma unroll
         for (int kk = 0; kk < T::kKk; ++kk) {
           const u32x4 qa = lds16(q_lds + (32 * qh + l32) * T::kP + 16 * kk + 8 * h);
@@ -752,10 +775,11 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
 // global_load_lds into a ring of four stages, three tiles ahead of the math,
 // one barrier per tile. Stage = Q and dO tiles (64 rows of 128 bytes, chunks
 // swizzled by swz64: conflict-free for the S/dP operands' 16-byte row reads and
-// the dK/dV operands' transpose reads), then LSE·log2e and Δ of the 64 queries.
+// the dK/dV operands' transpose reads), then LSE·log2e and −Δ of the 64 queries.
 // Wave w copies Q and dO rows 16w..16w+15 (two 8-row instructions each); wave 2
-// also copies the 64 LSE values (and converts them in place once they have
-// landed), wave 3 the 64 Δ values. Rows past S read row S-1 (always masked).
+// also copies the 64 LSE values and wave 3 the 64 Δ values, each converting
+// its values in place once they have landed. Rows past S read row S-1 (always
+// masked).
 constexpr int kKvStages = 4;
 constexpr int kKvTileB = 64 * 128;             // one 64x64 16-bit tile, bytes
 constexpr int kKvStageB = 2 * kKvTileB + 512;  // Q, dO, LSE·log2e, Δ
@@ -868,9 +892,11 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
     }
     const uint16_t* st = ring + (i % kKvStages) * (kKvStageB / 2);
     float* lse2 = reinterpret_cast<float*>(const_cast<uint16_t*>(st) + 2 * (kKvTileB / 2));
-    if (wave == 2) {
-      // LSE -> LSE·log2e, in place (this wave's copy has landed)
-      lse2[lane] = lse_log2<false>(lse2[lane]);
+    if (wave >= 2) {
+      // LSE -> LSE·log2e (wave 2) and Δ -> −Δ (wave 3), in place (this wave's
+      // copy has landed)
+      float* v = lse2 + 64 * (wave - 2) + lane;
+      *v = wave == 2 ? lse_log2<false>(*v) : -*v;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     // every wave's copies of tile i are in LDS (and converted), and every wave
@@ -885,14 +911,14 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
       const uint16_t* q_lds = st;
       const uint16_t* g_lds = st + kKvTileB / 2;
       const float* lse_l = lse2;
-      const float* dl_l = lse2 + 64;
+      const float* ndl_l = lse2 + 64;
       // S and dP of both 32-query halves first: the second half's MFMAs run
       // while the first half's softmax is on the vector ALU.
       f32x16 s2[2], dp2[2];
 #pragma unroll
       for (int qh = 0; qh < 2; ++qh) {
         s2[qh] = f32x16{};
-        dp2[qh] = f32x16{};
+        dp2[qh] = DR ? f32x16{} : neg_delta_acc(ndl_l, qh, h);
 #pragma unroll
         for (int kk = 0; kk < T::kKk; ++kk) {
           const u32x4 qa = lds16(q_lds + swz64(32 * qh + l32, 2 * kk + h));
@@ -910,7 +936,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
       for (int qh = 0; qh < 2; ++qh) {
         f32x16& s = s2[qh];
         f32x16& dp = dp2[qh];
-        kv_half_update<DT, D, DR>(s, dp, scale_log2, lse_l, dl_l, qh, qt * 64, h, grp, lane, key,
+        kv_half_update<DT, D, DR>(s, dp, scale_log2, lse_l, ndl_l, qh, qt * 64, h, grp, lane, key,
                                   bh, ax, q_lds, g_lds, dkt, dvt,
                                   [&](const uint16_t* t, int r0, int r1, int c0) {
                                     return lds_read_tr4x2_swz64(t, r0, r1, c0, lane);
