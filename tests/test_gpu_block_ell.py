@@ -340,6 +340,23 @@ def test_fwd_gelu_aux_outputs_bit_exact(dev, dtype, M):
     assert torch.equal(a, kb._bell_fwd(*args, True))
 
 
+@pytest.mark.parametrize("M", [0, 5])
+def test_forward_rejects_bad_bias_for_any_row_count(dev, M):
+    """A bias of the wrong length or dtype raises also when x has no rows (as the
+    kernel-launching case does), for both forward entry points."""
+    pat, X, V, _, b = data(max(M, 1), 2, 3, 2, torch.bfloat16, seed=7)
+    i = pat.device_index(dev)
+    x = X[:M].to(dev)
+    base = (x, V.to(dev), i["col_idx"], i["t_ptr"], i["t_row"], i["t_vblk"], i["order"])
+    for bad in (b[:-1].to(dev), b.to(dev, torch.float32)):
+        with pytest.raises(ValueError):
+            kb._bell_fwd(*base, bad, False)
+        with pytest.raises(ValueError):
+            kb._bell_fwd_gelu(*base, bad)
+    y, z = kb._bell_fwd_gelu(*base, b.to(dev))
+    assert y.shape == z.shape == (M, 3 * 64)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N", [(0, 64), (1, 64), (257, 192), (5000, 2560)])
 def test_gelu_bwd_and_bias_grad(dev, dtype, M, N):

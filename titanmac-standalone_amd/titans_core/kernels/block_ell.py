@@ -142,14 +142,14 @@ def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_pt
     if x.dtype != values.dtype:
         raise TypeError(f"bell_fwd: x dtype {x.dtype} != values dtype {values.dtype}")
     dev = _lib.require_device(x, values, t_ptr, what="bell_fwd")
+    if bias is not None:
+        if bias.shape != (N,) or bias.dtype != x.dtype:
+            raise ValueError(f"bell_fwd: bias must be [{N}] of {x.dtype}")
+        bias = bias.contiguous()
     x2, ldx = _rows(x, K)
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
-        if bias is not None:
-            if bias.shape != (N,) or bias.dtype != x.dtype:
-                raise ValueError(f"bell_fwd: bias must be [{N}] of {x.dtype}")
-            bias = bias.contiguous()
         with _lib.device_guard(dev):
             rc = _lib.lib().tmac_bell_fwd(
                 _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
@@ -185,15 +185,15 @@ def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
     if x.dtype != values.dtype:
         raise TypeError(f"bell_fwd_gelu: x dtype {x.dtype} != values dtype {values.dtype}")
     dev = _lib.require_device(x, values, t_ptr, what="bell_fwd_gelu")
+    if bias is not None:
+        if bias.shape != (N,) or bias.dtype != x.dtype:
+            raise ValueError(f"bell_fwd_gelu: bias must be [{N}] of {x.dtype}")
+        bias = bias.contiguous()
     x2, ldx = _rows(x, K)
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     z = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
-        if bias is not None:
-            if bias.shape != (N,) or bias.dtype != x.dtype:
-                raise ValueError(f"bell_fwd_gelu: bias must be [{N}] of {x.dtype}")
-            bias = bias.contiguous()
         with _lib.device_guard(dev):
             rc = _lib.lib().tmac_bell_fwd_gelu_aux(
                 _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
