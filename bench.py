@@ -15,6 +15,8 @@ The same run also times, as secondary figures:
     denominator of `attn_speedup_vs_dense`); also at the model-shaped S=4112
     (4096 tokens + 16 persistent) and with BlockSparseAttention's block-window
     mask (block 64);
+  - config 1 on the GPU: the fp32 WindowedAttention module (B=2, T=512, d=512, 8 heads,
+    w=256, Np=16; qkv GEMM -> fp32 tile kernel -> out GEMM), beside its CPU timing;
   - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
     masked bf16 backward (five bmm over the full S x S);
   - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40), and one
@@ -41,7 +43,7 @@ PyTorch paths of configs 1, 3 and 4 are timed on the CPU as secondary figures.
 roofline.traffic is measured by the run itself: two rocprofv3 counter passes (FETCH_SIZE,
 WRITE_SIZE) over `--mode traffic` of the current build, scaled by a plain 1 GiB copy.
 
-Modes (for profiling runs): all (default), spmm, attn, attn_bwd, attn_ex, dx, sddmm, bell_f32,
+Modes (for profiling runs): all (default), spmm, attn, attn_cfg1, attn_bwd, attn_ex, dx, sddmm, bell_f32,
 mlp_train, conv, norm, mac, mac_ttm, memupd, copy (a plain 1 GiB device copy, used to scale rocprofv3's FETCH_SIZE / WRITE_SIZE),
 traffic (the copy then the SpMM, three launches each: what the counter passes profile).
 """
@@ -234,6 +236,24 @@ def setup_attn(dev, S=None, pattern=None, block_size=64):
     bytes_ = 4 * bh * c["S"] * c["dh"] * 2
     return dict(launch=launch, flops=flops, bytes=bytes_, tokens=c["B"] * c["S"],
                 keep=(qkv, out, row_ptr, entries, order), q=q, k=k, v=v, fwd_args=args)
+
+
+def setup_attn_cfg1(dev):
+    """Config 1 on the GPU: the fp32 WindowedAttention module (qkv GEMM -> fp32 tile
+    kernel -> out GEMM) at B=2, T=512, d=512, 8 heads, w=256, Np=16, eval, the shape
+    cpu_secondary times on the host."""
+    from titans_core.attn.windowed_attention import WindowConfig, WindowedAttention
+    torch.manual_seed(1)
+    B1, T1, d1, H1 = 2, 512, 512, 8
+    mod = WindowedAttention(WindowConfig(window_size=256, num_heads=H1, head_dim=d1 // H1,
+                                         n_persistent=16)).to(dev).eval()
+    x = gen((B1, T1, d1), 1, dtype=torch.float32).to(dev)
+
+    def launch():
+        with torch.no_grad():
+            mod(x)
+
+    return dict(launch=launch, tokens=B1 * T1, keep=(mod, x))
 
 
 def setup_attn_bwd(dev, att):
@@ -747,7 +767,7 @@ def main() -> int:
                     help="with --mode attn_bwd: skip the dense baseline (profiling runs)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the rocprofv3 measurement of roofline.traffic (null)")
-    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_bwd", "attn_ex", "dx",
+    ap.add_argument("--mode", default="all", choices=["all", "spmm", "attn", "attn_cfg1", "attn_bwd", "attn_ex", "dx",
                                                      "bell_f32", "mlp_train",
                                                      "sddmm", "conv",
                                                      "norm", "mac", "mac_ttm", "memupd", "copy",
@@ -813,6 +833,11 @@ def main() -> int:
                 out["attn"][key] = dict(ms=ms_x, tokens_per_s=extra["tokens"] / ms_x * 1e3,
                                         tflops=extra["flops"] / ms_x / 1e9)
                 del extra
+    if args.mode in ("all", "attn_cfg1"):
+        wl = setup_attn_cfg1(dev)
+        ms = timed(wl["launch"], K, W, stream)
+        out["attn_cfg1"] = dict(ms=ms, tokens_per_s=wl["tokens"] / ms * 1e3)
+        del wl
     if args.mode in ("all", "attn_bwd"):
         bwd = setup_attn_bwd(dev, att)
         ms = timed(bwd["launch"], K, W, stream)
@@ -925,6 +950,8 @@ def main() -> int:
             "windowed_attn_fwd_s4112_tokens_per_s": round(a["s4112"]["tokens_per_s"], 1),
             "blocksparse_attn_fwd_blockwin_ms": round(a["blockwin"]["ms"], 5),
             "blocksparse_attn_fwd_blockwin_tflops_algorithmic": round(a["blockwin"]["tflops"], 3),
+            "windowed_attention_module_cfg1_fp32_ms": round(out["attn_cfg1"]["ms"], 5),
+            "windowed_attention_module_cfg1_fp32_tokens_per_s": round(out["attn_cfg1"]["tokens_per_s"], 1),
             "windowed_attn_bwd_ms": round(out["attn_bwd"]["ms"], 5),
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),

@@ -470,6 +470,189 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   if (lse) lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + log2f(l_run)) * kLn2;
 }
 
+// fp32 path on the matrix cores (no caller mask or dropout, head dimension 32
+// or 64): the structure of wattn_fwd_mfma_kernel with v_mfma_f32_32x32x2_f32
+// (fp32 products and sums). A workgroup of 4 waves owns 128 query rows, wave w
+// rows 32w..32w+31, and per listed 64-key tile:
+//   - Sᵀ = K·Qᵀ: an MFMA k-step sums two head dimensions, one per lane half
+//     (k-step s: dimension s in lanes 0-31, D/2 + s in lanes 32-63). Each lane
+//     holds the D/2 contiguous dimensions of its query row that its half
+//     needs, pre-multiplied by scale·log2e (B operand), and reads the same
+//     slice of a key row from LDS in 16-byte chunks (A operand);
+//   - masking and the online softmax as in the 16-bit kernel (same accumulator
+//     layout: lane = query row, keys 32kh + 8(j/4) + 4h + j%4);
+//   - Oᵀ += Vᵀ·Pᵀ with k-steps over key pairs: k-step s of key half kh takes
+//     key 32kh + 8(s/4) + 4h + s%4 in lane half h, where the Sᵀ accumulator
+//     left that lane's probability, so Pᵀ is used in place and Vᵀ is one
+//     4-byte LDS read per lane and k-step.
+// K and V tiles are staged with rows padded to D + 4 floats, double-buffered
+// with a register prefetch of the next tile.
+template <int D>
+__global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
+    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
+    int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
+    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
+  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr int kP = D + 4;           // row pitch, floats
+  constexpr int kTile = 64 * kP;      // one staged tile, floats
+  constexpr int kHalf = D / 2;        // Sᵀ k-steps; dimensions per lane
+  constexpr int kDt = D / 32;         // 32-wide dimension tiles of O
+  constexpr int kC4 = D / 4;          // 16-byte chunks per row
+  constexpr int kRpp = 256 / kC4;     // rows per staging pass
+  constexpr int kPasses = 64 / kRpp;  // staging passes per tile
+  // [buffer][K, V] 64 x D tiles
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTile];
+
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int q_row = qb * 128 + wave * 32 + l32;
+  const Span span = mask_row_span(mp, q_row);
+
+  const float* Kbh = K + b * ksb + hd * ksh;
+  const float* Vbh = V + b * vsb + hd * vsh;
+
+  float qf[kHalf];
+  {
+    const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss + h * kHalf;
+#pragma unroll
+    for (int c = 0; c < kHalf; c += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(qp + c);
+      qf[c] = v.x * scale_log2;
+      qf[c + 1] = v.y * scale_log2;
+      qf[c + 2] = v.z * scale_log2;
+      qf[c + 3] = v.w * scale_log2;
+    }
+  }
+  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+
+  // Staging: pass p moves row r0 + p * kRpp, chunk tid % kC4, of both tiles.
+  f32x4 pre[2 * kPasses];
+  const int r0 = tid / kC4, c4 = (tid % kC4) * 4;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int key = min(kt * 64 + r0 + p * kRpp, S - 1);  // rows past S: always masked
+      pre[p] = *reinterpret_cast<const f32x4*>(Kbh + key * kss + c4);
+      pre[kPasses + p] = *reinterpret_cast<const f32x4*>(Vbh + key * vss + c4);
+    }
+  };
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int off = (r0 + p * kRpp) * kP + c4;
+      *reinterpret_cast<f32x4*>(smem + (2 * buf) * kTile + off) = pre[p];
+      *reinterpret_cast<f32x4*>(smem + (2 * buf + 1) * kTile + off) = pre[kPasses + p];
+    }
+  };
+
+  f32x16 ot[kDt];
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt) ot[dt] = f32x16{};
+  constexpr float kTau = 8.f;  // lazy reference, as in the 16-bit kernel
+  float m_ref = -INFINITY, l_run = 0.f;
+
+  if (e0 < e1) {
+    gload(entries[e0] & 0xffff);
+    sstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int kt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    const bool more = e + 1 < e1;
+    if (more) gload(entries[e + 1] & 0xffff);
+
+    if (kind != 0) {
+      const float* kt_lds = smem + (2 * buf) * kTile;
+      const float* vt_lds = smem + (2 * buf + 1) * kTile;
+      f32x16 st[2];
+      st[0] = f32x16{};
+      st[1] = f32x16{};
+#pragma unroll
+      for (int c = 0; c < kHalf; c += 4) {
+        f32x4 a4[2];
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+          a4[kh] = *reinterpret_cast<const f32x4*>(kt_lds + (32 * kh + l32) * kP + h * kHalf + c);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+            st[kh] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[kh][t], qf[c + t], st[kh], 0, 0, 0);
+      }
+      // st[kh][j] = S[q_row][key]·scale·log2e, key = kt*64 + 32kh + 8(j/4) + 4h + j%4
+      if (kind == 2) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) apply_bits(st[kh], span_bits32(span, kt * 64 + 32 * kh + 4 * h));
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[kh][j]);
+      mx = xor32_max(mx);
+      const bool move = mx > m_ref + kTau;  // false while the row is fully masked
+      if (__builtin_amdgcn_ballot_w64(move)) {
+        const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mx) : 1.f;  // 0 from -inf
+        const float m_new = move ? mx : m_ref;
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kDt; ++dt) ot[dt] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+      float r4[4];
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const float p = __builtin_amdgcn_exp2f(st[kh][j] - m_use);
+          st[kh][j] = p;
+          r4[j & 3] = (kh == 0 && j < 4) ? p : r4[j & 3] + p;
+        }
+      l_run += xor32_add((r4[0] + r4[1]) + (r4[2] + r4[3]));
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+          const int key = 32 * kh + 8 * (s >> 2) + 4 * h + (s & 3);
+#pragma unroll
+          for (int dt = 0; dt < kDt; ++dt)
+            ot[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt_lds[key * kP + 32 * dt + l32], st[kh][s],
+                                                          ot[dt], 0, 0, 0);
+        }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if (q_row >= S) return;
+  const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
+  float* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
+  // ot[dt][j] = O[q_row][32dt + 8(j/4) + 4h + j%4]: four consecutive dimensions per j/4.
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg)
+      *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * jg + 4 * h) =
+          f32x4{ot[dt][4 * jg] * inv_l, ot[dt][4 * jg + 1] * inv_l, ot[dt][4 * jg + 2] * inv_l,
+                ot[dt][4 * jg + 3] * inv_l};
+  if (lse && h == 0)
+    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
+}
+
 // ---------------------------------------------------------------------------
 // Backward (16-bit MFMA path). With P = softmax(S) recomputed from the
 // forward's log-sum-exp, Δ = rowsum(dO ⊙ O):
@@ -1677,6 +1860,15 @@ template <int D, int FEAT>
 void launch_fwd(const AttnLaunch& a) {
   const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os;
   if (a.dtype == TMAC_F32) {
+    if constexpr (FEAT == 0 && D <= 64) {
+      hipLaunchKernelGGL((wattn_fwd_f32m_kernel<D>), dim3(a.grid_q), dim3(256), 0, a.s,
+                         static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
+                         static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
+                         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],
+                         os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order,
+                         a.wm_q);
+      return;
+    }
     hipLaunchKernelGGL((wattn_fwd_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s,
                        static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
                        static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
