@@ -1610,6 +1610,312 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
   }
 }
 
+// fp32 backward on the matrix cores (no caller mask or dropout, head dimension
+// 32 or 64; Δ from wattn_bwd_delta_f32_kernel). The layouts of
+// wattn_fwd_f32m_kernel: a v_mfma_f32_32x32x2_f32 k-step sums two head
+// dimensions, one per lane half, for the score-like products (each lane holds
+// the D/2 dimensions of its row that its half needs, the other operand comes
+// from LDS in 16-byte row chunks), and two keys or queries, one per lane half,
+// for the gradient products (the probability or dS the accumulator left in the
+// lane is the B operand in place; the staged tile gives a 4-byte read per lane).
+//
+// dQ: the forward's work list; wave w owns queries 32w..32w+31 of the
+// 128-query block, Q·scale·log2e and dO rows in registers. Per listed key tile
+// and 32-key half: Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ, P = exp2(Sᵀ − LSE·log2e),
+// dSᵀ = P ⊙ (dPᵀ − Δ), dQᵀ += Kᵀ·dSᵀ.
+template <int D>
+__global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
+    int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
+    int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
+    float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
+  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
+  constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTile];  // [buffer][K, V]
+
+  int bh, qb;
+  if (!work_item(wm, order, bh, qb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int q_row = qb * 128 + wave * 32 + l32;
+  const int qc = min(q_row, S - 1);
+  const Span span = mask_row_span(mp, q_row);
+
+  float qf[kHalf], gf[kHalf];
+  {
+    const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss + h * kHalf;
+    const float* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss + h * kHalf;
+#pragma unroll
+    for (int c = 0; c < kHalf; c += 4) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(qp + c);
+      const f32x4 w = *reinterpret_cast<const f32x4*>(gp + c);
+      qf[c] = v.x * scale_log2;
+      qf[c + 1] = v.y * scale_log2;
+      qf[c + 2] = v.z * scale_log2;
+      qf[c + 3] = v.w * scale_log2;
+      gf[c] = w.x;
+      gf[c + 1] = w.y;
+      gf[c + 2] = w.z;
+      gf[c + 3] = w.w;
+    }
+  }
+  const float l2 = lse_log2<false>(lse[static_cast<int64_t>(bh) * S + qc]);
+  const float dl = delta[static_cast<int64_t>(bh) * S + qc];
+  const float* Kbh = K + b * ksb + hd * ksh;
+  const float* Vbh = V + b * vsb + hd * vsh;
+  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+
+  f32x4 pre[2 * kPasses];
+  const int r0 = tid / kC4, c4 = (tid % kC4) * 4;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int key = min(kt * 64 + r0 + p * kRpp, S - 1);  // rows past S: always masked
+      pre[p] = *reinterpret_cast<const f32x4*>(Kbh + key * kss + c4);
+      pre[kPasses + p] = *reinterpret_cast<const f32x4*>(Vbh + key * vss + c4);
+    }
+  };
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int off = (r0 + p * kRpp) * kP + c4;
+      *reinterpret_cast<f32x4*>(smem + (2 * buf) * kTile + off) = pre[p];
+      *reinterpret_cast<f32x4*>(smem + (2 * buf + 1) * kTile + off) = pre[kPasses + p];
+    }
+  };
+
+  f32x16 dqt[kDt];
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt) dqt[dt] = f32x16{};
+  if (e0 < e1) {
+    gload(entries[e0] & 0xffff);
+    sstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int kt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    const bool more = e + 1 < e1;
+    if (more) gload(entries[e + 1] & 0xffff);
+    if (kind != 0) {
+      const float* kt_lds = smem + (2 * buf) * kTile;
+      const float* vt_lds = smem + (2 * buf + 1) * kTile;
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh) {
+        f32x16 st = f32x16{}, dpt = f32x16{};
+#pragma unroll
+        for (int c = 0; c < kHalf; c += 4) {
+          const f32x4 ka = *reinterpret_cast<const f32x4*>(kt_lds + (32 * kh + l32) * kP + h * kHalf + c);
+          const f32x4 va = *reinterpret_cast<const f32x4*>(vt_lds + (32 * kh + l32) * kP + h * kHalf + c);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            st = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], qf[c + t], st, 0, 0, 0);
+            dpt = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], gf[c + t], dpt, 0, 0, 0);
+          }
+        }
+        // st[j]: key kt*64 + 32kh + 8(j/4) + 4h + j%4 of this lane's query
+        if (kind == 2) apply_bits(st, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          st[j] = __builtin_amdgcn_exp2f(st[j] - l2) * (dpt[j] - dl);
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+          const int key = 32 * kh + 8 * (s >> 2) + 4 * h + (s & 3);
+#pragma unroll
+          for (int dt = 0; dt < kDt; ++dt)
+            dqt[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(kt_lds[key * kP + 32 * dt + l32], st[s],
+                                                           dqt[dt], 0, 0, 0);
+        }
+      }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  if (q_row >= S) return;
+  float* op = dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss;
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg)
+      *reinterpret_cast<f32x4*>(op + 32 * dt + 8 * jg + 4 * h) =
+          f32x4{dqt[dt][4 * jg] * scale, dqt[dt][4 * jg + 1] * scale, dqt[dt][4 * jg + 2] * scale,
+                dqt[dt][4 * jg + 3] * scale};
+}
+
+// dK, dV: the key-major work list; wave w owns keys 32w..32w+31 of the 128-key
+// block, K·scale·log2e and V rows in registers. Per listed query tile, Q, dO,
+// LSE·log2e and Δ of its 64 queries are staged in LDS; per 32-query half:
+// S = Q·Kᵀ and dP = dO·Vᵀ (lane = key, element j = query 32qh + 8(j/4) + 4h +
+// j%4), P = exp2(S − LSE·log2e), dS = P ⊙ (dP − Δ), dVᵀ += dOᵀ·P and
+// dKᵀ += Qᵀ·dS.
+template <int D>
+__global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
+    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
+    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
+    float* __restrict__ dK, float* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
+    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
+    int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
+    int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
+    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
+    const int32_t* __restrict__ order, WorkMap wm) {
+  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
+  constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
+  // [buffer][Q, dO] tiles, then [buffer][LSE·log2e, Δ] of the 64 queries
+  __shared__ __attribute__((aligned(16))) float smem[4 * kTile];
+  __shared__ __attribute__((aligned(16))) float stat[2][2][64];
+
+  int bh, kb;
+  if (!work_item(wm, order, bh, kb)) return;
+  const int b = bh / H, hd = bh - b * H;
+  const int S = mp.S;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int key = kb * 128 + wave * 32 + l32;
+  const int kc = min(key, S - 1);
+  const Span span = mask_col_span(mp, key);
+
+  float kf[kHalf], vf[kHalf];
+  {
+    const float* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + h * kHalf;
+    const float* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + h * kHalf;
+#pragma unroll
+    for (int c = 0; c < kHalf; c += 4) {
+      const f32x4 a = *reinterpret_cast<const f32x4*>(kp + c);
+      const f32x4 w = *reinterpret_cast<const f32x4*>(vp + c);
+      kf[c] = a.x * scale_log2;
+      kf[c + 1] = a.y * scale_log2;
+      kf[c + 2] = a.z * scale_log2;
+      kf[c + 3] = a.w * scale_log2;
+      vf[c] = w.x;
+      vf[c + 1] = w.y;
+      vf[c + 2] = w.z;
+      vf[c + 3] = w.w;
+    }
+  }
+  const float* Qbh = Q + b * qsb + hd * qsh;
+  const float* Gbh = dO + b * gsb + hd * gsh;
+  const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
+  const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
+  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+
+  f32x4 pre[2 * kPasses];
+  float st_pre = 0.f;
+  const int r0 = tid / kC4, c4 = (tid % kC4) * 4;
+  auto gload = [&](int qt) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int qr = min(qt * 64 + r0 + p * kRpp, S - 1);  // rows past S: always masked
+      pre[p] = *reinterpret_cast<const f32x4*>(Qbh + qr * qss + c4);
+      pre[kPasses + p] = *reinterpret_cast<const f32x4*>(Gbh + qr * gss + c4);
+    }
+    // LSE (threads 0-63) and Δ (64-127) of the tile's queries
+    st_pre = ((tid & 64) ? dl_bh : lse_bh)[min(qt * 64 + (tid & 63), S - 1)];
+  };
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int off = (r0 + p * kRpp) * kP + c4;
+      *reinterpret_cast<f32x4*>(smem + (2 * buf) * kTile + off) = pre[p];
+      *reinterpret_cast<f32x4*>(smem + (2 * buf + 1) * kTile + off) = pre[kPasses + p];
+    }
+    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<false>(st_pre) : st_pre;
+  };
+
+  f32x16 dkt[kDt], dvt[kDt];
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt) {
+    dkt[dt] = f32x16{};
+    dvt[dt] = f32x16{};
+  }
+  if (e0 < e1) {
+    gload(entries[e0] & 0xffff);
+    sstore(0);
+  }
+  __syncthreads();
+  int buf = 0;
+  for (int e = e0; e < e1; ++e) {
+    const int ent = entries[e];
+    const int qt = ent & 0xffff;
+    const int kind = (ent >> (16 + 2 * wave)) & 3;
+    const bool more = e + 1 < e1;
+    if (more) gload(entries[e + 1] & 0xffff);
+    if (kind != 0) {
+      const float* q_lds = smem + (2 * buf) * kTile;
+      const float* g_lds = smem + (2 * buf + 1) * kTile;
+      const float* l2_l = &stat[buf][0][0];
+      const float* dl_l = &stat[buf][1][0];
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int c = 0; c < kHalf; c += 4) {
+          const f32x4 qa = *reinterpret_cast<const f32x4*>(q_lds + (32 * qh + l32) * kP + h * kHalf + c);
+          const f32x4 ga = *reinterpret_cast<const f32x4*>(g_lds + (32 * qh + l32) * kP + h * kHalf + c);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            s = __builtin_amdgcn_mfma_f32_32x32x2f32(qa[t], kf[c + t], s, 0, 0, 0);
+            dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga[t], vf[c + t], dp, 0, 0, 0);
+          }
+        }
+        // s[j]: query qt*64 + 32qh + 8(j/4) + 4h + j%4 of this lane's key
+        if (kind == 2) apply_bits(s, span_bits32(span, qt * 64 + 32 * qh + 4 * h));
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2_l + 32 * qh + 8 * g + 4 * h);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl_l + 32 * qh + 8 * g + 4 * h);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float pj = __builtin_amdgcn_exp2f(s[4 * g + t] - l4[t]);
+            s[4 * g + t] = pj;
+            dp[4 * g + t] = pj * (dp[4 * g + t] - d4[t]);
+          }
+        }
+#pragma unroll
+        for (int k2 = 0; k2 < 16; ++k2) {
+          const int qr = 32 * qh + 8 * (k2 >> 2) + 4 * h + (k2 & 3);
+#pragma unroll
+          for (int dt = 0; dt < kDt; ++dt) {
+            dvt[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(g_lds[qr * kP + 32 * dt + l32], s[k2],
+                                                           dvt[dt], 0, 0, 0);
+            dkt[dt] = __builtin_amdgcn_mfma_f32_32x32x2f32(q_lds[qr * kP + 32 * dt + l32], dp[k2],
+                                                           dkt[dt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  if (key >= S) return;
+  float* dkp = dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss;
+  float* dvp = dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss;
+  // dkt[dt][j] = dKᵀ[32dt + 8(j/4) + 4h + j%4][key]: four consecutive dimensions per j/4
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+    for (int jg = 0; jg < 4; ++jg) {
+      const int d0 = 32 * dt + 8 * jg + 4 * h;
+      *reinterpret_cast<f32x4*>(dkp + d0) =
+          f32x4{dkt[dt][4 * jg] * scale, dkt[dt][4 * jg + 1] * scale, dkt[dt][4 * jg + 2] * scale,
+                dkt[dt][4 * jg + 3] * scale};
+      *reinterpret_cast<f32x4*>(dvp + d0) =
+          f32x4{dvt[dt][4 * jg], dvt[dt][4 * jg + 1], dvt[dt][4 * jg + 2], dvt[dt][4 * jg + 3]};
+    }
+}
+
 // Work lists of a caller's mask (kFeatMask), built on the device in two launches.
 //
 // 1. wattn_mask_kinds_kernel: one workgroup per (mask row mr, 128x128 square
@@ -1941,6 +2247,19 @@ void launch_bwd_f32(const AttnLaunch& a) {
   const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);
   hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
                      a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
+  if constexpr (FEAT == 0 && D <= 64) {
+    hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K, V,
+                       G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
+                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
+                       a.scale_log2, a.col_ptr, a.entries_kv, a.order_kv, a.wm_kv);
+    hipLaunchKernelGGL((wattn_bwd_q_f32m_kernel<D>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V, G,
+                       a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+                       ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
+                       dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
+                       a.wm_q);
+    return;
+  }
   hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
                      V, G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
                      qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
