@@ -16,7 +16,8 @@ The same run also times, as secondary figures:
     (4096 tokens + 16 persistent) and with BlockSparseAttention's block-window
     mask (block 64);
   - config 1 on the GPU: the fp32 WindowedAttention module (B=2, T=512, d=512, 8 heads,
-    w=256, Np=16; qkv GEMM -> fp32 tile kernel -> out GEMM), beside its CPU timing;
+    w=256, Np=16; qkv GEMM -> fp32 tile kernel -> out GEMM), beside its CPU timing, and
+    its forward + backward;
   - the windowed attention backward (dQ, dK, dV) of config 3, against a dense
     masked bf16 backward (five bmm over the full S x S);
   - Block-ELL dX and dW-SDDMM of config 4 (M=32768, W [640, 2560], width 20 of 40), and one
@@ -248,12 +249,17 @@ def setup_attn_cfg1(dev):
     mod = WindowedAttention(WindowConfig(window_size=256, num_heads=H1, head_dim=d1 // H1,
                                          n_persistent=16)).to(dev).eval()
     x = gen((B1, T1, d1), 1, dtype=torch.float32).to(dev)
+    xg = x.clone().requires_grad_(True)
+    gy = gen((B1, T1, d1), 2, dtype=torch.float32).to(dev)
 
     def launch():
         with torch.no_grad():
             mod(x)
 
-    return dict(launch=launch, tokens=B1 * T1, keep=(mod, x))
+    def train():  # forward + backward (input and weight gradients)
+        mod(xg).backward(gy)
+
+    return dict(launch=launch, train=train, tokens=B1 * T1, keep=(mod, x, xg, gy))
 
 
 def setup_attn_bwd(dev, att):
@@ -836,7 +842,8 @@ def main() -> int:
     if args.mode in ("all", "attn_cfg1"):
         wl = setup_attn_cfg1(dev)
         ms = timed(wl["launch"], K, W, stream)
-        out["attn_cfg1"] = dict(ms=ms, tokens_per_s=wl["tokens"] / ms * 1e3)
+        out["attn_cfg1"] = dict(ms=ms, tokens_per_s=wl["tokens"] / ms * 1e3,
+                                train_ms=timed(wl["train"], K, W, stream))
         del wl
     if args.mode in ("all", "attn_bwd"):
         bwd = setup_attn_bwd(dev, att)
@@ -952,6 +959,7 @@ def main() -> int:
             "blocksparse_attn_fwd_blockwin_tflops_algorithmic": round(a["blockwin"]["tflops"], 3),
             "windowed_attention_module_cfg1_fp32_ms": round(out["attn_cfg1"]["ms"], 5),
             "windowed_attention_module_cfg1_fp32_tokens_per_s": round(out["attn_cfg1"]["tokens_per_s"], 1),
+            "windowed_attention_module_cfg1_fp32_fwd_bwd_ms": round(out["attn_cfg1"]["train_ms"], 5),
             "windowed_attn_bwd_ms": round(out["attn_bwd"]["ms"], 5),
             "windowed_attn_bwd_tflops_algorithmic": round(out["attn_bwd"]["tflops"], 3),
             "dense_masked_bwd_bmm_ms": round(out["attn_bwd"]["dense_bwd_ms"], 4),
