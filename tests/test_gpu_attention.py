@@ -53,8 +53,9 @@ def test_attention_parity_16bit(dev, dtype, B, H, S, w, Np, causal, pattern, bs)
     close(o.float().cpu(), ref)
 
 
-@pytest.mark.parametrize("B,H,S,w,Np,causal,pattern,bs", GRID[:12:2] + GRID[12:13])
+@pytest.mark.parametrize("B,H,S,w,Np,causal,pattern,bs", GRID)
 def test_attention_parity_fp32(dev, B, H, S, w, Np, causal, pattern, bs):
+    """fp32 path (fp32 MFMA kernel): within 1e-4 of the largest output entry."""
     q, k, v = qkv((B, H, S, 64), torch.float32, seed=7 * S + w)
     o = windowed_attention(q.to(dev), k.to(dev), v.to(dev), w, Np, causal, pattern, bs)
     mask = om.make_mask(S, w, Np, causal, pattern, bs)
