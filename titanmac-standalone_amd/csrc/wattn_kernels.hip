@@ -354,7 +354,8 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
     lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
 }
 
-// fp32 path: one query row per thread, 128 rows per workgroup (2 waves). FEAT
+// fp32 path at head dimension 128 (32 and 64 take wattn_fwd_f32m_kernel): one
+// query row per thread, 128 rows per workgroup (2 waves), FMA arithmetic. FEAT
 // as for the MFMA kernel.
 template <int D, int FEAT = 0>
 __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
@@ -470,8 +471,8 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
   if (lse) lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + log2f(l_run)) * kLn2;
 }
 
-// fp32 path on the matrix cores (no caller mask or dropout, head dimension 32
-// or 64): the structure of wattn_fwd_mfma_kernel with v_mfma_f32_32x32x2_f32
+// fp32 path on the matrix cores (head dimension 32 or 64): the structure of
+// wattn_fwd_mfma_kernel with v_mfma_f32_32x32x2_f32
 // (fp32 products and sums). A workgroup of 4 waves owns 128 query rows, wave w
 // rows 32w..32w+31, and per listed 64-key tile:
 //   - Sᵀ = K·Qᵀ: an MFMA k-step sums two head dimensions, one per lane half
@@ -486,16 +487,20 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 //     left that lane's probability, so Pᵀ is used in place and Vᵀ is one
 //     4-byte LDS read per lane and k-step.
 // K and V tiles are staged with rows padded to D + 4 floats, double-buffered
-// with a register prefetch of the next tile.
-template <int D>
+// with a register prefetch of the next tile. FEAT as for the 16-bit kernel: the
+// caller's mask from its device work lists (scores in log2 units, partial slices
+// from the allowed-pair bits or the mask's bias), dropout factors on the P·V
+// operand while the row sum takes the undropped probabilities.
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
   static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4;           // row pitch, floats
   constexpr int kTile = 64 * kP;      // one staged tile, floats
   constexpr int kHalf = D / 2;        // Sᵀ k-steps; dimensions per lane
@@ -532,7 +537,17 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
       qf[c + 3] = v.w * scale_log2;
     }
   }
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1, mrow = 0;
+  if constexpr (CM) {
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
+  uint64_t wb = 0, wb_next = 0;  // caller's mask: this row's allowed-key bits, two tiles
 
   // Staging: pass p moves row r0 + p * kRpp, chunk tid % kC4, of both tiles.
   f32x4 pre[2 * kPasses];
@@ -562,6 +577,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
 
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -571,7 +587,10 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, q_row, entries[e + 1] & 0xffff, S);
+    }
 
     if (kind != 0) {
       const float* kt_lds = smem + (2 * buf) * kTile;
@@ -592,7 +611,21 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
             st[kh] = __builtin_amdgcn_mfma_f32_32x32x2f32(a4[kh][t], qf[c + t], st[kh], 0, 0, 0);
       }
       // st[kh][j] = S[q_row][key]·scale·log2e, key = kt*64 + 32kh + 8(j/4) + 4h + j%4
-      if (kind == 2) {
+      if constexpr (CM) {
+        if (kind == 2) {
+          const uint64_t w = wb >> (4 * h);
+          apply_bits(st[0], static_cast<uint32_t>(w));
+          apply_bits(st[1], static_cast<uint32_t>(w >> 32));
+        } else if (kind == 3) {
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+              st[kh][j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
+            }
+        }
+      } else if (kind == 2) {
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) apply_bits(st[kh], span_bits32(span, kt * 64 + 32 * kh + 4 * h));
       }
@@ -622,6 +655,18 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
           r4[j & 3] = (kh == 0 && j < 4) ? p : r4[j & 3] + p;
         }
       l_run += xor32_add((r4[0] + r4[1]) + (r4[2] + r4[3]));
+      if constexpr (DR) {
+        // P ⊙ Z for O: the factors of four consecutive keys per draw
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float z4[4];
+            drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * g + 4 * h, z4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) st[kh][4 * g + t] *= z4[t];
+          }
+      }
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -634,6 +679,7 @@ __global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
         }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -1342,8 +1388,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
   store_row<DT, T::kDt>(dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss, dqt, scale, h);
 }
 
-// fp32 backward (FMA path, for fp32 modules). Δ[b, h, q] = Σ_d dO · O, D/8
-// lanes per row (eight elements each).
+// fp32 backward. Δ[b, h, q] = Σ_d dO · O, D/8 lanes per row (eight elements
+// each), for every head dimension.
 template <int D>
 __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
     const float* __restrict__ O, const float* __restrict__ dO, float* __restrict__ delta,
@@ -1371,7 +1417,8 @@ __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
   if (row < n_rows && ch == 0) delta[row] = acc;
 }
 
-// fp32 dQ: one query row per thread (128 per workgroup, the forward's work
+// fp32 dQ at head dimension 128 (FMA; 32 and 64 take the matrix-core kernels
+// below): one query row per thread (128 per workgroup, the forward's work
 // list); K and V tiles staged in LDS and read as broadcasts.
 template <int D, int FEAT = 0>
 __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
@@ -1480,7 +1527,8 @@ __global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
         f32x4{dq[d] * scale, dq[d + 1] * scale, dq[d + 2] * scale, dq[d + 3] * scale};
 }
 
-// fp32 dK, dV: two lanes per key (lane and lane + 32 hold head dims 0..D/2-1
+// fp32 dK, dV at head dimension 128 (FMA; 32 and 64 take the matrix-core
+// kernels below): two lanes per key (lane and lane + 32 hold head dims 0..D/2-1
 // and D/2..D-1), 32 keys per wave, 128 per workgroup (the key-major work
 // list); Q, dO, LSE and Δ of each listed 64-query tile staged in LDS.
 template <int D, int FEAT = 0>
@@ -1610,8 +1658,8 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
   }
 }
 
-// fp32 backward on the matrix cores (no caller mask or dropout, head dimension
-// 32 or 64; Δ from wattn_bwd_delta_f32_kernel). The layouts of
+// fp32 backward on the matrix cores (head dimension 32 or 64; Δ from
+// wattn_bwd_delta_f32_kernel; FEAT as for the 16-bit kernels). The layouts of
 // wattn_fwd_f32m_kernel: a v_mfma_f32_32x32x2_f32 k-step sums two head
 // dimensions, one per lane half, for the score-like products (each lane holds
 // the D/2 dimensions of its row that its half needs, the other operand comes
@@ -1622,8 +1670,8 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
 // dQ: the forward's work list; wave w owns queries 32w..32w+31 of the
 // 128-query block, Q·scale·log2e and dO rows in registers. Per listed key tile
 // and 32-key half: Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ, P = exp2(Sᵀ − LSE·log2e),
-// dSᵀ = P ⊙ (dPᵀ − Δ), dQᵀ += Kᵀ·dSᵀ.
-template <int D>
+// dSᵀ = P ⊙ (dPᵀ − Δ) (with dropout P ⊙ (Z ⊙ dPᵀ − Δ)), dQᵀ += Kᵀ·dSᵀ.
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -1631,8 +1679,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
     int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
   static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
   constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
   __shared__ __attribute__((aligned(16))) float smem[4 * kTile];  // [buffer][K, V]
@@ -1666,11 +1715,21 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
       gf[c + 3] = w.w;
     }
   }
-  const float l2 = lse_log2<false>(lse[static_cast<int64_t>(bh) * S + qc]);
+  const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + qc]);
   const float dl = delta[static_cast<int64_t>(bh) * S + qc];
   const float* Kbh = K + b * ksb + hd * ksh;
   const float* Vbh = V + b * vsb + hd * vsh;
-  const int e0 = row_ptr[qb], e1 = row_ptr[qb + 1];
+  int e0, e1, mrow = 0;
+  if constexpr (CM) {
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + qb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = row_ptr[qb];
+    e1 = row_ptr[qb + 1];
+  }
+  uint64_t wb = 0, wb_next = 0;  // caller's mask: this row's allowed-key bits, two tiles
 
   f32x4 pre[2 * kPasses];
   const int r0 = tid / kC4, c4 = (tid % kC4) * 4;
@@ -1696,6 +1755,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
   for (int dt = 0; dt < kDt; ++dt) dqt[dt] = f32x16{};
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -1705,7 +1765,10 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, q_row, entries[e + 1] & 0xffff, S);
+    }
     if (kind != 0) {
       const float* kt_lds = smem + (2 * buf) * kTile;
       const float* vt_lds = smem + (2 * buf + 1) * kTile;
@@ -1723,10 +1786,33 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
           }
         }
         // st[j]: key kt*64 + 32kh + 8(j/4) + 4h + j%4 of this lane's query
-        if (kind == 2) apply_bits(st, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
+        if constexpr (CM) {
+          if (kind == 2) {
+            apply_bits(st, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * kh)));
+          } else if (kind == 3) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-          st[j] = __builtin_amdgcn_exp2f(st[j] - l2) * (dpt[j] - dl);
+            for (int j = 0; j < 16; ++j) {
+              const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
+              st[j] += mask_bias(ax, b, hd, q_row, key, S) * kLog2e;
+            }
+          }
+        } else if (kind == 2) {
+          apply_bits(st, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
+        }
+        if constexpr (DR) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float z4[4];
+            drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * g + 4 * h, z4);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              st[4 * g + t] = __builtin_amdgcn_exp2f(st[4 * g + t] - l2) * (z4[t] * dpt[4 * g + t] - dl);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 16; ++j)
+            st[j] = __builtin_amdgcn_exp2f(st[j] - l2) * (dpt[j] - dl);
+        }
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
           const int key = 32 * kh + 8 * (s >> 2) + 4 * h + (s & 3);
@@ -1738,6 +1824,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
       }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -1757,8 +1844,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
 // LSE·log2e and Δ of its 64 queries are staged in LDS; per 32-query half:
 // S = Q·Kᵀ and dP = dO·Vᵀ (lane = key, element j = query 32qh + 8(j/4) + 4h +
 // j%4), P = exp2(S − LSE·log2e), dS = P ⊙ (dP − Δ), dVᵀ += dOᵀ·P and
-// dKᵀ += Qᵀ·dS.
-template <int D>
+// dKᵀ += Qᵀ·dS; with dropout dV takes P ⊙ Z and dS = P ⊙ (Z ⊙ dP − Δ).
+template <int D, int FEAT = 0>
 __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -1767,8 +1854,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
     int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm) {
+    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
   static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
   constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
   // [buffer][Q, dO] tiles, then [buffer][LSE·log2e, Δ] of the 64 queries
@@ -1808,7 +1896,17 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
   const float* Gbh = dO + b * gsb + hd * gsh;
   const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
   const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
-  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  int e0, e1, mrow = 0;
+  if constexpr (CM) {
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + kb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = col_ptr[kb];
+    e1 = col_ptr[kb + 1];
+  }
+  uint64_t wb = 0, wb_next = 0;  // caller's mask: allowed-query bits of this key, two tiles
 
   f32x4 pre[2 * kPasses];
   float st_pre = 0.f;
@@ -1830,7 +1928,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
       *reinterpret_cast<f32x4*>(smem + (2 * buf) * kTile + off) = pre[p];
       *reinterpret_cast<f32x4*>(smem + (2 * buf + 1) * kTile + off) = pre[kPasses + p];
     }
-    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<false>(st_pre) : st_pre;
+    if (tid < 128) stat[buf][tid >> 6][tid & 63] = tid < 64 ? lse_log2<CM>(st_pre) : st_pre;
   };
 
   f32x16 dkt[kDt], dvt[kDt];
@@ -1841,6 +1939,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
   }
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
+    if constexpr (CM) wb = mask_word(ax, mrow, key, entries[e0] & 0xffff, S);
     sstore(0);
   }
   __syncthreads();
@@ -1850,7 +1949,10 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
     const int qt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) gload(entries[e + 1] & 0xffff);
+    if (more) {
+      gload(entries[e + 1] & 0xffff);
+      if constexpr (CM) wb_next = mask_word(ax, mrow, key, entries[e + 1] & 0xffff, S);
+    }
     if (kind != 0) {
       const float* q_lds = smem + (2 * buf) * kTile;
       const float* g_lds = smem + (2 * buf + 1) * kTile;
@@ -1870,16 +1972,36 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
           }
         }
         // s[j]: query qt*64 + 32qh + 8(j/4) + 4h + j%4 of this lane's key
-        if (kind == 2) apply_bits(s, span_bits32(span, qt * 64 + 32 * qh + 4 * h));
+        if constexpr (CM) {
+          if (kind == 2) {
+            apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
+          } else if (kind == 3) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
+              s[j] += mask_bias(ax, b, hd, qr, key, S) * kLog2e;
+            }
+          }
+        } else if (kind == 2) {
+          apply_bits(s, span_bits32(span, qt * 64 + 32 * qh + 4 * h));
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2_l + 32 * qh + 8 * g + 4 * h);
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl_l + 32 * qh + 8 * g + 4 * h);
+          uint32_t kq = 0;
+          if constexpr (DR) kq = keep_quad(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h, key, lane & 3);
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float pj = __builtin_amdgcn_exp2f(s[4 * g + t] - l4[t]);
-            s[4 * g + t] = pj;
-            dp[4 * g + t] = pj * (dp[4 * g + t] - d4[t]);
+            if constexpr (DR) {
+              const float z = ((kq >> (4 * t)) & 1u) ? ax.keep_scale : 0.f;
+              s[4 * g + t] = pj * z;
+              dp[4 * g + t] = pj * (z * dp[4 * g + t] - d4[t]);
+            } else {
+              s[4 * g + t] = pj;
+              dp[4 * g + t] = pj * (dp[4 * g + t] - d4[t]);
+            }
           }
         }
 #pragma unroll
@@ -1896,6 +2018,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
       }
     }
     if (more) sstore(buf ^ 1);
+    if constexpr (CM) wb = wb_next;
     __syncthreads();
     buf ^= 1;
   }
@@ -2166,21 +2289,21 @@ template <int D, int FEAT>
 void launch_fwd(const AttnLaunch& a) {
   const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os;
   if (a.dtype == TMAC_F32) {
-    if constexpr (FEAT == 0 && D <= 64) {
-      hipLaunchKernelGGL((wattn_fwd_f32m_kernel<D>), dim3(a.grid_q), dim3(256), 0, a.s,
+    if constexpr (D <= 64) {
+      hipLaunchKernelGGL((wattn_fwd_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s,
                          static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
                          static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
                          qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],
                          os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order,
-                         a.wm_q);
-      return;
+                         a.wm_q, a.ax_q);
+    } else {  // head dimension 128: one thread per query row (FMA)
+      hipLaunchKernelGGL((wattn_fwd_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s,
+                         static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
+                         static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
+                         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],
+                         os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order,
+                         a.wm_q, a.ax_q);
     }
-    hipLaunchKernelGGL((wattn_fwd_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s,
-                       static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
-                       static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
-                       os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order, a.wm_q,
-                       a.ax_q);
   } else if (a.dtype == TMAC_BF16) {
     hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16, D, FEAT>), dim3(a.grid_q), dim3(256), 0,
                        a.s, static_cast<const uint16_t*>(a.Q), static_cast<const uint16_t*>(a.K),
@@ -2247,29 +2370,31 @@ void launch_bwd_f32(const AttnLaunch& a) {
   const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);
   hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
                      a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
-  if constexpr (FEAT == 0 && D <= 64) {
-    hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K, V,
-                       G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
-                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
-                       gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
-                       a.scale_log2, a.col_ptr, a.entries_kv, a.order_kv, a.wm_kv);
-    hipLaunchKernelGGL((wattn_bwd_q_f32m_kernel<D>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V, G,
-                       a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+  if constexpr (D <= 64) {
+    hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
+                       K, V, G, a.lse, a.delta, static_cast<float*>(a.dK),
+                       static_cast<float*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],
+                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],
+                       dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
+                       a.order_kv, a.wm_kv, a.ax_kv);
+    hipLaunchKernelGGL((wattn_bwd_q_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K,
+                       V, G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
                        ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
                        dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
-                       a.wm_q);
-    return;
+                       a.wm_q, a.ax_q);
+  } else {  // head dimension 128: FMA kernels (two lanes per key; one thread per query)
+    hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
+                       K, V, G, a.lse, a.delta, static_cast<float*>(a.dK),
+                       static_cast<float*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],
+                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],
+                       dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
+                       a.order_kv, a.wm_kv, a.ax_kv);
+    hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s, Q, K,
+                       V, G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+                       ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
+                       dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
+                       a.wm_q, a.ax_q);
   }
-  hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
-                     V, G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
-                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
-                     gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
-                     a.scale_log2, a.col_ptr, a.entries_kv, a.order_kv, a.wm_kv, a.ax_kv);
-  hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s, Q, K, V,
-                     G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
-                     ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
-                     dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
-                     a.wm_q, a.ax_q);
 }
 
 template <int FEAT>
