@@ -24,9 +24,8 @@
 //      through ds_read_b64_tr_b16 in the same permuted key order.
 // The output keeps one query row per lane, so normalisation needs no exchange.
 //
-// fp32 path: the exact-precision variant used by fp32 modules. One thread per
-// query row (128 rows per workgroup), K/V tiles staged in LDS as fp32, plain
-// FMA arithmetic, same work list and the same online softmax.
+// fp32 path (fp32 modules): the same structure on v_mfma_f32_32x32x2_f32,
+// fp32 products and sums (wattn_fwd_f32m_kernel).
 
 #include <math.h>
 
@@ -354,124 +353,7 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
     lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
 }
 
-// fp32 path at head dimension 128 (32 and 64 take wattn_fwd_f32m_kernel): one
-// query row per thread, 128 rows per workgroup (2 waves), FMA arithmetic. FEAT
-// as for the MFMA kernel.
-template <int D, int FEAT = 0>
-__global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
-    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
-    int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
-    const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
-  __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
-  __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
-
-  int bh, qb;
-  if (!work_item(wm, order, bh, qb)) return;
-  const int b = bh / H, hd = bh - b * H;
-  const int S = mp.S;
-  const int tid = threadIdx.x;
-  const int q_row = qb * 128 + tid;
-  const int sub = tid >> 5;  // 32-row slice of this thread
-  const Span span = mask_row_span(mp, q_row);
-
-  float q[D], o[D];
-  {
-    const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss;
-#pragma unroll
-    for (int d = 0; d < D; d += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(qp + d);
-      q[d] = v.x * scale_log2;
-      q[d + 1] = v.y * scale_log2;
-      q[d + 2] = v.z * scale_log2;
-      q[d + 3] = v.w * scale_log2;
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d) o[d] = 0.f;
-  float m_run = -INFINITY, l_run = 0.f;
-
-  const float* Kbh = K + b * ksb + hd * ksh;
-  const float* Vbh = V + b * vsb + hd * vsh;
-  int e0, e1;
-  if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
-    e0 = row * ax.cap;
-    e1 = e0 + ax.cnt[row];
-  } else {
-    e0 = row_ptr[qb];
-    e1 = row_ptr[qb + 1];
-  }
-  for (int e = e0; e < e1; ++e) {
-    const int ent = entries[e];
-    const int kt = ent & 0xffff;
-    __syncthreads();
-    // 64 rows x D/4 chunks of 16 bytes per tile.
-    for (int c = tid; c < 64 * (D / 4); c += 128) {
-      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-      const int key = min(kt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(kt_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Kbh + key * kss + col);
-      *reinterpret_cast<f32x4*>(vt_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Vbh + key * vss + col);
-    }
-    __syncthreads();
-    const int kind = (ent >> (16 + 2 * sub)) & 3;
-    if (kind == 0) continue;
-    float s[64];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      float acc = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) acc = fmaf(q[d], kt_lds[j * D + d], acc);
-      if constexpr (CM) {
-        if (kind >= 2) acc += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
-      } else {
-        if (kind == 2 && !span_has(span, kt * 64 + j)) acc = -INFINITY;
-      }
-      s[j] = acc;
-      mx = fmaxf(mx, acc);
-    }
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    l_run *= alpha;
-#pragma unroll
-    for (int d = 0; d < D; ++d) o[d] *= alpha;
-    // dropout: keep bits of the tile's 64 keys, drawn before the unrolled loop
-    uint64_t keep = ~0ull;
-    if constexpr (DR) {
-      keep = 0;
-#pragma unroll 1
-      for (int g = 0; g < 16; ++g)
-        keep |= static_cast<uint64_t>(keep4(ax, bh, q_row, kt * 64 + 4 * g)) << (4 * g);
-    }
-#pragma unroll
-    for (int j = 0; j < 64; ++j) {
-      const float pj = exp2f(s[j] - m_use);
-      l_run += pj;
-      float pv = pj;
-      if constexpr (DR) pv = ((keep >> j) & 1) ? pj * ax.keep_scale : 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) o[d] = fmaf(pv, vt_lds[j * D + d], o[d]);
-    }
-    m_run = m_new;
-  }
-  if (q_row >= S) return;
-  const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
-  float* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
-#pragma unroll
-  for (int d = 0; d < D; d += 4)
-    *reinterpret_cast<f32x4*>(op + d) =
-        f32x4{o[d] * inv_l, o[d + 1] * inv_l, o[d + 2] * inv_l, o[d + 3] * inv_l};
-  if (lse) lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_run + log2f(l_run)) * kLn2;
-}
-
-// fp32 path on the matrix cores (head dimension 32 or 64): the structure of
+// fp32 path on the matrix cores (head dimension 32, 64 or 128): the structure of
 // wattn_fwd_mfma_kernel with v_mfma_f32_32x32x2_f32
 // (fp32 products and sums). A workgroup of 4 waves owns 128 query rows, wave w
 // rows 32w..32w+31, and per listed 64-key tile:
@@ -487,19 +369,20 @@ __global__ __launch_bounds__(128) void wattn_fwd_f32_kernel(
 //     left that lane's probability, so Pᵀ is used in place and Vᵀ is one
 //     4-byte LDS read per lane and k-step.
 // K and V tiles are staged with rows padded to D + 4 floats, double-buffered
-// with a register prefetch of the next tile. FEAT as for the 16-bit kernel: the
+// with a register prefetch of the next tile (two workgroups per CU; one at head
+// dimension 128, where LDS and the register file hold one). FEAT as for the 16-bit kernel: the
 // caller's mask from its device work lists (scores in log2 units, partial slices
 // from the allowed-pair bits or the mask's bias), dropout factors on the P·V
 // operand while the row sum takes the undropped probabilities.
 template <int D, int FEAT = 0>
-__global__ __launch_bounds__(256, 2) void wattn_fwd_f32m_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_fwd_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     float* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
     int64_t osh, int64_t oss, int H, MaskParams mp, float scale_log2,
     const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  static_assert(D == 32 || D == 64 || D == 128, "head dimension 32, 64 or 128");
   constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4;           // row pitch, floats
   constexpr int kTile = 64 * kP;      // one staged tile, floats
@@ -1417,248 +1300,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_delta_f32_kernel(
   if (row < n_rows && ch == 0) delta[row] = acc;
 }
 
-// fp32 dQ at head dimension 128 (FMA; 32 and 64 take the matrix-core kernels
-// below): one query row per thread (128 per workgroup, the forward's work
-// list); K and V tiles staged in LDS and read as broadcasts.
-template <int D, int FEAT = 0>
-__global__ __launch_bounds__(128) void wattn_bwd_q_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
-    int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb, int64_t gsh, int64_t gss,
-    int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
-    float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
-  __shared__ __attribute__((aligned(16))) float kt_lds[64 * D];
-  __shared__ __attribute__((aligned(16))) float vt_lds[64 * D];
-
-  int bh, qb;
-  if (!work_item(wm, order, bh, qb)) return;
-  const int b = bh / H, hd = bh - b * H;
-  const int S = mp.S;
-  const int tid = threadIdx.x;
-  const int q_row = qb * 128 + tid;
-  const int qc = min(q_row, S - 1);
-  const int sub = tid >> 5;
-  const Span span = mask_row_span(mp, q_row);
-
-  float q[D], g[D], dq[D];
-  {
-    const float* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(qc) * qss;
-    const float* gp = dO + b * gsb + hd * gsh + static_cast<int64_t>(qc) * gss;
-#pragma unroll
-    for (int d = 0; d < D; d += 4) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(qp + d);
-      const f32x4 w = *reinterpret_cast<const f32x4*>(gp + d);
-      q[d] = v.x * scale_log2;
-      q[d + 1] = v.y * scale_log2;
-      q[d + 2] = v.z * scale_log2;
-      q[d + 3] = v.w * scale_log2;
-      g[d] = w.x;
-      g[d + 1] = w.y;
-      g[d + 2] = w.z;
-      g[d + 3] = w.w;
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < D; ++d) dq[d] = 0.f;
-  const float l2 = lse_log2<CM>(lse[static_cast<int64_t>(bh) * S + qc]);
-  const float dl = delta[static_cast<int64_t>(bh) * S + qc];
-
-  const float* Kbh = K + b * ksb + hd * ksh;
-  const float* Vbh = V + b * vsb + hd * vsh;
-  int e0, e1;
-  if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + qb;
-    e0 = row * ax.cap;
-    e1 = e0 + ax.cnt[row];
-  } else {
-    e0 = row_ptr[qb];
-    e1 = row_ptr[qb + 1];
-  }
-  for (int e = e0; e < e1; ++e) {
-    const int ent = entries[e];
-    const int kt = ent & 0xffff;
-    __syncthreads();
-    for (int c = tid; c < 64 * (D / 4); c += 128) {
-      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-      const int key = min(kt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(kt_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Kbh + key * kss + col);
-      *reinterpret_cast<f32x4*>(vt_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Vbh + key * vss + col);
-    }
-    __syncthreads();
-    const int kind = (ent >> (16 + 2 * sub)) & 3;
-    if (kind == 0) continue;
-    uint64_t keep = ~0ull;  // dropout: keep bits of the tile's 64 keys
-    if constexpr (DR) {
-      keep = 0;
-#pragma unroll 1
-      for (int g = 0; g < 16; ++g)
-        keep |= static_cast<uint64_t>(keep4(ax, bh, q_row, kt * 64 + 4 * g)) << (4 * g);
-    }
-    for (int j = 0; j < 64; ++j) {
-      float sj = 0.f, dp = 0.f;
-#pragma unroll
-      for (int d = 0; d < D; ++d) {
-        sj = fmaf(q[d], kt_lds[j * D + d], sj);
-        dp = fmaf(g[d], vt_lds[j * D + d], dp);
-      }
-      if constexpr (CM) {
-        if (kind >= 2) sj += mask_bias(ax, b, hd, q_row, kt * 64 + j, S) * kLog2e;
-      }
-      float pj = __builtin_amdgcn_exp2f(sj - l2);
-      if constexpr (!CM) {
-        if (kind == 2 && !span_has(span, kt * 64 + j)) pj = 0.f;
-      }
-      if constexpr (DR) dp *= ((keep >> j) & 1) ? ax.keep_scale : 0.f;
-      const float ds = pj * (dp - dl);
-#pragma unroll
-      for (int d = 0; d < D; ++d) dq[d] = fmaf(ds, kt_lds[j * D + d], dq[d]);
-    }
-  }
-  if (q_row >= S) return;
-  float* dp_out = dQ + b * dqsb + hd * dqsh + static_cast<int64_t>(q_row) * dqss;
-#pragma unroll
-  for (int d = 0; d < D; d += 4)
-    *reinterpret_cast<f32x4*>(dp_out + d) =
-        f32x4{dq[d] * scale, dq[d + 1] * scale, dq[d + 2] * scale, dq[d + 3] * scale};
-}
-
-// fp32 dK, dV at head dimension 128 (FMA; 32 and 64 take the matrix-core
-// kernels below): two lanes per key (lane and lane + 32 hold head dims 0..D/2-1
-// and D/2..D-1), 32 keys per wave, 128 per workgroup (the key-major work
-// list); Q, dO, LSE and Δ of each listed 64-query tile staged in LDS.
-template <int D, int FEAT = 0>
-__global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
-    const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
-    const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
-    float* __restrict__ dK, float* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
-    int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t gsb,
-    int64_t gsh, int64_t gss, int64_t dksb, int64_t dksh, int64_t dkss, int64_t dvsb,
-    int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
-    const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
-    const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
-  constexpr int kHd = D / 2;  // head dims per lane
-  __shared__ __attribute__((aligned(16))) float q_lds[64 * D];
-  __shared__ __attribute__((aligned(16))) float g_lds[64 * D];
-  __shared__ float l2_lds[64], dl_lds[64];
-
-  int bh, kb;
-  if (!work_item(wm, order, bh, kb)) return;
-  const int b = bh / H, hd = bh - b * H;
-  const int S = mp.S;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int half = lane >> 5;
-  const int key = kb * 128 + wave * 32 + (lane & 31);
-  const int kc = min(key, S - 1);
-  const Span span = mask_col_span(mp, key);
-
-  float k[kHd], v[kHd], dk[kHd], dv[kHd];
-  {
-    const float* kp = K + b * ksb + hd * ksh + static_cast<int64_t>(kc) * kss + kHd * half;
-    const float* vp = V + b * vsb + hd * vsh + static_cast<int64_t>(kc) * vss + kHd * half;
-#pragma unroll
-    for (int d = 0; d < kHd; d += 4) {
-      const f32x4 a = *reinterpret_cast<const f32x4*>(kp + d);
-      const f32x4 c = *reinterpret_cast<const f32x4*>(vp + d);
-      k[d] = a.x;
-      k[d + 1] = a.y;
-      k[d + 2] = a.z;
-      k[d + 3] = a.w;
-      v[d] = c.x;
-      v[d + 1] = c.y;
-      v[d + 2] = c.z;
-      v[d + 3] = c.w;
-    }
-  }
-#pragma unroll
-  for (int d = 0; d < kHd; ++d) {
-    dk[d] = 0.f;
-    dv[d] = 0.f;
-  }
-  const float* Qbh = Q + b * qsb + hd * qsh;
-  const float* Gbh = dO + b * gsb + hd * gsh;
-  const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
-  const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
-  int e0, e1;
-  if constexpr (CM) {
-    const int row = mask_row(ax, b, hd) * ((S + 127) >> 7) + kb;
-    e0 = row * ax.cap;
-    e1 = e0 + ax.cnt[row];
-  } else {
-    e0 = col_ptr[kb];
-    e1 = col_ptr[kb + 1];
-  }
-  for (int e = e0; e < e1; ++e) {
-    const int ent = entries[e];
-    const int qt = ent & 0xffff;
-    __syncthreads();
-    for (int c = tid; c < 64 * (D / 4); c += 256) {
-      const int row = c / (D / 4), col = (c % (D / 4)) * 4;
-      const int qr = min(qt * 64 + row, S - 1);
-      *reinterpret_cast<f32x4*>(q_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Qbh + qr * qss + col);
-      *reinterpret_cast<f32x4*>(g_lds + row * D + col) =
-          *reinterpret_cast<const f32x4*>(Gbh + qr * gss + col);
-    }
-    if (tid < 64) {
-      const int qr = min(qt * 64 + tid, S - 1);
-      l2_lds[tid] = lse_log2<CM>(lse_bh[qr]);
-      dl_lds[tid] = dl_bh[qr];
-    }
-    __syncthreads();
-    const int kind = (ent >> (16 + 2 * wave)) & 3;
-    if (kind == 0) continue;
-    for (int i = 0; i < 64; ++i) {
-      const float* qi = q_lds + i * D + kHd * half;
-      const float* gi = g_lds + i * D + kHd * half;
-      float sp = 0.f, dpp = 0.f;
-#pragma unroll
-      for (int d = 0; d < kHd; ++d) {
-        sp = fmaf(qi[d], k[d], sp);
-        dpp = fmaf(gi[d], v[d], dpp);
-      }
-      sp += __shfl_xor(sp, 32);
-      dpp += __shfl_xor(dpp, 32);
-      float sl = sp * scale_log2;
-      if constexpr (CM) {
-        if (kind >= 2) sl += mask_bias(ax, b, hd, qt * 64 + i, key, S) * kLog2e;
-      }
-      float pi = __builtin_amdgcn_exp2f(sl - l2_lds[i]);
-      if constexpr (!CM) {
-        if (kind == 2 && !span_has(span, qt * 64 + i)) pi = 0.f;
-      }
-      float pz = pi;
-      if constexpr (DR) {
-        const float z = drop1(ax, bh, qt * 64 + i, key);
-        pz = pi * z;
-        dpp *= z;
-      }
-      const float ds = pi * (dpp - dl_lds[i]);
-#pragma unroll
-      for (int d = 0; d < kHd; ++d) {
-        dv[d] = fmaf(pz, gi[d], dv[d]);
-        dk[d] = fmaf(ds, qi[d], dk[d]);
-      }
-    }
-  }
-  if (key >= S) return;
-  float* dkp = dK + b * dksb + hd * dksh + static_cast<int64_t>(key) * dkss + kHd * half;
-  float* dvp = dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss + kHd * half;
-#pragma unroll
-  for (int d = 0; d < kHd; d += 4) {
-    *reinterpret_cast<f32x4*>(dkp + d) =
-        f32x4{dk[d] * scale, dk[d + 1] * scale, dk[d + 2] * scale, dk[d + 3] * scale};
-    *reinterpret_cast<f32x4*>(dvp + d) = f32x4{dv[d], dv[d + 1], dv[d + 2], dv[d + 3]};
-  }
-}
-
-// fp32 backward on the matrix cores (head dimension 32 or 64; Δ from
+// fp32 backward on the matrix cores (head dimension 32, 64 or 128; Δ from
 // wattn_bwd_delta_f32_kernel; FEAT as for the 16-bit kernels). The layouts of
 // wattn_fwd_f32m_kernel: a v_mfma_f32_32x32x2_f32 k-step sums two head
 // dimensions, one per lane half, for the score-like products (each lane holds
@@ -1672,7 +1314,7 @@ __global__ __launch_bounds__(256) void wattn_bwd_kv_f32_kernel(
 // and 32-key half: Sᵀ = K·Qᵀ and dPᵀ = V·dOᵀ, P = exp2(Sᵀ − LSE·log2e),
 // dSᵀ = P ⊙ (dPᵀ − Δ) (with dropout P ⊙ (Z ⊙ dPᵀ − Δ)), dQᵀ += Kᵀ·dSᵀ.
 template <int D, int FEAT = 0>
-__global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dQ, int64_t qsb, int64_t qsh, int64_t qss, int64_t ksb, int64_t ksh,
@@ -1680,7 +1322,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
     int64_t dqsb, int64_t dqsh, int64_t dqss, int H, MaskParams mp, float scale,
     float scale_log2, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  static_assert(D == 32 || D == 64 || D == 128, "head dimension 32, 64 or 128");
   constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
   constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
@@ -1846,7 +1488,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_q_f32m_kernel(
 // j%4), P = exp2(S − LSE·log2e), dS = P ⊙ (dP − Δ), dVᵀ += dOᵀ·P and
 // dKᵀ += Qᵀ·dS; with dropout dV takes P ⊙ Z and dS = P ⊙ (Z ⊙ dP − Δ).
 template <int D, int FEAT = 0>
-__global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_f32m_kernel(
     const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ dO, const float* __restrict__ lse, const float* __restrict__ delta,
     float* __restrict__ dK, float* __restrict__ dV, int64_t qsb, int64_t qsh, int64_t qss,
@@ -1855,7 +1497,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv_f32m_kernel(
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  static_assert(D == 32 || D == 64, "head dimension 32 or 64");
+  static_assert(D == 32 || D == 64 || D == 128, "head dimension 32, 64 or 128");
   constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   constexpr int kP = D + 4, kTile = 64 * kP, kHalf = D / 2, kDt = D / 32;
   constexpr int kC4 = D / 4, kRpp = 256 / kC4, kPasses = 64 / kRpp;
@@ -2289,21 +1931,12 @@ template <int D, int FEAT>
 void launch_fwd(const AttnLaunch& a) {
   const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os;
   if (a.dtype == TMAC_F32) {
-    if constexpr (D <= 64) {
-      hipLaunchKernelGGL((wattn_fwd_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s,
-                         static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
-                         static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
-                         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],
-                         os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order,
-                         a.wm_q, a.ax_q);
-    } else {  // head dimension 128: one thread per query row (FMA)
-      hipLaunchKernelGGL((wattn_fwd_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s,
-                         static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
-                         static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
-                         qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0],
-                         os[1], os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order,
-                         a.wm_q, a.ax_q);
-    }
+    hipLaunchKernelGGL((wattn_fwd_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s,
+                       static_cast<const float*>(a.Q), static_cast<const float*>(a.K),
+                       static_cast<const float*>(a.V), static_cast<float*>(a.Out), a.lse_out,
+                       qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], os[0], os[1],
+                       os[2], a.H, a.mp, a.scale_log2, a.row_ptr, a.entries, a.order, a.wm_q,
+                       a.ax_q);
   } else if (a.dtype == TMAC_BF16) {
     hipLaunchKernelGGL((wattn_fwd_mfma_kernel<TMAC_BF16, D, FEAT>), dim3(a.grid_q), dim3(256), 0,
                        a.s, static_cast<const uint16_t*>(a.Q), static_cast<const uint16_t*>(a.K),
@@ -2370,31 +2003,16 @@ void launch_bwd_f32(const AttnLaunch& a) {
   const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);
   hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
                      a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
-  if constexpr (D <= 64) {
-    hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
-                       K, V, G, a.lse, a.delta, static_cast<float*>(a.dK),
-                       static_cast<float*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],
-                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],
-                       dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
-                       a.order_kv, a.wm_kv, a.ax_kv);
-    hipLaunchKernelGGL((wattn_bwd_q_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K,
-                       V, G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
-                       ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
-                       dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
-                       a.wm_q, a.ax_q);
-  } else {  // head dimension 128: FMA kernels (two lanes per key; one thread per query)
-    hipLaunchKernelGGL((wattn_bwd_kv_f32_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
-                       K, V, G, a.lse, a.delta, static_cast<float*>(a.dK),
-                       static_cast<float*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0],
-                       vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1],
-                       dvs[2], a.H, a.mp, a.scale, a.scale_log2, a.col_ptr, a.entries_kv,
-                       a.order_kv, a.wm_kv, a.ax_kv);
-    hipLaunchKernelGGL((wattn_bwd_q_f32_kernel<D, FEAT>), dim3(a.grid_q), dim3(128), 0, a.s, Q, K,
-                       V, G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
-                       ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
-                       dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
-                       a.wm_q, a.ax_q);
-  }
+  hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
+                     V, G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
+                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
+                     gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
+                     a.scale_log2, a.col_ptr, a.entries_kv, a.order_kv, a.wm_kv, a.ax_kv);
+  hipLaunchKernelGGL((wattn_bwd_q_f32m_kernel<D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V,
+                     G, a.lse, a.delta, static_cast<float*>(a.dQ), qs[0], qs[1], qs[2], ks[0],
+                     ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dqs[0], dqs[1],
+                     dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr, a.entries, a.order,
+                     a.wm_q, a.ax_q);
 }
 
 template <int FEAT>
