@@ -241,7 +241,7 @@ def test_device_work_lists_bit_exact(dev, lead, kind, S):
     raw = ws.cpu().numpy()
     n_b, n_t = -(-S // 128), -(-S // 64)
     rows = mb * mh * n_b
-    kinds = (n_b * 4 + 255) // 256 * 256
+    kinds = (2 * n_b * 4 + 255) // 256 * 256
     ent_off = kinds + (2 * rows * n_t + 255) // 256 * 256
     cnt_off = ent_off + (2 * rows * n_t * 4 + 255) // 256 * 256
     ent = raw[ent_off:ent_off + 2 * rows * n_t * 4].view(np.int32).reshape(2, rows, n_t)
@@ -249,7 +249,12 @@ def test_device_work_lists_bit_exact(dev, lead, kind, S):
     bits_off = cnt_off + (2 * rows * 4 + 255) // 256 * 256
     words = mb * mh * n_b * 128 * n_t
     bits = raw[bits_off:bits_off + 2 * words * 8].view(np.uint64).reshape(2, mb * mh, n_b * 128, n_t)
-    assert np.array_equal(raw[:n_b * 4].view(np.int32), np.arange(n_b))
+    # launch orders: blocks by their longest list over the mask rows, longest first,
+    # ties by block index (query-major, then key-major)
+    order = raw[:2 * n_b * 4].view(np.int32).reshape(2, n_b)
+    for side in range(2):
+        longest = cnt[side].reshape(mb * mh, n_b)[:64].max(axis=0)
+        assert np.array_equal(order[side], np.argsort(-longest, kind="stable")), side
     m4 = mask.reshape((1,) * (4 - mask.ndim) + mask.shape)
     for r in range(mb * mh):
         one = m4[r // mh, r % mh] if m4.shape[0] > 1 else m4[0, r % mh]

@@ -394,8 +394,10 @@ def test_mask_workspace_size(lib):
         rows = mb * mh * n_b
         bitmaps = 2 * mb * mh * n_b * 128 * n_t * 8
         assert n % 256 == 0
-        assert n >= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps
-        assert n <= 4 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps + 4 * 256
+        # two launch orders, kinds (1 byte) and entries (4 bytes) per list row and tile,
+        # counts, bitmaps; each part 256-byte aligned
+        assert n >= 8 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps
+        assert n <= 8 * n_b + 2 * rows * n_t * (1 + 4) + 2 * rows * 4 + bitmaps + 4 * 256
     for bad in [(0, 1, 1), (64, 0, 1), (64, 1, 0), (-5, 1, 1)]:
         assert lib.tmac_wattn_mask_workspace(*bad) == 0
 

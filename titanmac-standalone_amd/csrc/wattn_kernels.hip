@@ -1681,7 +1681,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_f32m_kernel(
     }
 }
 
-// Work lists of a caller's mask (kFeatMask), built on the device in two launches.
+// Work lists of a caller's mask (kFeatMask), built on the device in three launches.
 //
 // 1. wattn_mask_kinds_kernel: one workgroup per (mask row mr, 128x128 square
 //    (query block i, key block j)); wave w reads the square's 32 query rows
@@ -1702,8 +1702,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_f32m_kernel(
 //    Positions at or past S count as masked.
 // 2. wattn_mask_compact_kernel: one wave per list row (query-major rows, then
 //    key-major rows): entries[row * n_t + c] = t | kinds << 16 for the tiles t
-//    with a nonzero kind, t ascending, and cnt[row] = their number. Wave 0 also
-//    writes the identity launch order of the blocks.
+//    with a nonzero kind, t ascending, and cnt[row] = their number.
 __global__ __launch_bounds__(256) void wattn_mask_kinds_kernel(AttnX ax, int S, int n_b, int n_t,
                                                                uint8_t* __restrict__ kinds_q,
                                                                uint8_t* __restrict__ kinds_kv,
@@ -1796,12 +1795,10 @@ __global__ __launch_bounds__(256) void wattn_mask_kinds_kernel(AttnX ax, int S, 
 }
 
 __global__ __launch_bounds__(256) void wattn_mask_compact_kernel(
-    const uint8_t* __restrict__ kinds, int n_rows, int n_t, int n_b, int32_t* __restrict__ entries,
-    int32_t* __restrict__ cnt, int32_t* __restrict__ order) {
+    const uint8_t* __restrict__ kinds, int n_rows, int n_t, int32_t* __restrict__ entries,
+    int32_t* __restrict__ cnt) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (blockIdx.x == 0 && threadIdx.x < 64)
-    for (int b = lane; b < n_b; b += 64) order[b] = b;
   if (row >= n_rows) return;
   const uint8_t* kr = kinds + static_cast<int64_t>(row) * n_t;
   int32_t* er = entries + static_cast<int64_t>(row) * n_t;
@@ -1820,9 +1817,43 @@ __global__ __launch_bounds__(256) void wattn_mask_compact_kernel(
   if (lane == 0) cnt[row] = count;
 }
 
+// 3. wattn_mask_order_kernel: the launch order of each orientation (workgroup 0:
+//    query-major, 1: key-major): blocks by list length, longest first (ties by
+//    block index), the length of a block being its largest over the first
+//    kOrderRows mask rows; rank r launches order[r] of every head, and rank 0 of
+//    all heads goes first (one lead rank, as in the host schedule). Up to
+//    kOrderBlocks blocks (S <= 65536); beyond that the order is the identity.
+constexpr int kOrderBlocks = 512, kOrderRows = 64;
+
+__global__ __launch_bounds__(256) void wattn_mask_order_kernel(const int32_t* __restrict__ cnt,
+                                                               int n_mr, int n_b,
+                                                               int32_t* __restrict__ order) {
+  __shared__ int len[kOrderBlocks];
+  const int side = blockIdx.x;
+  const int32_t* c = cnt + static_cast<int64_t>(side) * n_mr * n_b;
+  int32_t* o = order + side * n_b;
+  if (n_b > kOrderBlocks) {
+    for (int b = threadIdx.x; b < n_b; b += 256) o[b] = b;
+    return;
+  }
+  const int rows = min(n_mr, kOrderRows);
+  for (int b = threadIdx.x; b < n_b; b += 256) {
+    int m = 0;
+    for (int r = 0; r < rows; ++r) m = max(m, c[static_cast<int64_t>(r) * n_b + b]);
+    len[b] = m;
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < n_b; b += 256) {
+    const int lb = len[b];
+    int rank = 0;
+    for (int b2 = 0; b2 < n_b; ++b2) rank += (len[b2] > lb) | ((len[b2] == lb) & (b2 < b));
+    o[rank] = b;
+  }
+}
+
 // Byte offsets of the parts of a mask workspace (each 256-byte aligned): the
-// launch order; the tile kinds, query-major rows then key-major rows; the
-// entries, same order; the counts, same order.
+// launch orders, query-major then key-major; the tile kinds, query-major rows
+// then key-major rows; the entries, same order; the counts, same order.
 struct MaskWs {
   size_t order, kinds_q, kinds_kv, ent_q, ent_kv, cnt_q, cnt_kv, bits_q, bits_kv, total;
   int64_t rows;  // list rows of each orientation: mask rows x blocks
@@ -1833,8 +1864,8 @@ inline MaskWs mask_ws_layout(int S, int mask_batch, int mask_heads) {
   const size_t rows = static_cast<size_t>(mask_batch) * mask_heads * n_b;
   MaskWs w;
   w.rows = static_cast<int64_t>(rows);
-  w.order = 0;
-  w.kinds_q = up(n_b * 4);
+  w.order = 0;  // query-major, then key-major at order + n_b * 4
+  w.kinds_q = up(2 * n_b * 4);
   w.kinds_kv = w.kinds_q + rows * n_t;
   w.ent_q = w.kinds_q + up(2 * rows * n_t);
   w.ent_kv = w.ent_q + rows * n_t * 4;
@@ -2081,9 +2112,10 @@ int setup_lists(AttnLaunch& a, const tmac_attn_opts* opts, int window, int n_per
     a.ax_kv.bits = reinterpret_cast<const uint64_t*>(ws + w.bits_kv);
     a.entries = reinterpret_cast<const int32_t*>(ws + w.ent_q);
     a.entries_kv = reinterpret_cast<const int32_t*>(ws + w.ent_kv);
-    a.order = a.order_kv = reinterpret_cast<const int32_t*>(ws + w.order);
+    a.order = reinterpret_cast<const int32_t*>(ws + w.order);
+    a.order_kv = a.order + n_qb;
     a.row_ptr = a.col_ptr = nullptr;
-    n_lead = n_lead_kv = 0;  // identity order, no lead blocks
+    n_lead = n_lead_kv = 1;  // the longest list of every head first (wattn_mask_order_kernel)
     a.mp = MaskParams{a.S, a.S, 0, 0, TMAC_PATTERN_BAND, 1};
   } else {
     if (!row_ptr || !entries || !order) return TMAC_ERR_NULL;
@@ -2203,9 +2235,11 @@ extern "C" int tmac_wattn_mask_lists(const tmac_attn_opts* opts, int S, void* st
                      reinterpret_cast<uint32_t*>(ws + w.bits_kv));
   const int64_t n_rows = 2 * w.rows;  // query-major rows, then key-major rows
   hipLaunchKernelGGL(wattn_mask_compact_kernel, dim3(static_cast<unsigned>((n_rows + 3) / 4)),
-                     dim3(256), 0, s, kinds_q, static_cast<int>(n_rows), n_t, n_b,
+                     dim3(256), 0, s, kinds_q, static_cast<int>(n_rows), n_t,
                      reinterpret_cast<int32_t*>(ws + w.ent_q),
-                     reinterpret_cast<int32_t*>(ws + w.cnt_q),
+                     reinterpret_cast<int32_t*>(ws + w.cnt_q));
+  hipLaunchKernelGGL(wattn_mask_order_kernel, dim3(2), dim3(256), 0, s,
+                     reinterpret_cast<const int32_t*>(ws + w.cnt_q), static_cast<int>(n_mr), n_b,
                      reinterpret_cast<int32_t*>(ws + w.order));
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
