@@ -882,8 +882,9 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
   store_row<DT, T::kDt>(dV + b * dvsb + hd * dvsh + static_cast<int64_t>(key) * dvss, dvt, 1.f, h);
 }
 
-// dK, dV at head dimension 64 without a caller's mask (FEAT 0 or kFeatDrop):
-// the work of wattn_bwd_kv_kernel, with the query tiles copied HBM/L2 -> LDS by
+// dK, dV at head dimension 64 (every FEAT; a caller's mask word of the next
+// tile is loaded during the current one): the work of wattn_bwd_kv_kernel, with
+// the query tiles copied HBM/L2 -> LDS by
 // global_load_lds into a ring of four stages, three tiles ahead of the math,
 // one barrier per tile. Stage = Q and dO tiles (64 rows of 128 bytes, chunks
 // swizzled by swz64: conflict-free for the S/dP operands' 16-byte row reads and
@@ -906,9 +907,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
     int64_t dvsh, int64_t dvss, int H, MaskParams mp, float scale, float scale_log2,
     const int32_t* __restrict__ col_ptr, const int32_t* __restrict__ entries,
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
-  static_assert((FEAT & kFeatMask) == 0, "caller masks take wattn_bwd_kv_kernel");
   constexpr int D = 64;
-  constexpr bool DR = (FEAT & kFeatDrop) != 0;
+  constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
   __shared__ __attribute__((aligned(16))) uint16_t ring[kKvStages * kKvStageB / 2];
 
@@ -944,8 +944,22 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
   const uint16_t* Gbh = dO + b * gsb + hd * gsh;
   const float* lse_bh = lse + static_cast<int64_t>(bh) * S;
   const float* dl_bh = delta + static_cast<int64_t>(bh) * S;
-  const int e0 = col_ptr[kb], e1 = col_ptr[kb + 1];
+  int e0, e1, mrow = 0;
+  if constexpr (CM) {
+    mrow = mask_row(ax, b, hd);
+    const int row = mrow * ((S + 127) >> 7) + kb;
+    e0 = row * ax.cap;
+    e1 = e0 + ax.cnt[row];
+  } else {
+    e0 = col_ptr[kb];
+    e1 = col_ptr[kb + 1];
+  }
   const int n = e1 - e0;
+  // caller's mask: allowed-query bits of this key in the current and the next tile
+  uint64_t wb = 0, wb_next = 0;
+  if constexpr (CM) {
+    if (n > 0) wb = mask_word(ax, mrow, key, entries[e0] & 0xffff, S);
+  }
 
   // Copies: this wave's rows of Q and dO, chunk positions as for swz64 (lane L
   // of an instruction covering rows R..R+7 fills chunk position L & 7 of row
@@ -1008,7 +1022,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
       // LSE -> LSE·log2e (wave 2) and Δ -> −Δ (wave 3), in place (this wave's
       // copy has landed)
       float* v = lse2 + 64 * (wave - 2) + lane;
-      *v = wave == 2 ? lse_log2<false>(*v) : -*v;
+      *v = wave == 2 ? lse_log2<CM>(*v) : -*v;
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     // every wave's copies of tile i are in LDS (and converted), and every wave
@@ -1019,6 +1033,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
     const int ent = entries[e0 + i];
     const int qt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
+    if constexpr (CM) {
+      if (i + 1 < n) wb_next = mask_word(ax, mrow, key, entries[e0 + i + 1] & 0xffff, S);
+    }
     if (kind != 0) {
       const uint16_t* q_lds = st;
       const uint16_t* g_lds = st + kKvTileB / 2;
@@ -1040,7 +1057,25 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
         }
       }
       // s2[qh][j] = S[query][key], query = qt*64 + 32qh + 8(j/4) + 4h + j%4
-      if (kind == 2) {
+      if constexpr (CM) {
+        // log2 units; partial slices take -inf from the mask's bits (kind 2) or
+        // add the mask's bias element by element (kind 3)
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) s2[qh] *= scale_log2;
+        if (kind == 2) {
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh)
+            apply_bits(s2[qh], static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
+        } else if (kind == 3) {
+#pragma unroll
+          for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+              const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
+              s2[qh][j] += mask_bias(ax, b, hd, qr, key, S) * kLog2e;
+            }
+        }
+      } else if (kind == 2) {
 #pragma unroll
         for (int qh = 0; qh < 2; ++qh) apply_bits(s2[qh], span_bits32(span, qt * 64 + 32 * qh + 4 * h));
       }
@@ -1048,13 +1083,14 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
       for (int qh = 0; qh < 2; ++qh) {
         f32x16& s = s2[qh];
         f32x16& dp = dp2[qh];
-        kv_half_update<DT, D, DR>(s, dp, scale_log2, lse_l, ndl_l, qh, qt * 64, h, grp, lane, key,
+        kv_half_update<DT, D, DR>(s, dp, CM ? 1.f : scale_log2, lse_l, ndl_l, qh, qt * 64, h, grp, lane, key,
                                   bh, ax, q_lds, g_lds, dkt, dvt,
                                   [&](const uint16_t* t, int r0, int r1, int c0) {
                                     return lds_read_tr4x2_swz64(t, r0, r1, c0, lane);
                                   });
       }
     }
+    if constexpr (CM) wb = wb_next;
   }
 
   if (key >= S) return;
@@ -2001,7 +2037,7 @@ void launch_bwd_mfma(const AttnLaunch& a) {
                      gs[2], dqs[0], dqs[1], dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr,
                      a.entries, a.order, a.wm_q, a.ax_q);
   // The copy-ring kernel addresses 64 rows of Q and dO with 32-bit byte offsets.
-  if constexpr (D == 64 && (FEAT & kFeatMask) == 0) {
+  if constexpr (D == 64) {
     if (qs[2] <= (1ll << 25) && gs[2] <= (1ll << 25)) {
       hipLaunchKernelGGL((wattn_bwd_kv64_kernel<DT, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
                          K, V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
