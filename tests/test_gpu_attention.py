@@ -112,6 +112,32 @@ def test_config1_module_fp32(dev):
     assert np.abs(got - want).max() <= 1e-4 * np.abs(want).max()
 
 
+def test_config3_full_size_fp32(dev):
+    """Config 3's shape in fp32 (B=8, H=10, S=4096, w=512, Np=16: the fp32 matrix-core
+    kernel at 80 heads): (b, h) = (0, 0) and (7, 9) in full, and in every (b, h) the
+    mask's boundary rows and 6 random rows, within 1e-4 of the largest oracle entry."""
+    B, H, S = 8, 10, 4096
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(B, H, S, 64, generator=g) for _ in range(3))
+    o = windowed_attention(q.to(dev), k.to(dev), v.to(dev), 512, 16).cpu().numpy()
+    assert np.isfinite(o).all()
+    mask = om.band_mask(S, 512, 16)
+    qn, kn, vn = q.numpy(), k.numpy(), v.numpy()
+
+    def chk(got, ref, what):
+        err = np.abs(got - ref).max()
+        assert err <= 1e-4 * np.abs(ref).max(), f"{what}: {err}"
+
+    for b, h in [(0, 0), (7, 9)]:
+        chk(o[b, h], oa.masked_attention(qn[b, h], kn[b, h], vn[b, h], mask), f"({b}, {h})")
+    rng = np.random.default_rng(32)
+    for b in range(B):
+        for h in range(H):
+            rows = sampled.sample_rows(S, 16, 512, rng)
+            chk(o[b, h][rows], sampled.fwd_rows_ref(qn[b, h], kn[b, h], vn[b, h], mask, rows),
+                f"(b, h) = ({b}, {h})")
+
+
 def test_config3_full_size(dev):
     """BASELINE config 3 (B=8, H=10, S=4096, w=512, Np=16, bf16): two (b, h) pairs
     checked in full against the oracle; in every one of the 80 (b, h) pairs, the

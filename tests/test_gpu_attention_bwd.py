@@ -152,6 +152,38 @@ def test_backward_full_size_cfg3(dev):
             close(gv[b, h][cols], ref_v, what=f"dv ({b}, {h})")
 
 
+def test_backward_full_size_cfg3_fp32(dev):
+    """Config 3's shape in fp32 (the fp32 matrix-core dQ and dK/dV kernels at 80 heads):
+    (b, h) = (0, 0) and (7, 9) in full, and in every (b, h) dQ on the boundary rows and 6
+    random rows and dK, dV on 3 sequence keys, within 1e-4 of the largest oracle entry."""
+    B, H, S, w, Np = 8, 10, 4096, 512, 16
+    q, k, v, do = tensors((B, H, S, 64), torch.float32, seed=16)
+    _, dq, dk, dv = run_bwd(dev, q, k, v, do, w, Np, True, "band", 64)
+    gq, gk, gv = (t.cpu().numpy() for t in (dq, dk, dv))
+    assert all(np.isfinite(t).all() for t in (gq, gk, gv))
+    mask = om.band_mask(S, w, Np)
+    qn, kn, vn, dn = (t.numpy() for t in (q, k, v, do))
+
+    def chk(got, ref, what):
+        err = np.abs(got - ref).max()
+        assert err <= 1e-4 * max(1.0, np.abs(ref).max()), f"{what}: {err}"
+
+    for b, h in [(0, 0), (7, 9)]:
+        want = oa.masked_attention_grads(qn[b, h], kn[b, h], vn[b, h], dn[b, h], mask)
+        for got, ref, name in zip((gq, gk, gv), want, "qkv"):
+            chk(got[b, h], ref, f"d{name} ({b}, {h})")
+    rng = np.random.default_rng(33)
+    for b in range(B):
+        for h in range(H):
+            args = (qn[b, h], kn[b, h], vn[b, h], dn[b, h], mask)
+            rows = sampled.sample_rows(S, Np, w, rng)
+            chk(gq[b, h][rows], sampled.dq_rows_ref(*args, rows), f"dq ({b}, {h})")
+            cols = np.array(sorted({Np, *rng.choice(np.arange(Np + 1, S), 2, replace=False)}))
+            ref_k, ref_v = sampled.dkv_cols_ref(*args, cols)
+            chk(gk[b, h][cols], ref_k, f"dk ({b}, {h})")
+            chk(gv[b, h][cols], ref_v, f"dv ({b}, {h})")
+
+
 def _module_grads_fp64(m, x, dy, mask, conv=False):
     """fp64 CPU autograd of the attention module's function on the module's own weights."""
     w_qkv = m.qkv_proj.weight.detach().double().cpu().requires_grad_()
