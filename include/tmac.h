@@ -328,12 +328,14 @@ typedef struct {
    * dropout_p (attn/windowed_attention.py:318-323) and
    * BlockSparseAttention's F.dropout of the weights
    * (attn/block_sparse_attention.py:196-197): each probability of (b, h, q, k)
-   * is kept with probability 1 - p and scaled by 1 / (1 - p); the row sums
-   * (lse) use the undropped probabilities. The keep decision is the Philox
-   * 4x32-10 draw (Salmon et al., SC 2011) of counter
-   * {k / 4, q, b * H + h, 0} under key {seed low 32 bits, seed high 32 bits},
-   * word k % 4, compared with p * 2^32 (kept iff draw >= floor(p * 2^32)): the
-   * same seed gives the same mask in forward and backward. 0 <= p < 1. */
+   * is kept with probability 1 - p (to within 2^-16) and scaled by the
+   * inverse of its keep probability; the row sums (lse) use the undropped
+   * probabilities. The keep decision is a 16-bit draw of Philox 4x32-10
+   * (Salmon et al., SC 2011) at counter {k / 8, q, b * H + h, 0} under key
+   * {seed low 32 bits, seed high 32 bits}: draw k % 8 (bits 16 * (k % 2) ..
+   * of word (k % 8) / 2), kept iff draw >= t = floor(p * 2^16), and kept
+   * entries are scaled by 2^16 / (2^16 - t). The same seed gives the same mask
+   * in forward and backward. 0 <= p < 1. */
   float dropout_p;
   uint64_t dropout_seed;
 } tmac_attn_opts;

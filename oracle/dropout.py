@@ -15,8 +15,13 @@ round multipliers 0xD2511F53 and 0xCD9E8D57, Weyl key increments 0x9E3779B9
 and 0xBB67AE85. Pinned by the Random123 known-answer vectors (tests).
 
 Decision of pair (bh, q, k) for seed s and probability p: counter
-{k // 4, q, bh, 0}, key {s mod 2^32, s // 2^32}, output word k % 4; kept iff
-word >= floor(p · 2^32) (p as float32, then exact).
+{k // 8, q, bh, 0}, key {s mod 2^32, s // 2^32}; the 128-bit output read as
+eight 16-bit draws, draw i = bits 16(i % 2) .. 16(i % 2) + 15 of word i // 2,
+and key k takes draw k % 8; kept iff draw >= t = floor(p · 2^16) (p as float32,
+then exact, at most 2^16 - 1). Kept entries are scaled by 2^16 / (2^16 - t), the
+inverse of the exact keep probability (1 - p to within 2^-16), so the expected
+factor is 1. One draw decides eight pairs, so the kernels make one Philox call
+per eight decisions.
 """
 from __future__ import annotations
 
@@ -44,35 +49,40 @@ def philox4x32_10(ctr: np.ndarray, key) -> np.ndarray:
 
 
 def threshold(p: float) -> int:
-    """floor(p · 2^32) of p rounded to float32, clamped to 2^32 - 1."""
-    t = np.floor(float(np.float32(p)) * 4294967296.0)
-    return int(min(t, 4294967295.0))
+    """floor(p · 2^16) of p rounded to float32, clamped to 2^16 - 1."""
+    t = np.floor(float(np.float32(p)) * 65536.0)
+    return int(min(t, 65535.0))
+
+
+def keep_scale(p: float) -> float:
+    """Factor of a kept entry: 2^16 / (2^16 - threshold(p)), as the kernels compute it in float32."""
+    return float(np.float32(65536.0) / np.float32(65536 - threshold(p)))
 
 
 def keep_mask(bh: int, rows: np.ndarray, cols: np.ndarray, seed: int, p: float) -> np.ndarray:
     """bool [len(rows), len(cols)]: whether pair (bh, q, k) survives dropout p.
 
-    One Philox call per (row, key group k // 4) that the columns touch; key k takes
-    word k % 4 of its group's draw."""
+    One Philox call per (row, key group k // 8) that the columns touch; key k takes
+    the 16-bit draw k % 8 of its group's output."""
     rows = np.asarray(rows, dtype=np.int64)
     cols = np.asarray(cols, dtype=np.int64)
     t = threshold(p)
-    if t >= 2**32:
-        return np.zeros((rows.size, cols.size), bool)
-    groups, inv = np.unique(cols // 4, return_inverse=True)
+    groups, inv = np.unique(cols // 8, return_inverse=True)
     ctr = np.zeros((rows.size, groups.size, 4), dtype=np.uint32)
     ctr[..., 0] = groups[None, :]
     ctr[..., 1] = rows[:, None]
     ctr[..., 2] = bh
     out = philox4x32_10(ctr, (seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF))  # [rows, groups, 4]
-    words = out[:, inv, cols % 4]  # [rows, cols]
-    return words >= np.uint32(t)
+    i = cols % 8
+    words = out[:, inv, i // 2]  # [rows, cols]
+    draws = (words >> (16 * (i % 2)).astype(np.uint32)) & np.uint32(0xFFFF)
+    return draws >= np.uint32(t)
 
 
 def drop_factors(B: int, H: int, S: int, seed: int, p: float, rows=None) -> np.ndarray:
-    """float64 [B, H, len(rows), S]: 1 / (1 - p) where kept, else 0 (rows default: all)."""
+    """float64 [B, H, len(rows), S]: keep_scale(p) where kept, else 0 (rows default: all)."""
     rows = np.arange(S) if rows is None else np.asarray(rows)
-    scale = 1.0 / (1.0 - float(np.float32(p)))
+    scale = keep_scale(p)
     z = np.empty((B, H, rows.size, S))
     cols = np.arange(S)
     for b in range(B):

@@ -332,7 +332,7 @@ def test_config3_size_caller_mask_and_dropout_sampled(dev):
         b, h = divmod(bh, H)
         rows = sampled.sample_rows(S, 16, 512, rng, n_random=4)
         rows = np.unique(np.concatenate([rows, [100]]))
-        z = od.keep_mask(bh, rows, cols, seed, p) / (1.0 - float(np.float32(p)))
+        z = od.keep_mask(bh, rows, cols, seed, p) * od.keep_scale(p)
         want = oa.biased_attention(qn[b, h, rows], kn[b, h], vn[b, h], bias[rows], 0.125, z)
         close(o_np[b, h, rows], want, what=f"out (b,h)={b, h}")
         gq, _, _ = oa.biased_attention_grads(qn[b, h, rows], kn[b, h], vn[b, h], gn[b, h, rows],
@@ -342,7 +342,7 @@ def test_config3_size_caller_mask_and_dropout_sampled(dev):
         b, h = divmod(bh, H)
         keys = np.array(sorted({0, 15, 16, 17, 511, 512, 2047, 4095} | set(rng.choice(S, 4).tolist())))
         qrows = np.nonzero(mask[:, keys].any(axis=1))[0]
-        z = od.keep_mask(bh, qrows, cols, seed, p) / (1.0 - float(np.float32(p)))
+        z = od.keep_mask(bh, qrows, cols, seed, p) * od.keep_scale(p)
         _, gk, gv = oa.biased_attention_grads(qn[b, h, qrows], kn[b, h], vn[b, h], gn[b, h, qrows],
                                               bias[qrows], 0.125, z, out=o_np[b, h, qrows])
         close(dk[b, h, keys], gk[keys], what=f"dk (b,h)={b, h}")

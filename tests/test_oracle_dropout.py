@@ -4,8 +4,9 @@ caller-mask / dropout attention (biased_attention and its gradients).
 - Philox4x32-10 against the Random123 known-answer vectors (the published
   reference implementation of Salmon et al., SC 2011, kat_vectors file);
 - keep decisions: rate within binomial bounds, p = 0 keeps everything, the
-  threshold is floor(p * 2^32) of p as float32, distinct (bh, q, k) draw from
-  distinct (counter, word) pairs;
+  threshold is floor(p * 2^16) of p as float32 and the kept factor the inverse of
+  the exact keep probability, distinct (bh, q, k) draw from distinct (counter,
+  16-bit draw) pairs;
 - biased_attention against torch's fp64 SDPA with the same float or bool mask
   (a library routine), including rows with every key masked (SDPA returns 0);
 - gradients against torch autograd of the same function written with torch ops
@@ -45,11 +46,16 @@ def test_philox_vectorised_equals_scalar():
         assert np.array_equal(got[idx], od.philox4x32_10(ctr[idx], key))
 
 
-def test_threshold():
+def test_threshold_and_scale():
     assert od.threshold(0.0) == 0
-    assert od.threshold(0.5) == 2**31
-    assert od.threshold(0.1) == int(np.floor(float(np.float32(0.1)) * 2**32))
-    assert od.threshold(np.nextafter(np.float32(1), np.float32(0))) < 2**32
+    assert od.threshold(0.5) == 2**15
+    assert od.threshold(0.1) == int(np.floor(float(np.float32(0.1)) * 2**16)) == 6553
+    assert od.threshold(np.nextafter(np.float32(1), np.float32(0))) == 2**16 - 1
+    assert od.keep_scale(0.0) == 1.0 and od.keep_scale(0.5) == 2.0
+    # a 16-bit draw is kept with probability (2^16 - t) / 2^16: the factor makes E[z] = 1
+    t = od.threshold(0.1)
+    assert abs(od.keep_scale(0.1) * (65536 - t) / 65536 - 1.0) < 1e-7
+    assert abs(od.keep_scale(0.1) - 1 / 0.9) < 2e-5
 
 
 @pytest.mark.parametrize("p", [0.0, 0.1, 0.5, 0.9])
@@ -71,19 +77,21 @@ def test_keep_mask_depends_on_every_coordinate_and_seed():
     assert not np.array_equal(base, od.keep_mask(4, rows, cols, seed=11, p=0.5))
     assert not np.array_equal(base, od.keep_mask(3, rows, cols, seed=12, p=0.5))
     assert not np.array_equal(base, od.keep_mask(3, rows, cols, seed=11 + (1 << 32), p=0.5))
-    # rows and columns are not interchangeable, and columns 4 apart use different counters
+    # rows and columns are not interchangeable, and columns 8 apart use different counters
     assert not np.array_equal(base, base.T)
-    assert not np.array_equal(base[:, :4], base[:, 4:8])
+    assert not np.array_equal(base[:, :8], base[:, 8:16])
 
 
-def test_keep_mask_word_layout():
-    """Key k uses word k % 4 of the draw of counter {k // 4, q, bh, 0}."""
+def test_keep_mask_draw_layout():
+    """Key k uses the 16-bit draw k % 8 (low half of word (k % 8) // 2 first) of
+    counter {k // 8, q, bh, 0}."""
     seed, p = 99, 0.3
-    k = np.arange(16)
+    k = np.arange(24)
     keep = od.keep_mask(5, np.array([9]), k, seed, p)[0]
-    for g in range(4):
-        r = od.philox4x32_10(np.array([g, 9, 5, 0], dtype=np.uint32), (seed, 0))
-        assert np.array_equal(keep[4 * g:4 * g + 4], r >= od.threshold(p))
+    for g in range(3):
+        r = [int(w) for w in od.philox4x32_10(np.array([g, 9, 5, 0], dtype=np.uint32), (seed, 0))]
+        draws = [(r[i // 2] >> (16 * (i % 2))) & 0xFFFF for i in range(8)]
+        assert list(keep[8 * g:8 * g + 8]) == [d >= od.threshold(p) for d in draws]
 
 
 def _torch_ref(q, k, v, bias, scale, z, do=None):
@@ -164,7 +172,8 @@ def test_biased_attention_grads_against_torch_autograd(p):
 def test_drop_factors_scale():
     z = od.drop_factors(1, 2, 50, seed=5, p=0.2)
     vals = np.unique(z)
-    assert set(vals.tolist()) <= {0.0, 1.0 / (1.0 - float(np.float32(0.2)))}
+    assert set(vals.tolist()) == {0.0, od.keep_scale(0.2)}
+    assert abs(od.keep_scale(0.2) - 1.0 / (1.0 - float(np.float32(0.2)))) < 3e-5
 
 
 def test_grads_with_stored_output():

@@ -325,8 +325,8 @@ struct AttnX {
   const uint64_t* bits;  // allowed-pair bitmap: word (mask row, position, tile) holds 64 bits,
                          // one per position of the other axis in that tile
   uint32_t seed0, seed1; // dropout seed
-  uint32_t thresh;       // dropped when the 32-bit draw is below thresh (= p * 2^32)
-  float keep_scale;      // 1 / (1 - p)
+  uint32_t thresh;       // dropped when the 16-bit draw is below thresh (= floor(p * 2^16))
+  float keep_scale;      // 2^16 / (2^16 - thresh): the inverse of the keep probability
 };
 
 // Row of the custom work lists of (b, head): the mask's own (batch, head) row.
@@ -353,52 +353,58 @@ __device__ __forceinline__ float mask_bias(const AttnX& x, int b, int hd, int q,
   return static_cast<const float*>(x.mask)[off];
 }
 
-// Dropout factor of (bh, q, k) for each of the four keys k0..k0+3 (k0 a multiple
-// of 4): keep_scale or 0.
-__device__ __forceinline__ void drop4(const AttnX& x, int bh, int q, int k0, float (&z)[4]) {
-  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k0) >> 2, static_cast<uint32_t>(q),
-                                      static_cast<uint32_t>(bh), 0u},
+// Dropout decisions. Pair (bh, q, k) is kept iff the 16-bit draw k % 8 of
+// Philox4x32-10 at counter {k / 8, q, bh, 0} (draw i = bits 16(i % 2).. of word
+// i / 2) is at least thresh: one call decides eight consecutive keys of a row.
+//
+// Dropout factors (keep_scale or 0) of a lane that holds query q and, of the 16
+// keys base .. base + 15 (base a multiple of 16), the keys base + 4h + t and
+// base + 8 + 4h + t, t = 0..3, where lane l ^ 32 holds the same query and the
+// other four of each eight (h = lane / 32): z[t] and z[4 + t]. Lane half h draws
+// the eight keys base + 8h .. +7 and hands the other half the two words of draws
+// it needs, so each call serves eight decisions.
+__device__ __forceinline__ void drop_row8(const AttnX& x, int bh, int q, int base, int h,
+                                          float (&z)[8]) {
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>((base >> 3) + h),
+                                      static_cast<uint32_t>(q), static_cast<uint32_t>(bh), 0u},
                                 x.seed0, x.seed1);
-  z[0] = r.x >= x.thresh ? x.keep_scale : 0.f;
-  z[1] = r.y >= x.thresh ? x.keep_scale : 0.f;
-  z[2] = r.z >= x.thresh ? x.keep_scale : 0.f;
-  z[3] = r.w >= x.thresh ? x.keep_scale : 0.f;
-}
-// Keep bits of (bh, q, k0..k0+3), bit i for key k0 + i (k0 a multiple of 4).
-__device__ __forceinline__ uint32_t keep4(const AttnX& x, int bh, int q, int k0) {
-  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k0) >> 2, static_cast<uint32_t>(q),
-                                      static_cast<uint32_t>(bh), 0u},
-                                x.seed0, x.seed1);
-  return static_cast<uint32_t>(r.x >= x.thresh) | (static_cast<uint32_t>(r.y >= x.thresh) << 1) |
-         (static_cast<uint32_t>(r.z >= x.thresh) << 2) |
-         (static_cast<uint32_t>(r.w >= x.thresh) << 3);
+  // words 0, 1 hold the draws of keys +0..3 of a group, words 2, 3 those of +4..7:
+  // half 0 keeps words 0, 1 of group 0 and sends 2, 3; half 1 keeps words 2, 3 of
+  // group 1 and sends 0, 1
+  const uint32_t keep_a = h ? r.z : r.x, keep_b = h ? r.w : r.y;
+  const uint32_t recv_a = static_cast<uint32_t>(__shfl_xor(static_cast<int>(h ? r.x : r.z), 32));
+  const uint32_t recv_b = static_cast<uint32_t>(__shfl_xor(static_cast<int>(h ? r.y : r.w), 32));
+  const uint32_t w[4] = {h ? recv_a : keep_a, h ? recv_b : keep_b,   // keys base + 4h + 0..3
+                         h ? keep_a : recv_a, h ? keep_b : recv_b};  // keys base + 8 + 4h + 0..3
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    z[i] = ((w[i >> 1] >> (16 * (i & 1))) & 0xffffu) >= x.thresh ? x.keep_scale : 0.f;
 }
 // Keep bits of a lane that holds key k and the four queries q0..q0+3 (q0 a
-// multiple of 4), where the four lanes of its quad (lane & ~3 .. +3, all active)
-// hold the keys (k & ~3) + 0..3 with the same q0 and iq = lane & 3 = k & 3: bit 4t
-// of the result is the decision of (q0 + t, k). Each lane draws one Philox call,
-// counter {k / 4, q0 + iq, bh, 0}, whose four words decide the quad's four keys
-// at query q0 + iq; the quad then exchanges those 4-bit groups (DPP broadcasts
-// within the quad), so each decision costs a quarter call, as in the row layout.
+// multiple of 4), where the four lanes of its quad (lane & ~3 .. +3, all active,
+// iq = lane & 3 = k & 3) hold keys with the same k / 4: bit 4t of the result is
+// the decision of (q0 + t, k). Lane iq draws the eight keys of k's group at query
+// q0 + iq; the quad's keys use two of its four words (draws 4·((k / 4) % 2) +
+// 0..3), which DPP broadcasts hand to every lane of the quad, so each call serves
+// four decisions of the quad.
 __device__ __forceinline__ uint32_t keep_quad(const AttnX& x, int bh, int q0, int k, int iq) {
-  const uint32_t nib = keep4(x, bh, q0 + iq, k & ~3);
-  uint32_t all = 0;
-  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0x00, 0xf, 0xf, false));
-  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0x55, 0xf, 0xf, false)) << 4;
-  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0xaa, 0xf, 0xf, false)) << 8;
-  all |= static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(nib), 0xff, 0xf, 0xf, false)) << 12;
-  // bit 4t + iq: query q0 + t, key (k & ~3) + iq = k
-  return all >> iq;
-}
-
-// Dropout factor of the single pair (bh, q, k).
-__device__ __forceinline__ float drop1(const AttnX& x, int bh, int q, int k) {
-  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k) >> 2, static_cast<uint32_t>(q),
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k >> 3), static_cast<uint32_t>(q0 + iq),
                                       static_cast<uint32_t>(bh), 0u},
                                 x.seed0, x.seed1);
-  const int t = k & 3;
-  const uint32_t v = t == 0 ? r.x : (t == 1 ? r.y : (t == 2 ? r.z : r.w));
-  return v >= x.thresh ? x.keep_scale : 0.f;
+  const bool upper = (k >> 2) & 1;  // keys +4..7 of the group: words 2, 3
+  const int wa = static_cast<int>(upper ? r.z : r.x), wb = static_cast<int>(upper ? r.w : r.y);
+  const int sh = 16 * (iq & 1);
+  const bool second = (iq >> 1) != 0;  // this lane's draw is in the second of the two words
+  uint32_t res = 0;
+  auto bit = [&](int a, int b) {
+    const uint32_t w = static_cast<uint32_t>(second ? b : a);
+    return static_cast<uint32_t>(((w >> sh) & 0xffffu) >= x.thresh);
+  };
+  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0x00, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0x00, 0xf, 0xf, false));
+  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0x55, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0x55, 0xf, 0xf, false)) << 4;
+  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0xaa, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0xaa, 0xf, 0xf, false)) << 8;
+  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0xff, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0xff, 0xf, 0xf, false)) << 12;
+  return res;
 }
 
 // Launch map of a per-(b, h) block work list whose lists differ in length.

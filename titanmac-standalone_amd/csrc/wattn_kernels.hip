@@ -295,16 +295,9 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         const int kh = ks >> 1, j0 = 8 * (ks & 1);
-        // dropout factors of the 8 keys: two groups of 4 consecutive keys
+        // dropout factors of the 8 keys: 16ks + 4h + 0..3 and 16ks + 8 + 4h + 0..3
         float z[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
-        if constexpr (DR) {
-          float z4[4];
-          const int k0 = kt * 64 + 32 * kh + 8 * (j0 >> 2) + 4 * h;
-          drop4(ax, bh, q_row, k0, z4);
-          z[0] = z4[0]; z[1] = z4[1]; z[2] = z4[2]; z[3] = z4[3];
-          drop4(ax, bh, q_row, k0 + 8, z4);
-          z[4] = z4[0]; z[5] = z4[1]; z[6] = z4[2]; z[7] = z4[3];
-        }
+        if constexpr (DR) drop_row8(ax, bh, q_row, kt * 64 + 16 * ks, h, z);
         uint32_t w[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -539,15 +532,16 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_fwd_f32m_kernel(
         }
       l_run += xor32_add((r4[0] + r4[1]) + (r4[2] + r4[3]));
       if constexpr (DR) {
-        // P ⊙ Z for O: the factors of four consecutive keys per draw
+        // P ⊙ Z for O: elements 8m + t and 8m + 4 + t are keys 16m + 4h + t and
+        // 16m + 8 + 4h + t of the half
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float z4[4];
-            drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * g + 4 * h, z4);
+          for (int m = 0; m < 2; ++m) {
+            float z8[8];
+            drop_row8(ax, bh, q_row, kt * 64 + 32 * kh + 16 * m, h, z8);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) st[kh][4 * g + t] *= z4[t];
+            for (int t = 0; t < 8; ++t) st[kh][8 * m + t] *= z8[t];
           }
       }
 #pragma unroll
@@ -1273,12 +1267,13 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
           apply_bits(s, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
         }
 #pragma unroll
-        for (int jg = 0; jg < 4; ++jg) {
-          float z[4] = {1.f, 1.f, 1.f, 1.f};
-          if constexpr (DR) drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * jg + 4 * h, z);
+        for (int m = 0; m < 2; ++m) {
+          // elements 8m + t and 8m + 4 + t: keys 16m + 4h + t and 16m + 8 + 4h + t of the half
+          float z[8] = {1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f, 1.f};
+          if constexpr (DR) drop_row8(ax, bh, q_row, kt * 64 + 32 * kh + 16 * m, h, z);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int j = 4 * jg + t;
+          for (int t = 0; t < 8; ++t) {
+            const int j = 8 * m + t;
             const float pj = __builtin_amdgcn_exp2f(fmaf(s[j], sc, -l2));
             dp[j] = DR ? pj * (z[t] * dp[j] - dl) : pj * (dp[j] - dl);
           }
@@ -1479,12 +1474,12 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_f32m_kernel(
         }
         if constexpr (DR) {
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            float z4[4];
-            drop4(ax, bh, q_row, kt * 64 + 32 * kh + 8 * g + 4 * h, z4);
+          for (int m = 0; m < 2; ++m) {
+            float z8[8];
+            drop_row8(ax, bh, q_row, kt * 64 + 32 * kh + 16 * m, h, z8);
 #pragma unroll
-            for (int t = 0; t < 4; ++t)
-              st[4 * g + t] = __builtin_amdgcn_exp2f(st[4 * g + t] - l2) * (z4[t] * dpt[4 * g + t] - dl);
+            for (int t = 0; t < 8; ++t)
+              st[8 * m + t] = __builtin_amdgcn_exp2f(st[8 * m + t] - l2) * (z8[t] * dpt[8 * m + t] - dl);
           }
         } else {
 #pragma unroll
@@ -1926,9 +1921,11 @@ int make_attn_x(const tmac_attn_opts* o, int B, int H, int S, AttnX* x, int* fea
   if (!(o->dropout_p >= 0.f && o->dropout_p < 1.f)) return TMAC_ERR_VALUE;
   if (o->dropout_p > 0.f) {
     *feat |= kFeatDrop;
-    const double th = static_cast<double>(o->dropout_p) * 4294967296.0;
-    x->thresh = th >= 4294967295.0 ? 0xffffffffu : static_cast<uint32_t>(th);
-    x->keep_scale = 1.f / (1.f - o->dropout_p);
+    // 16-bit draws: dropped below floor(p * 2^16); kept ones scaled by the inverse
+    // of the exact keep probability
+    const double th = floor(static_cast<double>(o->dropout_p) * 65536.0);
+    x->thresh = th >= 65535.0 ? 65535u : static_cast<uint32_t>(th);
+    x->keep_scale = 65536.f / static_cast<float>(65536u - x->thresh);
     x->seed0 = static_cast<uint32_t>(o->dropout_seed);
     x->seed1 = static_cast<uint32_t>(o->dropout_seed >> 32);
   }

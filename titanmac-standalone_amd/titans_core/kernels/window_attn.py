@@ -533,7 +533,8 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
     pattern, block_size are then unused), as in WindowedAttention.forward
     (:307-315). Rows with no allowed key give 0. No gradient flows to the mask.
     dropout_p: attention dropout after the softmax (kept probabilities scaled by
-    1 / (1 - p)); seed: its Philox seed (default: drawn from torch's CPU
+    the inverse of the keep probability, 1 / (1 - p) to within 2^-16); seed: its
+    Philox seed (default: drawn from torch's CPU
     generator), reused by the backward.
     """
     S = q.shape[2]
