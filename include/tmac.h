@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 5
+#define TMAC_ABI_VERSION 6
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -153,6 +153,15 @@ int tmac_bell_gelu_bwd_workspace(int M, int N, size_t* ws_bytes);
 int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_Z, int64_t ldz, void* d_gZ,
                        int64_t ldgz, float* d_dbias, void* d_ws, size_t ws_bytes, int M, int N,
                        int dtype, void* stream);
+
+/* Bias gradient of a Block-ELL linear without activation (fc2):
+ * dbias[n] = Σ_m gY[m][n] in fp32 over a [M, N] row-major 16-bit gradient (N and
+ * the pitch multiples of 8), summed in a fixed order (deterministic; 0 when
+ * M = 0). Replaces the bias gradient of F.linear in MLPBlock's backward
+ * (blocks/mlp.py:64). d_ws: tmac_bell_gelu_bwd_workspace(M, N) bytes. dtype:
+ * TMAC_BF16 or TMAC_F16. */
+int tmac_bell_bias_grad(const void* d_gY, int64_t ldgy, float* d_dbias, void* d_ws,
+                        size_t ws_bytes, int M, int N, int dtype, void* stream);
 
 /* Input gradient: dX[M, K] = dY[M, N] · Wᵀ, fp32 accumulation.
  * Replaces autograd's grad_input of F.linear in the MLP backward

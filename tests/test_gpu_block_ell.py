@@ -376,6 +376,23 @@ def test_gelu_bwd_and_bias_grad(dev, dtype, M, N):
     assert torch.equal(gz3, gz) and db3.numel() == 0
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N", [(0, 64), (1, 64), (257, 192), (32768, 640)])
+def test_bias_grad_column_sums(dev, dtype, M, N):
+    """tmac_bell_bias_grad: fp32 column sums of a 16-bit gradient against the fp64 sum,
+    bit-identical on a rerun, and 0 for no rows; a row-strided view gives the same bits."""
+    g = torch.Generator().manual_seed(M + 3 * N)
+    gy = torch.randn(M, N, generator=g).to(dtype)
+    db = kb._bell_bias_grad(gy.to(dev))
+    want = gy.double().numpy().sum(0)
+    scale = 1.0 + np.abs(gy.double().numpy()).sum(0).max() if M else 1.0
+    assert db.dtype == torch.float32 and np.abs(db.cpu().numpy() - want).max() <= 1e-5 * scale
+    assert torch.equal(db, kb._bell_bias_grad(gy.to(dev)))
+    wide = torch.zeros(M, N + 64, dtype=dtype)
+    wide[:, :N] = gy
+    assert torch.equal(db, kb._bell_bias_grad(wide.to(dev)[:, :N]))
+
+
 def test_mlp_block_ell_bf16_training_fused_gelu(dev):
     """A bf16 Block-ELL MLP in training (fc1 + GELU through the kernel that also stores
     the pre-activation; GELU' and fc1's bias gradient in one pass): output and the

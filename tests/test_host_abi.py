@@ -209,6 +209,28 @@ def test_bell_fwd_argument_errors(lib):
     assert lib.tmac_bell_fwd(*bad) == -5          # ldx not a multiple of 8
 
 
+def test_bias_grad_argument_errors(lib):
+    """tmac_bell_bias_grad rejects bad arguments before any launch (no GPU needed)."""
+    ws = ctypes.c_size_t(0)
+    assert lib.tmac_bell_gelu_bwd_workspace(32768, 640, ctypes.byref(ws)) == 0
+    g = [FAKE, 640, FAKE, FAKE, ws.value, 32768, 640, 1, None]
+    for i, code in ((0, -1), (2, -1), (3, -1)):
+        bad = list(g); bad[i] = None
+        assert lib.tmac_bell_bias_grad(*bad) == code
+    bad = list(g); bad[6] = 644
+    assert lib.tmac_bell_bias_grad(*bad) == -2           # N % 8
+    bad = list(g); bad[1] = 600
+    assert lib.tmac_bell_bias_grad(*bad) == -2           # pitch < N
+    bad = list(g); bad[5] = -1
+    assert lib.tmac_bell_bias_grad(*bad) == -2
+    bad = list(g); bad[7] = 0
+    assert lib.tmac_bell_bias_grad(*bad) == -4           # 16-bit only
+    bad = list(g); bad[4] = ws.value - 1
+    assert lib.tmac_bell_bias_grad(*bad) == -6
+    bad = list(g); bad[0] = MISALIGNED
+    assert lib.tmac_bell_bias_grad(*bad) == -5
+
+
 def test_fused_gelu_argument_errors(lib):
     """tmac_bell_fwd_gelu_aux and tmac_bell_gelu_bwd reject bad arguments before
     any launch (no GPU needed)."""

@@ -851,7 +851,7 @@ __global__ __launch_bounds__(256) void bell_sddmm_reduce_kernel(const float* __r
 // a fixed order: deterministic for given (M, N). Grid (ceil(N / 512), parts).
 constexpr int kGeluParts = 256;  // at most this many row parts
 
-template <int DT>
+template <int DT, bool GELU = true>
 __global__ __launch_bounds__(256) void bell_gelu_bwd_kernel(
     const uint16_t* __restrict__ gA, int64_t lda, const uint16_t* __restrict__ Z, int64_t ldz,
     uint16_t* __restrict__ gZ, int64_t ldg, float* __restrict__ part, int M, int N,
@@ -874,11 +874,21 @@ __global__ __launch_bounds__(256) void bell_gelu_bwd_kernel(
       for (int u = 0; u < 4; ++u) {
         const int rr = min(r + 4 * u, r1 - 1);
         a[u] = ldg16(gA + static_cast<int64_t>(rr) * lda + col);
-        z[u] = ldg16(Z + static_cast<int64_t>(rr) * ldz + col);
+        if constexpr (GELU) z[u] = ldg16(Z + static_cast<int64_t>(rr) * ldz + col);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const bool valid = r + 4 * u < r1;
+        if constexpr (!GELU) {
+          // column sums of the gradient itself (a plain bias gradient)
+          const uint32_t aw[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[2 * i] += valid ? Mfma<DT>::to_f32(static_cast<uint16_t>(aw[i] & 0xffff)) : 0.f;
+            acc[2 * i + 1] += valid ? Mfma<DT>::to_f32(static_cast<uint16_t>(aw[i] >> 16)) : 0.f;
+          }
+          continue;
+        }
         const uint32_t aw[4] = {a[u].x, a[u].y, a[u].z, a[u].w};
         const uint32_t zw[4] = {z[u].x, z[u].y, z[u].z, z[u].w};
         uint32_t ow[4];
@@ -1196,4 +1206,32 @@ extern "C" int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_
     return launch_status();
   }
   return TMAC_OK;
+}
+
+extern "C" int tmac_bell_bias_grad(const void* d_gY, int64_t ldgy, float* d_dbias, void* d_ws,
+                                   size_t ws_bytes, int M, int N, int dtype, void* stream) {
+  if ((M > 0 && !d_gY) || !d_dbias || !d_ws) return TMAC_ERR_NULL;
+  if (M < 0 || N <= 0 || (N % 8) || ldgy < N) return TMAC_ERR_SHAPE;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (!aligned16(d_gY) || (ldgy % 8) || !aligned16(d_ws)) return TMAC_ERR_ALIGN;
+  int n_parts, rows;
+  gelu_parts(M, &n_parts, &rows);
+  if (ws_bytes < static_cast<size_t>(n_parts) * N * sizeof(float)) return TMAC_ERR_WORKSPACE;
+  auto* part = static_cast<float*>(d_ws);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (M > 0) {
+    const dim3 grid(static_cast<unsigned>((N + 511) / 512), static_cast<unsigned>(n_parts));
+    const auto* gY = static_cast<const uint16_t*>(d_gY);
+    if (dtype == TMAC_BF16)
+      hipLaunchKernelGGL((bell_gelu_bwd_kernel<TMAC_BF16, false>), grid, dim3(256), 0, s, gY, ldgy,
+                         nullptr, int64_t{0}, nullptr, int64_t{0}, part, M, N, rows);
+    else
+      hipLaunchKernelGGL((bell_gelu_bwd_kernel<TMAC_F16, false>), grid, dim3(256), 0, s, gY, ldgy,
+                         nullptr, int64_t{0}, nullptr, int64_t{0}, part, M, N, rows);
+    const int st = launch_status();
+    if (st != TMAC_OK) return st;
+  }
+  hipLaunchKernelGGL(column_sum_kernel, dim3(static_cast<unsigned>((N + 63) / 64)), dim3(256), 0, s,
+                     part, d_dbias, static_cast<int64_t>(N), M > 0 ? n_parts : 0, int64_t{0});
+  return launch_status();
 }

@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -46,6 +46,7 @@ SIGNATURES = {
                                _i, _i, _vp],
     "tmac_bell_gelu_bwd_workspace": [_i, _i, ctypes.POINTER(_sz)],
     "tmac_bell_gelu_bwd": [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _vp],
+    "tmac_bell_bias_grad": [_vp, _i64, _vp, _vp, _sz, _i, _i, _i, _vp],
     "tmac_bell_dx": [_vp, _i64, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_sddmm_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
     "tmac_bell_sddmm": [_vp, _i64, _vp, _i64, _vp, _vp, _i, _vp, _sz, _i, _i, _i, _i, _i, _vp],

@@ -244,6 +244,25 @@ def _bell_gelu_bwd(ga: torch.Tensor, z: torch.Tensor, with_bias: bool) -> Tuple[
 bell_gelu_bwd = torch.library.custom_op("titanmac::bell_gelu_bwd", mutates_args=())(_bell_gelu_bwd)
 
 
+def _bell_bias_grad(gy: torch.Tensor) -> torch.Tensor:
+    """fp32 column sums of a 16-bit [M, N] gradient (rows at a pitch that is a
+    multiple of 8): the bias gradient of a linear layer, summed in a fixed order."""
+    import ctypes
+    M, N = gy.shape
+    dev = _lib.require_device(gy, what="bell_bias_grad")
+    g2, ldg = _rows(gy, N)
+    L = _lib.lib()
+    nb = ctypes.c_size_t(0)
+    _lib.check(L.tmac_bell_gelu_bwd_workspace(M, N, ctypes.byref(nb)), "tmac_bell_gelu_bwd_workspace")
+    ws = torch.empty(max(1, (nb.value + 15) // 16 * 4), dtype=torch.float32, device=dev)
+    db = torch.empty(N, dtype=torch.float32, device=dev)
+    with _lib.device_guard(dev):
+        rc = L.tmac_bell_bias_grad(_lib.ptr(g2), ldg, _lib.ptr(db), _lib.ptr(ws), ws.numel() * 4, M,
+                                   N, _lib.dtype_code(gy.dtype), _lib.stream_ptr(dev))
+    _lib.check(rc, "tmac_bell_bias_grad")
+    return db
+
+
 @bell_gelu_bwd.register_fake
 def _(ga, z, with_bias):
     return z.new_empty(z.shape), z.new_empty((z.shape[-1],) if with_bias else (0,), dtype=torch.float32)
@@ -354,7 +373,11 @@ def _fwd_backward(ctx, gy):
         gv = (_bell_sddmm if direct else bell_sddmm)(x, gy.to(x.dtype), col_idx, n_brow, width,
                                                      values.dtype)
     if ctx.has_bias and ctx.needs_input_grad[7]:
-        gb = gy.reshape(-1, gy.shape[-1]).sum(0)
+        g2 = gy.reshape(-1, gy.shape[-1])
+        if g2.dtype in (torch.bfloat16, torch.float16) and g2.shape[-1] % 8 == 0:
+            gb = _bell_bias_grad(g2).to(g2.dtype)  # fixed-order fp32 column sums
+        else:
+            gb = g2.sum(0)
     return gx, gv, None, None, None, None, None, gb, None
 
 
