@@ -380,31 +380,45 @@ __device__ __forceinline__ void drop_row8(const AttnX& x, int bh, int q, int bas
   for (int i = 0; i < 8; ++i)
     z[i] = ((w[i >> 1] >> (16 * (i & 1))) & 0xffffu) >= x.thresh ? x.keep_scale : 0.f;
 }
-// Keep bits of a lane that holds key k and the four queries q0..q0+3 (q0 a
-// multiple of 4), where the four lanes of its quad (lane & ~3 .. +3, all active,
-// iq = lane & 3 = k & 3) hold keys with the same k / 4: bit 4t of the result is
-// the decision of (q0 + t, k). Lane iq draws the eight keys of k's group at query
-// q0 + iq; the quad's keys use two of its four words (draws 4·((k / 4) % 2) +
-// 0..3), which DPP broadcasts hand to every lane of the quad, so each call serves
-// four decisions of the quad.
-__device__ __forceinline__ uint32_t keep_quad(const AttnX& x, int bh, int q0, int k, int iq) {
-  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k >> 3), static_cast<uint32_t>(q0 + iq),
+// Keep bits of a lane that holds key k and two groups of four queries, qa..qa+3
+// and qb..qb+3 (multiples of 4), where the eight lanes of its octet (lane & ~7 ..
+// +7, all active, j = lane & 7 = k & 7) hold the eight keys of k's group with the
+// same qa, qb: bit 4t of the result is the decision of (qa + t, k), bit 16 + 4t
+// that of (qb + t, k). Lane j draws k's group at query qa + j (j < 4) or
+// qb + j - 4 (j >= 4), so the octet's eight calls cover its 64 decisions. A lane
+// of the lower quad (keys +0..3) needs words 0 and 1 of every draw, one of the
+// upper quad words 2 and 3: each lane hands the other quad's two words to its
+// partner lane j ^ 4, and DPP broadcasts within the quad spread them.
+__device__ __forceinline__ uint32_t keep_octet2(const AttnX& x, int bh, int qa, int qb, int k, int j) {
+  const int q = j < 4 ? qa + j : qb + j - 4;
+  const U32x4 r = philox4x32_10(U32x4{static_cast<uint32_t>(k >> 3), static_cast<uint32_t>(q),
                                       static_cast<uint32_t>(bh), 0u},
                                 x.seed0, x.seed1);
-  const bool upper = (k >> 2) & 1;  // keys +4..7 of the group: words 2, 3
-  const int wa = static_cast<int>(upper ? r.z : r.x), wb = static_cast<int>(upper ? r.w : r.y);
-  const int sh = 16 * (iq & 1);
-  const bool second = (iq >> 1) != 0;  // this lane's draw is in the second of the two words
-  uint32_t res = 0;
-  auto bit = [&](int a, int b) {
-    const uint32_t w = static_cast<uint32_t>(second ? b : a);
+  const bool upper = j >= 4;
+  const int own0 = static_cast<int>(upper ? r.z : r.x), own1 = static_cast<int>(upper ? r.w : r.y);
+  const int cross0 = __shfl_xor(static_cast<int>(upper ? r.x : r.z), 4);
+  const int cross1 = __shfl_xor(static_cast<int>(upper ? r.y : r.w), 4);
+  const int sh = 16 * (j & 1);
+  const bool second = (j & 2) != 0;  // this lane's draw is in the second of its two words
+  auto bit = [&](int w0, int w1) {
+    const uint32_t w = static_cast<uint32_t>(second ? w1 : w0);
     return static_cast<uint32_t>(((w >> sh) & 0xffffu) >= x.thresh);
   };
-  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0x00, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0x00, 0xf, 0xf, false));
-  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0x55, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0x55, 0xf, 0xf, false)) << 4;
-  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0xaa, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0xaa, 0xf, 0xf, false)) << 8;
-  res |= bit(__builtin_amdgcn_mov_dpp(wa, 0xff, 0xf, 0xf, false), __builtin_amdgcn_mov_dpp(wb, 0xff, 0xf, 0xf, false)) << 12;
-  return res;
+  // quad lane t of this lane's own quad drew group (upper ? b : a); via the
+  // exchange, the same lane holds the other quad's lane t draw, group (upper ? a : b)
+  uint32_t own = 0, other = 0;
+#define TMAC_OCTET_T(t, ctl)                                                                     \
+  own |= bit(__builtin_amdgcn_mov_dpp(own0, ctl, 0xf, 0xf, false),                               \
+             __builtin_amdgcn_mov_dpp(own1, ctl, 0xf, 0xf, false)) << (4 * (t));                  \
+  other |= bit(__builtin_amdgcn_mov_dpp(cross0, ctl, 0xf, 0xf, false),                           \
+               __builtin_amdgcn_mov_dpp(cross1, ctl, 0xf, 0xf, false)) << (4 * (t));
+  TMAC_OCTET_T(0, 0x00)
+  TMAC_OCTET_T(1, 0x55)
+  TMAC_OCTET_T(2, 0xaa)
+  TMAC_OCTET_T(3, 0xff)
+#undef TMAC_OCTET_T
+  const uint32_t ga = upper ? other : own, gb = upper ? own : other;
+  return ga | (gb << 16);
 }
 
 // Launch map of a per-(b, h) block work list whose lists differ in length.

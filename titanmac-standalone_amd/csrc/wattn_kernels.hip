@@ -649,6 +649,14 @@ __device__ __forceinline__ void kv_half_update(f32x16& s, f32x16& dp, float sc, 
                                                const uint16_t* g_lds, f32x16 (&dkt)[D / 32],
                                                f32x16 (&dvt)[D / 32], TrRead tr) {
   // rows 32qh + 8g + 4h + 0..3 of the tile: LSE·log2e (and −Δ) as one 16-byte read each
+  uint32_t kq2[2] = {0u, 0u};  // keep bits of query groups (0, 1) and (2, 3)
+  if constexpr (DR) {
+#pragma unroll
+    for (int g2 = 0; g2 < 2; ++g2) {
+      const int qa = qbase + 32 * qh + 16 * g2 + 4 * h;
+      kq2[g2] = keep_octet2(ax, bh, qa, qa + 8, key, lane & 7);
+    }
+  }
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse_l + 32 * qh + 8 * g + 4 * h);
@@ -656,7 +664,7 @@ __device__ __forceinline__ void kv_half_update(f32x16& s, f32x16& dp, float sc, 
     if constexpr (DR) {
       const f32x4 d4 = *reinterpret_cast<const f32x4*>(ndl_l + 32 * qh + 8 * g + 4 * h);
       const float nd[4] = {d4.x, d4.y, d4.z, d4.w};
-      const uint32_t kq = keep_quad(ax, bh, qbase + 32 * qh + 8 * g + 4 * h, key, lane & 3);
+      const uint32_t kq = kq2[g >> 1] >> (16 * (g & 1));
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int j = 4 * g + t;
@@ -1658,12 +1666,20 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_f32m_kernel(
         } else if (kind == 2) {
           apply_bits(s, span_bits32(span, qt * 64 + 32 * qh + 4 * h));
         }
+        uint32_t kq2[2] = {0u, 0u};  // keep bits of query groups (0, 1) and (2, 3)
+        if constexpr (DR) {
+#pragma unroll
+          for (int g2 = 0; g2 < 2; ++g2) {
+            const int qa = qt * 64 + 32 * qh + 16 * g2 + 4 * h;
+            kq2[g2] = keep_octet2(ax, bh, qa, qa + 8, key, lane & 7);
+          }
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2_l + 32 * qh + 8 * g + 4 * h);
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(dl_l + 32 * qh + 8 * g + 4 * h);
           uint32_t kq = 0;
-          if constexpr (DR) kq = keep_quad(ax, bh, qt * 64 + 32 * qh + 8 * g + 4 * h, key, lane & 3);
+          if constexpr (DR) kq = kq2[g >> 1] >> (16 * (g & 1));
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const float pj = __builtin_amdgcn_exp2f(s[4 * g + t] - l4[t]);
