@@ -1107,8 +1107,11 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
 // 16 keys per lane), then dQᵀ += Kᵀ·dSᵀ with Kᵀ read by transpose reads in the
 // accumulator's permuted key order.
 // FEAT as for the forward: with kFeatDrop, dS = P ⊙ (Z ⊙ dP − Δ).
+// Three workgroups per CU at D ≤ 64 (≤ 168 VGPRs): the caller-mask variants
+// would otherwise take 169–174 and drop to two; with mask and dropout the cap
+// costs four spilled VGPRs and still runs faster.
 template <int DT, int D, int FEAT = 0>
-__global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O, int64_t osb, int64_t osh,
     int64_t oss, const float* __restrict__ lse, float* __restrict__ delta,
