@@ -313,7 +313,9 @@ __host__ __device__ inline U32x4 philox4x32_10(U32x4 c, uint32_t k0, uint32_t k1
 // Extra features of the attention kernels (template flag bits): a caller's mask
 // tensor instead of the band / block-window pattern (kFeatMask), attention dropout
 // (kFeatDrop).
-constexpr int kFeatMask = 1, kFeatDrop = 2;
+// kFeatBool (with kFeatMask): the mask is boolean, so no slice takes a bias
+// (kind 3) and the kernels leave that path out; it holds about 20 VGPRs.
+constexpr int kFeatMask = 1, kFeatDrop = 2, kFeatBool = 4;
 
 struct AttnX {
   const void* mask;      // TMAC_MASK_BOOL: uint8 (0 = masked); TMAC_MASK_ADD_F32: fp32 added to the scores

@@ -99,17 +99,21 @@ struct Tile {
   static constexpr int kDt = D / 32;      // 32-wide head-dimension tiles of an output
 };
 
-// Four workgroups per CU at D <= 64 (at most 128 VGPRs, 36 KB of LDS each), two at D = 128
-// and with a mask or dropout (whose extra state would spill at 128 VGPRs).
+// Four workgroups per CU at D <= 64 (at most 128 VGPRs, 36 KB of LDS each); with
+// dropout or a bool mask three (their extra state would spill at 128 VGPRs); two at
+// D = 128 and with an additive mask (whose bias path takes about 180 VGPRs).
 //
-// FEAT (kFeatMask, kFeatDrop bits, tmac_device.h): with kFeatMask the caller's mask
+// FEAT (kFeatMask, kFeatDrop, kFeatBool bits, tmac_device.h): with kFeatMask the caller's mask
 // tensor replaces the pattern (work lists built from it on the device, partial
 // slices masked element by element from the tensor, scores kept in log2 units
 // with the mask's bias added); with kFeatDrop each probability that enters O·V is
 // kept with probability 1 - p and scaled by 1 / (1 - p) (Philox draws), while the
 // row sum takes the undropped probabilities (dropout follows the softmax).
 template <int DT, int D, int FEAT = 0>
-__global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_mfma_kernel(
+__global__ __launch_bounds__(256, D > 64 ? 2
+                                  : FEAT == 0 ? 4
+                                  : ((FEAT & kFeatMask) && !(FEAT & kFeatBool)) ? 2 : 3)
+void wattn_fwd_mfma_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     uint16_t* __restrict__ O, float* __restrict__ lse, int64_t qsb, int64_t qsh, int64_t qss,
     int64_t ksb, int64_t ksh, int64_t kss, int64_t vsb, int64_t vsh, int64_t vss, int64_t osb,
@@ -254,7 +258,7 @@ __global__ __launch_bounds__(256, (D > 64 || FEAT != 0) ? 2 : 4) void wattn_fwd_
           const uint64_t w = wb >> (4 * h);
           apply_bits(st[0], static_cast<uint32_t>(w));
           apply_bits(st[1], static_cast<uint32_t>(w >> 32));
-        } else if (kind == 3) {
+        } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -492,7 +496,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_fwd_f32m_kernel(
           const uint64_t w = wb >> (4 * h);
           apply_bits(st[0], static_cast<uint32_t>(w));
           apply_bits(st[1], static_cast<uint32_t>(w >> 32));
-        } else if (kind == 3) {
+        } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
           for (int kh = 0; kh < 2; ++kh)
 #pragma unroll
@@ -856,7 +860,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_kernel(
           s *= scale_log2;
           if (kind == 2) {
             apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
-          } else if (kind == 3) {
+          } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
@@ -1068,7 +1072,7 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
 #pragma unroll
           for (int qh = 0; qh < 2; ++qh)
             apply_bits(s2[qh], static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
-        } else if (kind == 3) {
+        } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
           for (int qh = 0; qh < 2; ++qh)
 #pragma unroll
@@ -1267,7 +1271,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
           s *= scale_log2;
           if (kind == 2) {
             apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * kh)));
-          } else if (kind == 3) {
+          } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
@@ -1473,7 +1477,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_f32m_kernel(
         if constexpr (CM) {
           if (kind == 2) {
             apply_bits(st, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * kh)));
-          } else if (kind == 3) {
+          } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int key = kt * 64 + 32 * kh + 8 * (j >> 2) + 4 * h + (j & 3);
@@ -1659,7 +1663,7 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_kv_f32m_kernel(
         if constexpr (CM) {
           if (kind == 2) {
             apply_bits(s, static_cast<uint32_t>((wb >> (4 * h)) >> (32 * qh)));
-          } else if (kind == 3) {
+          } else if (!(FEAT & kFeatBool) && kind == 3) {
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
               const int qr = qt * 64 + 32 * qh + 8 * (j >> 2) + 4 * h + (j & 3);
@@ -1961,6 +1965,7 @@ int make_attn_x(const tmac_attn_opts* o, int B, int H, int S, AttnX* x, int* fea
     if (!o->d_mask_ws || o->mask_ws_bytes < w.total) return TMAC_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(o->d_mask_ws) & 255u) return TMAC_ERR_ALIGN;
     *feat |= kFeatMask;
+    if (o->mask_format == TMAC_MASK_BOOL) *feat |= kFeatBool;
     x->mask = o->d_mask;
     x->fmt = o->mask_format;
     x->msb = o->mask_strides[0];
@@ -2189,7 +2194,9 @@ int launch_status(const AttnLaunch& a, int feat, bool bwd) {
     case 0: dispatch<0>(a, bwd); break;
     case kFeatMask: dispatch<kFeatMask>(a, bwd); break;
     case kFeatDrop: dispatch<kFeatDrop>(a, bwd); break;
-    default: dispatch<kFeatMask | kFeatDrop>(a, bwd); break;
+    case kFeatMask | kFeatDrop: dispatch<kFeatMask | kFeatDrop>(a, bwd); break;
+    case kFeatMask | kFeatBool: dispatch<kFeatMask | kFeatBool>(a, bwd); break;
+    default: dispatch<kFeatMask | kFeatDrop | kFeatBool>(a, bwd); break;
   }
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
