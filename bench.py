@@ -114,6 +114,7 @@ def gen(shape, seed, scale=1.0, dtype=torch.bfloat16):
 # ---------------------------------------------------------------------------
 
 def setup_spmm(dev):
+    from titans_core.kernels import block_ell as kbe
     c = CFG2
     pat = BlockELLPattern.sample(c["seed"], c["n_brow"], c["n_bcol"], c["width"])
     K, N = BS * c["n_brow"], BS * c["n_bcol"]
@@ -127,8 +128,20 @@ def setup_spmm(dev):
     args = (_lib.ptr(X), K, _lib.ptr(V), _lib.ptr(idx["t_ptr"]), _lib.ptr(idx["t_row"]),
             _lib.ptr(idx["t_vblk"]), _lib.ptr(idx["order"]), _lib.ptr(None), _lib.ptr(Y), N,
             c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
+    # the headline path: the grouped forward (block-column pairs sharing block-rows, one
+    # activation-tile copy per union step), what block_ell_mm runs at this shape
+    ga = kbe._grouped_args(idx["grp"], c["M"], K, c["n_bcol"], torch.bfloat16)
+    assert ga is not None, "config 2 is expected to take the grouped forward"
+    gargs = (_lib.ptr(X), K, _lib.ptr(V), ga[0], ga[1], ga[2], ga[3], 2, _lib.ptr(None), _lib.ptr(Y),
+             N, c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
 
     def launch():
+        rc = L.tmac_bell_fwd_grouped(*gargs)
+        if rc:
+            _lib.check(rc, "tmac_bell_fwd_grouped")
+
+    # the per-block-column gather kernel on the same layer (secondary figure)
+    def launch_gather():
         rc = L.tmac_bell_fwd(*args)
         if rc:
             _lib.check(rc, "tmac_bell_fwd")
@@ -144,7 +157,8 @@ def setup_spmm(dev):
     nnz = c["n_brow"] * c["width"]
     flops = 2 * c["M"] * nnz * BS * BS
     bytes_ = c["M"] * K * 2 + nnz * BS * BS * 2 + (c["n_bcol"] + 1 + 2 * nnz + c["n_bcol"]) * 4 + c["M"] * N * 2
-    return dict(launch=launch, launch_m64=launch_m64, weight_bytes=nnz * BS * BS * 2, flops=flops,
+    return dict(launch=launch, launch_gather=launch_gather, launch_m64=launch_m64,
+                weight_bytes=nnz * BS * BS * 2, flops=flops,
                 bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu, keep=(X, V, Y, idx))
 
 
@@ -822,6 +836,7 @@ def main() -> int:
                            bytes=spmm["bytes"])
         if args.mode == "all":
             out["spmm"]["dense_ms"] = dense_gemm_baseline(spmm, dev, K, stream)
+        out["spmm"]["gather_ms"] = timed(spmm["launch_gather"], K, W, stream)
         out["spmm"]["m64_ms"] = timed(spmm["launch_m64"], K, W, stream)
         out["spmm"]["m64_weight_tbs"] = spmm["weight_bytes"] / out["spmm"]["m64_ms"] / 1e9
     if args.mode in ("all", "attn", "attn_bwd"):
@@ -976,6 +991,7 @@ def main() -> int:
             "windowed_attn_bwd_dropout0.1_ms": round(out["attn_ex"]["dropout"]["bwd_ms"], 5),
             "windowed_attn_fwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["fwd_ms"], 5),
             "windowed_attn_bwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["bwd_ms"], 5),
+            "bell_fwd_cfg2_gather_kernel_ms": round(out["spmm"]["gather_ms"], 5),
             "bell_fwd_cfg2_m64_us": round(out["spmm"]["m64_ms"] * 1e3, 2),
             "bell_fwd_cfg2_m64_weight_tbs": round(out["spmm"]["m64_weight_tbs"], 3),
             "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),

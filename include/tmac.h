@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 6
+#define TMAC_ABI_VERSION 7
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -104,6 +104,24 @@ int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_bcol, int wi
                         int32_t* h_t_ptr, int32_t* h_t_row, int32_t* h_t_vblk,
                         int32_t* h_order);
 
+/* Grouped schedule of the gather GEMM (host, deterministic). The output blocks
+ * (block-columns for dir = 0, the forward; block-rows for dir = 1, dX) are
+ * grouped `group` at a time (2 or 4) so that the members share many list
+ * entries: greedily, each group seeded by the longest remaining list (lowest
+ * index on ties) and filled with the remaining output sharing the most entries
+ * with the group so far (then fewest new entries, then lowest index). A
+ * group's steps are the union of its members' lists, ascending by input block;
+ * step record = {input block, value block of member 0 .. group-1 or -1}, so a
+ * member's active steps are its own list in its own order. Groups are listed
+ * longest first. Output: h_grp_ptr [n_groups + 1] (step offsets), h_grp_out
+ * [n_groups * group] (member output blocks, -1 pads the last group), h_steps
+ * [capacity * (1 + group)]; capacity >= n_brow * width always suffices.
+ * n_groups = ceil(n_out / group). No counterpart in the reference (its MLP is
+ * dense); it serves tmac_bell_fwd_grouped. */
+int tmac_bell_group_schedule(const int32_t* h_col_idx, int n_brow, int n_bcol, int width, int dir,
+                             int group, int32_t* h_grp_ptr, int32_t* h_grp_out, int32_t* h_steps,
+                             int capacity, int* n_groups, int* n_steps);
+
 /* ------------------------------------------------------------------------- */
 /* Block-ELL kernels (device).                                                */
 /* ------------------------------------------------------------------------- */
@@ -137,6 +155,29 @@ int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
                            const int32_t* d_t_vblk, const int32_t* d_order,
                            const void* d_bias, void* d_Y, int64_t ldy, void* d_Z, int64_t ldz,
                            int M, int n_brow, int n_bcol, int width, int dtype, void* stream);
+
+/* The same forward as tmac_bell_fwd (replacing `self.fc1(x)` / `self.fc2(hidden)`
+ * of MLPBlock.forward, blocks/mlp.py:58,64) through the grouped schedule:
+ * pairs of block-columns sharing many block-rows, one activation-tile copy per
+ * union step instead of one per stored block (-30% copied bytes at config 2),
+ * persistent 512-row tiles. Bitwise-identical to tmac_bell_fwd (each output is
+ * summed over its own list in the same order). 16-bit only; group must be 2;
+ * d_grp_ptr/d_grp_out/d_steps: device copies of tmac_bell_group_schedule(dir 0,
+ * group 2); ldx <= 2^22. Faster than tmac_bell_fwd once ceil(M/512) *
+ * n_groups fills the GPU (>= 256 tiles); the Python wrapper chooses. */
+int tmac_bell_fwd_grouped(const void* d_X, int64_t ldx, const void* d_vals,
+                          const int32_t* d_grp_ptr, const int32_t* d_grp_out,
+                          const int32_t* d_steps, int n_groups, int group, const void* d_bias,
+                          void* d_Y, int64_t ldy, int M, int n_brow, int n_bcol, int width,
+                          int dtype, int epi, void* stream);
+
+/* tmac_bell_fwd_gelu_aux through the grouped schedule (Y = gelu(Z), Z kept). */
+int tmac_bell_fwd_grouped_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
+                                   const int32_t* d_grp_ptr, const int32_t* d_grp_out,
+                                   const int32_t* d_steps, int n_groups, int group,
+                                   const void* d_bias, void* d_Y, int64_t ldy, void* d_Z,
+                                   int64_t ldz, int M, int n_brow, int n_bcol, int width,
+                                   int dtype, void* stream);
 
 /* Bytes of device workspace tmac_bell_gelu_bwd needs for the bias gradient. */
 int tmac_bell_gelu_bwd_workspace(int M, int N, size_t* ws_bytes);

@@ -300,6 +300,318 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
   }
 }
 
+// Grouped gather GEMM, forward (16-bit). bell_gemm_kernel copies an activation
+// tile once per stored weight block, i.e. once for every output block-column
+// that uses it, and those L2 -> LDS copies (2.1 GB at config 2) are what bound
+// it. Here the output block-columns are grouped in pairs on the host so that the
+// two members share many block-rows (tmac_bell_group_schedule), and a workgroup
+// walks the union of the pair's lists, ascending by block-row: per union step
+// the activation tile is copied once and used by each member holding a block
+// there. A member's active steps are its own list in its own order, so each
+// output is summed exactly as in bell_gemm_kernel (bitwise-identical results).
+//
+// Tiles are 512 rows by 2 block-columns; 8 waves, wave w owns rows
+// 128 (w % 4) .. +127 of member w / 4 (4 x 2 MFMA tiles, 32 MFMAs per step),
+// so the two waves on each SIMD cover both members and every SIMD gets the
+// same MFMA work per step.
+//
+// Copies: global_load_lds (1 KB per wave instruction, eight lanes per 128-byte
+// row) written as assembly with an SGPR base and per-lane 32-bit offsets fixed
+// for the tile, into a two-stage ring (activation tile 64 KB + two weight
+// slots 16 KB per stage, all of LDS). Each wave copies 64 rows of the
+// activation tile and, when its member is active, 16 rows of that member's
+// weight block; the next step's copies go out right after the barrier that
+// opens a step, and each wave waits for its own copies with an exact vmcnt
+// before the next barrier.
+//
+// Persistent: workgroup b runs on XCD b % 8 and walks that XCD's share of the
+// logical tiles (slab-major, longest group first) round-robin. After a tile's
+// last step it issues the next tile's first copies and only then converts and
+// stores the finished tile, staged through the activation stage the next tile
+// does not use yet, so the stores drain while the next tile computes.
+constexpr int kGM = 512;  // output rows per grouped tile (4 waves x 128 per member)
+
+// s_waitcnt vmcnt(n) for a run-time n in 0..31 (exact); larger n waits for 31.
+__device__ __forceinline__ void wait_vm_upto31(int n) {
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 25: asm volatile("s_waitcnt vmcnt(25)" ::: "memory"); break;
+    case 26: asm volatile("s_waitcnt vmcnt(26)" ::: "memory"); break;
+    case 27: asm volatile("s_waitcnt vmcnt(27)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
+    case 29: asm volatile("s_waitcnt vmcnt(29)" ::: "memory"); break;
+    case 30: asm volatile("s_waitcnt vmcnt(30)" ::: "memory"); break;
+    case 31: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(31)" ::: "memory"); break;
+  }
+}
+
+template <int DT, bool EPI>
+__global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
+    const int32_t* __restrict__ grp_ptr, const int32_t* __restrict__ grp_out,
+    const int32_t* __restrict__ steps, const uint16_t* __restrict__ bias, int epi,
+    uint16_t* __restrict__ Y, int64_t ldy, uint16_t* __restrict__ Z, int64_t ldz, int M,
+    int n_groups, int n_tiles, int per_xcd) {
+  constexpr int G = 2;                   // members per group
+  constexpr int kX = kGM * 64;           // activation tile, 16-bit elements (64 KB)
+  constexpr int kW = G * 4096;           // weight slots of a stage (16 KB)
+  constexpr int kRec = 1 + G;            // step record: block-row, G value blocks (-1: none)
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * kX + 2 * kW];
+
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, n_slots = gridDim.x >> 3;
+  const int t_end = min(n_tiles, (xcd + 1) * per_xcd);
+  int t = xcd * per_xcd + slot;
+  if (t >= t_end) return;
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int q = wave & 3, mem = wave >> 2;
+  const int l32 = lane & 31, h = lane >> 5;
+  const int grp = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile
+  const int drow = lane >> 3, dpos = lane & 7;
+  // Per-lane copy offsets (bytes). Lane L of an instruction covering rows
+  // R..R+7 fills LDS chunk position L & 7 of row R + L / 8 and fetches the
+  // global chunk that the swizzle stores there.
+  uint32_t woff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 16 * q + 8 * j + drow;
+    const int a = (row >> 1) & 7;
+    woff[j] = static_cast<uint32_t>(row * 128 + 16 * (dpos ^ (((a & 1) << 2) | (a >> 1))));
+  }
+  const uint32_t lds0 = lds_offset(smem);
+
+  // the current tile
+  int mtile = t / n_groups, gi = t - (t / n_groups) * n_groups;
+  int n_steps = grp_ptr[gi + 1] - grp_ptr[gi];
+  const int32_t* rec0 = steps + static_cast<int64_t>(grp_ptr[gi]) * kRec;
+  int m_tile0 = mtile * kGM;
+  // activation rows past M read row M-1 (valid memory, results never stored)
+  uint32_t xoff[8];
+  auto set_xoff = [&]() {
+    const int last = M - 1 - m_tile0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int row = 64 * wave + 8 * j + drow;
+      const int chunk = dpos ^ ((row >> 1) & 7);
+      xoff[j] = static_cast<uint32_t>(min(row, last)) * static_cast<uint32_t>(2 * lda) +
+                16u * static_cast<uint32_t>(chunk);
+    }
+  };
+  set_xoff();
+
+  // Step records of the current tile in VGPRs, 64 steps per window (lane L
+  // holds step 64k + L), read with readlane: no memory access on the per-step
+  // path. Two windows are resident, since the look-ahead crosses into the next.
+  int win_in0 = 0, win_in1 = 0, win_vb0 = -1, win_vb1 = -1;
+  auto load_window = [&](int k) {
+    const int j = min(64 * k + lane, n_steps - 1);
+    const int a = rec0[j * kRec], b = rec0[j * kRec + 1 + mem];
+    if (k & 1) {
+      win_in1 = a;
+      win_vb1 = b;
+    } else {
+      win_in0 = a;
+      win_vb0 = b;
+    }
+  };
+  auto step_in = [&](int i) {
+    return __builtin_amdgcn_readlane((i & 64) ? win_in1 : win_in0, i & 63);
+  };
+  // this wave's member's value block at step i (-1: the member has none there)
+  auto own_vb = [&](int i) {
+    return __builtin_amdgcn_readlane((i & 64) ? win_vb1 : win_vb0, i & 63);
+  };
+  // copies of step i of the current tile into ring stage gs & 1
+  auto issue = [&](int i, int gs) {
+    const uint32_t sx = lds0 + static_cast<uint32_t>((gs & 1) * kX * 2);
+    const uint16_t* xb = A + static_cast<int64_t>(m_tile0) * lda + static_cast<int64_t>(step_in(i)) * 64;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) dma_lds16(xb, xoff[j], sx + (64 * wave + 8 * j) * 128);
+    const int vb = own_vb(i);
+    if (vb >= 0) {
+      const uint32_t sw = lds0 + static_cast<uint32_t>((2 * kX + (gs & 1) * kW + mem * 4096) * 2);
+      const uint16_t* wb = vals + static_cast<int64_t>(vb) * 4096;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) dma_lds16(wb, woff[j], sw + (16 * q + 8 * j) * 128);
+    }
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
+  // MFMA operands of k-step kk: the wave's activation rows (B operand, 16-byte
+  // reads of the swizzled tile) and its member's weight block (A operand,
+  // transpose reads: W is N-contiguous but the reduction runs over K).
+  auto read_ops = [&](u32x4(&xa)[4], u32x4(&wf)[2], const uint16_t* xt, const uint16_t* wt, int kk) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) xa[mi] = lds16(xt + xswz(128 * q + 32 * mi + l32, 2 * kk + h));
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) wf[ni] = lds_read_tr8_swz64(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
+  };
+  // operand reads of k-step kk + 1 are issued before the MFMAs of k-step kk
+  auto compute = [&](const uint16_t* xt, const uint16_t* wt) {
+    u32x4 xa[2][4], wf[2][2];
+    read_ops(xa[0], wf[0], xt, wt, 0);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], xt, wt, kk + 1);
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+          acc[mi][ni] = Mfma<DT>::run(wf[kk & 1][ni], xa[kk & 1][mi], acc[mi][ni]);
+    }
+  };
+
+  int gs = 0;       // steps this workgroup has walked (ring parity)
+  int pending = 0;  // this wave's stores issued after the current tile's first copies
+  if (n_steps > 0) {
+    load_window(0);
+    if (n_steps > 64) load_window(1);
+    issue(0, 0);
+  }
+  for (;;) {
+    for (int i = 0; i < n_steps; ++i) {
+      // entering window k >= 1: fetch window k + 1 into the slot of window k - 1
+      if ((i & 63) == 0 && i > 0 && i + 64 < n_steps) load_window((i >> 6) + 1);
+      // This wave's copies of step i have landed once at most the previous
+      // tile's stores (step 0 only) are outstanding behind them: copies and
+      // stores complete in issue order.
+      wait_vm_upto31(i == 0 ? pending : 0);
+      // every wave's copies of step i are in LDS, and every wave is done with
+      // step i - 1, whose stage the next copies overwrite
+      asm volatile("s_barrier" ::: "memory");
+      if (i + 1 < n_steps) issue(i + 1, gs + i + 1);
+      if (own_vb(i) >= 0) compute(smem + ((gs + i) & 1) * kX, smem + 2 * kX + ((gs + i) & 1) * kW + mem * 4096);
+    }
+    gs += n_steps;
+    const int ob = grp_out[gi * G + mem];
+    const int m_out = m_tile0 + 128 * q;
+    const int64_t col0 = static_cast<int64_t>(ob) * 64;
+    // The bias of this lane's 32 columns, loaded and waited for before the
+    // next tile's copies are issued, so that no wait on it covers them.
+    u32x2 bb[2][4] = {};
+    if (EPI && bias && ob >= 0) {
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+        for (int jg = 0; jg < 4; ++jg)
+          bb[ni][jg] = *reinterpret_cast<const u32x2*>(bias + col0 + 32 * ni + 8 * jg + 4 * h);
+      asm volatile("" ::"v"(bb[0][0]), "v"(bb[0][1]), "v"(bb[0][2]), "v"(bb[0][3]), "v"(bb[1][0]),
+                   "v"(bb[1][1]), "v"(bb[1][2]), "v"(bb[1][3]));
+    }
+    // every wave is done with the ring before the next tile's copies go in
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    const int t_next = t + n_slots;
+    const bool more = t_next < t_end;
+    if (more) {
+      t = t_next;
+      mtile = t / n_groups;
+      gi = t - mtile * n_groups;
+      n_steps = grp_ptr[gi + 1] - grp_ptr[gi];
+      rec0 = steps + static_cast<int64_t>(grp_ptr[gi]) * kRec;
+      m_tile0 = mtile * kGM;
+      set_xoff();
+      if (n_steps > 0) {
+        load_window(0);
+        if (n_steps > 64) load_window(1);
+        issue(0, gs);
+      }
+    }
+    // Epilogue of the finished tile (block-column ob, rows m_out..m_out+127),
+    // one 32-row MFMA tile at a time: bias and activation in place, conversion,
+    // then through this wave's 4 KB of staging (32 rows x 64, chunks
+    // XOR-swizzled by row) in the activation stage the next tile's first step
+    // does not use, and out as 128-byte row segments. A store instruction is
+    // issued (and counted) only when some of its rows are in range.
+    uint16_t* stage = smem + ((gs + 1) & 1) * kX + wave * 2048;
+    int n_st = 0;
+    if (ob >= 0) {
+      auto stage_store = [&](const f32x16(&v)[2], int mi, uint16_t* out, int64_t ld) {
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+          for (int jg = 0; jg < 4; ++jg) {
+            u32x2 packed;
+            packed.x = Mfma<DT>::pack2(v[ni][4 * jg], v[ni][4 * jg + 1]);
+            packed.y = Mfma<DT>::pack2(v[ni][4 * jg + 2], v[ni][4 * jg + 3]);
+            const int chunk = 4 * ni + jg;
+            *reinterpret_cast<u32x2*>(stage + l32 * 64 + ((chunk ^ (l32 & 7)) << 3) + 4 * h) = packed;
+          }
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const int base = m_out + 32 * mi + 8 * it;
+          if (base < M) {
+            const int row = 8 * it + (lane >> 3), ch = lane & 7;
+            const u32x4 v4 = lds16(stage + row * 64 + ((ch ^ (row & 7)) << 3));
+            if (base + (lane >> 3) < M)
+              stg16(out + static_cast<int64_t>(base + (lane >> 3)) * ld + col0 + ch * 8, v4);
+            n_st += 1;
+          }
+        }
+      };
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        if (EPI && bias) {
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int jg = 0; jg < 4; ++jg) {
+              const u32x2 b2 = bb[ni][jg];
+              acc[mi][ni][4 * jg] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x & 0xffff));
+              acc[mi][ni][4 * jg + 1] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.x >> 16));
+              acc[mi][ni][4 * jg + 2] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y & 0xffff));
+              acc[mi][ni][4 * jg + 3] += Mfma<DT>::to_f32(static_cast<uint16_t>(b2.y >> 16));
+            }
+        }
+        if (EPI && Z) stage_store(acc[mi], mi, Z, ldz);
+        if (EPI && epi == TMAC_EPI_GELU) {
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) acc[mi][ni][j] = gelu_erf(acc[mi][ni][j]);
+        }
+        stage_store(acc[mi], mi, Y, ldy);
+      }
+    }
+    if (!more) break;
+    pending = n_st;
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
+  }
+}
+
 // Forward for few rows (M <= kSmallM: decoding, small batches). The gather GEMM
 // above gives such a call one 256-row tile per block-column and walks each list
 // one entry at a time, so it pays one memory latency per entry whatever M is.
@@ -1048,6 +1360,86 @@ extern "C" int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* 
   if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
   return bell_fwd_impl(d_X, ldx, d_vals, d_t_ptr, d_t_row, d_t_vblk, d_order, d_bias, d_Y, ldy,
                        d_Z, ldz, M, n_brow, n_bcol, width, dtype, TMAC_EPI_GELU, stream);
+}
+
+namespace {
+
+// Launch of the grouped forward: one persistent workgroup per CU (at most 32
+// per XCD), fewer when there are fewer tiles.
+int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, const int32_t* d_grp_ptr,
+                          const int32_t* d_grp_out, const int32_t* d_steps, int n_groups, int group,
+                          const void* d_bias, int epi, void* d_Y, int64_t ldy, void* d_Z, int64_t ldz,
+                          int M, int n_brow, int n_bcol, int width, int dtype, void* stream) {
+  if (!d_A || !d_vals || !d_grp_ptr || !d_grp_out || !d_steps || !d_Y) return TMAC_ERR_NULL;
+  int st = check_bell_shape(M, n_brow, n_bcol, width);
+  if (st != TMAC_OK) return st;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
+  if (group != 2) return TMAC_ERR_VALUE;
+  if (epi != TMAC_EPI_NONE && epi != TMAC_EPI_GELU) return TMAC_ERR_VALUE;
+  if (n_groups != (n_bcol + group - 1) / group) return TMAC_ERR_SHAPE;
+  const int64_t K = 64ll * n_brow, N = 64ll * n_bcol;
+  if (lda < K || ldy < N || (d_Z && ldz < N)) return TMAC_ERR_SHAPE;
+  // the copies address 512 activation rows with 32-bit byte offsets
+  if (lda > (1ll << 22)) return TMAC_ERR_SHAPE;
+  if (!aligned16(d_A) || !aligned16(d_vals) || !aligned16(d_Y) || (lda % 8) || (ldy % 8))
+    return TMAC_ERR_ALIGN;
+  if (d_bias && !aligned16(d_bias)) return TMAC_ERR_ALIGN;
+  if (d_Z && (!aligned16(d_Z) || (ldz % 8))) return TMAC_ERR_ALIGN;
+  if (M == 0) return TMAC_OK;
+  const int n_mtiles = (M + kGM - 1) / kGM;
+  const int64_t total = static_cast<int64_t>(n_mtiles) * n_groups;
+  if (total > (1ll << 30)) return TMAC_ERR_SHAPE;
+  const int per_xcd = static_cast<int>((total + 7) / 8);
+  const int grid = 8 * (per_xcd < 32 ? per_xcd : 32);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const auto* A = static_cast<const uint16_t*>(d_A);
+  const auto* V = static_cast<const uint16_t*>(d_vals);
+  const auto* b = static_cast<const uint16_t*>(d_bias);
+  auto* Y = static_cast<uint16_t*>(d_Y);
+  auto* Z = static_cast<uint16_t*>(d_Z);
+  // the epilogue's bias / activation / Z code is compiled only where used
+  const bool epi_any = b || Z || epi != TMAC_EPI_NONE;
+#define TMAC_GG_LAUNCH(DT, E)                                                                       \
+  hipLaunchKernelGGL((bell_ggemm_kernel<DT, E>), dim3(grid), dim3(512), 0, s, A, lda, V, d_grp_ptr, \
+                     d_grp_out, d_steps, b, epi, Y, ldy, Z, ldz, M, n_groups,                      \
+                     static_cast<int>(total), per_xcd)
+  if (dtype == TMAC_BF16) {
+    if (epi_any)
+      TMAC_GG_LAUNCH(TMAC_BF16, true);
+    else
+      TMAC_GG_LAUNCH(TMAC_BF16, false);
+  } else {
+    if (epi_any)
+      TMAC_GG_LAUNCH(TMAC_F16, true);
+    else
+      TMAC_GG_LAUNCH(TMAC_F16, false);
+  }
+#undef TMAC_GG_LAUNCH
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" int tmac_bell_fwd_grouped(const void* d_X, int64_t ldx, const void* d_vals,
+                                     const int32_t* d_grp_ptr, const int32_t* d_grp_out,
+                                     const int32_t* d_steps, int n_groups, int group,
+                                     const void* d_bias, void* d_Y, int64_t ldy, int M, int n_brow,
+                                     int n_bcol, int width, int dtype, int epi, void* stream) {
+  return bell_fwd_grouped_impl(d_X, ldx, d_vals, d_grp_ptr, d_grp_out, d_steps, n_groups, group,
+                               d_bias, epi, d_Y, ldy, nullptr, 0, M, n_brow, n_bcol, width, dtype,
+                               stream);
+}
+
+extern "C" int tmac_bell_fwd_grouped_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
+                                              const int32_t* d_grp_ptr, const int32_t* d_grp_out,
+                                              const int32_t* d_steps, int n_groups, int group,
+                                              const void* d_bias, void* d_Y, int64_t ldy, void* d_Z,
+                                              int64_t ldz, int M, int n_brow, int n_bcol, int width,
+                                              int dtype, void* stream) {
+  if (!d_Z) return TMAC_ERR_NULL;
+  return bell_fwd_grouped_impl(d_X, ldx, d_vals, d_grp_ptr, d_grp_out, d_steps, n_groups, group,
+                               d_bias, TMAC_EPI_GELU, d_Y, ldy, d_Z, ldz, M, n_brow, n_bcol, width,
+                               dtype, stream);
 }
 
 extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,

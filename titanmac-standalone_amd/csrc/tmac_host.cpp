@@ -123,6 +123,121 @@ extern "C" int tmac_bell_transpose(const int32_t* h_col_idx, int n_brow, int n_b
   return TMAC_OK;
 }
 
+extern "C" int tmac_bell_group_schedule(const int32_t* h_col_idx, int n_brow, int n_bcol,
+                                        int width, int dir, int group, int32_t* h_grp_ptr,
+                                        int32_t* h_grp_out, int32_t* h_steps, int capacity,
+                                        int* n_groups, int* n_steps) {
+  if (!h_grp_ptr || !h_grp_out || !h_steps || !n_groups || !n_steps) return TMAC_ERR_NULL;
+  if (dir != 0 && dir != 1) return TMAC_ERR_VALUE;
+  if (group != 2 && group != 4) return TMAC_ERR_VALUE;
+  const int st = tmac_bell_validate(h_col_idx, n_brow, n_bcol, width);
+  if (st != TMAC_OK) return st;
+  // Lists of (input block, value block) per output block, ascending by input:
+  // forward (dir 0): output block-column c, inputs = the block-rows holding a
+  // block in c; dX (dir 1): output block-row r, inputs = col_idx[r].
+  const int n_out = dir == 0 ? n_bcol : n_brow;
+  const int n_in = dir == 0 ? n_brow : n_bcol;
+  std::vector<std::vector<std::pair<int32_t, int32_t>>> lists(n_out);
+  for (int r = 0; r < n_brow; ++r)
+    for (int s = 0; s < width; ++s) {
+      const int c = h_col_idx[static_cast<size_t>(r) * width + s];
+      if (dir == 0)
+        lists[c].push_back({r, r * width + s});
+      else
+        lists[r].push_back({c, r * width + s});
+    }
+  // Input sets as bitsets, for the overlap counts of the greedy grouping.
+  const int words = (n_in + 63) / 64;
+  std::vector<uint64_t> bits(static_cast<size_t>(n_out) * words, 0);
+  for (int o = 0; o < n_out; ++o)
+    for (const auto& e : lists[o]) bits[static_cast<size_t>(o) * words + e.first / 64] |= 1ull << (e.first % 64);
+  auto popc = [](uint64_t x) { return __builtin_popcountll(x); };
+  // Greedy grouping: seed = the longest remaining list (lowest index on ties);
+  // then, until the group is full, add the remaining output sharing the most
+  // inputs with the group's union (fewest new inputs, then lowest index, on ties).
+  std::vector<char> used(n_out, 0);
+  std::vector<std::vector<int>> groups;
+  std::vector<uint64_t> uni(words);
+  int left = n_out;
+  while (left > 0) {
+    int seed = -1;
+    for (int o = 0; o < n_out; ++o)
+      if (!used[o] && (seed < 0 || lists[o].size() > lists[seed].size())) seed = o;
+    used[seed] = 1;
+    --left;
+    std::vector<int> g{seed};
+    std::copy(bits.begin() + static_cast<size_t>(seed) * words,
+              bits.begin() + static_cast<size_t>(seed + 1) * words, uni.begin());
+    while (static_cast<int>(g.size()) < group && left > 0) {
+      int best = -1, best_sh = -1, best_new = 0;
+      for (int o = 0; o < n_out; ++o) {
+        if (used[o]) continue;
+        int sh = 0, nw = 0;
+        for (int w = 0; w < words; ++w) {
+          const uint64_t b = bits[static_cast<size_t>(o) * words + w];
+          sh += popc(b & uni[w]);
+          nw += popc(b & ~uni[w]);
+        }
+        if (sh > best_sh || (sh == best_sh && nw < best_new)) {
+          best = o;
+          best_sh = sh;
+          best_new = nw;
+        }
+      }
+      used[best] = 1;
+      --left;
+      g.push_back(best);
+      for (int w = 0; w < words; ++w) uni[w] |= bits[static_cast<size_t>(best) * words + w];
+    }
+    groups.push_back(std::move(g));
+  }
+  // Union length of each group; groups are launched longest first.
+  const int ng = static_cast<int>(groups.size());
+  std::vector<int> ulen(ng);
+  for (int gi = 0; gi < ng; ++gi) {
+    std::fill(uni.begin(), uni.end(), 0);
+    for (int o : groups[gi])
+      for (int w = 0; w < words; ++w) uni[w] |= bits[static_cast<size_t>(o) * words + w];
+    int n = 0;
+    for (int w = 0; w < words; ++w) n += popc(uni[w]);
+    ulen[gi] = n;
+  }
+  std::vector<int> gorder(ng);
+  for (int gi = 0; gi < ng; ++gi) gorder[gi] = gi;
+  std::stable_sort(gorder.begin(), gorder.end(), [&](int a, int b) { return ulen[a] > ulen[b]; });
+  // Steps: the group's union in ascending input order, each with the value
+  // block of every member that holds that input (or -1). A member's active
+  // steps are then exactly its own list in its own order.
+  const int rec = 1 + group;
+  int count = 0;
+  std::vector<int32_t> vb(static_cast<size_t>(n_in) * group);
+  h_grp_ptr[0] = 0;
+  for (int k = 0; k < ng; ++k) {
+    const std::vector<int>& g = groups[gorder[k]];
+    std::fill(vb.begin(), vb.end(), -1);
+    for (int j = 0; j < group; ++j) {
+      const int o = j < static_cast<int>(g.size()) ? g[j] : -1;
+      h_grp_out[static_cast<size_t>(k) * group + j] = o;
+      if (o < 0) continue;
+      for (const auto& e : lists[o]) vb[static_cast<size_t>(e.first) * group + j] = e.second;
+    }
+    for (int i = 0; i < n_in; ++i) {
+      bool any = false;
+      for (int j = 0; j < group; ++j) any |= vb[static_cast<size_t>(i) * group + j] >= 0;
+      if (!any) continue;
+      if (count >= capacity) return TMAC_ERR_CAPACITY;
+      int32_t* out = h_steps + static_cast<size_t>(count) * rec;
+      out[0] = i;
+      for (int j = 0; j < group; ++j) out[1 + j] = vb[static_cast<size_t>(i) * group + j];
+      ++count;
+    }
+    h_grp_ptr[k + 1] = count;
+  }
+  *n_groups = ng;
+  *n_steps = count;
+  return TMAC_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Attention tile maps
 // ---------------------------------------------------------------------------

@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -41,6 +41,12 @@ SIGNATURES = {
     "tmac_bell_sample_col_idx": [_u64, _i, _i, _i, _vp],
     "tmac_bell_validate": [_vp, _i, _i, _i],
     "tmac_bell_transpose": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
+    "tmac_bell_group_schedule": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, ctypes.POINTER(_i),
+                                 ctypes.POINTER(_i)],
+    "tmac_bell_fwd_grouped": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _i, _i, _i, _i,
+                              _i, _i, _vp],
+    "tmac_bell_fwd_grouped_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _vp,
+                                       _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_fwd": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_fwd_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i, _i, _i,
                                _i, _i, _vp],

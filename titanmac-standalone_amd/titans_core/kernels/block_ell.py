@@ -36,8 +36,10 @@ class BlockELLPattern:
     """Sparsity pattern of a Block-ELL matrix with `n_bcol` block-columns.
 
     col_idx: int32 [n_brow, width], each row strictly increasing.
-    Derived (host, via libtmac): the transposed index (t_ptr, t_row, t_vblk)
-    and the longest-first column order used by the forward kernel.
+    Derived (host, via libtmac): the transposed index (t_ptr, t_row, t_vblk),
+    the longest-first column order used by the forward kernel, and the grouped
+    forward schedule (`grp`: block-columns paired by shared block-rows, see
+    tmac_bell_group_schedule), packed as [grp_ptr, grp_out, steps].
     Device copies are cached per device.
     """
 
@@ -59,7 +61,24 @@ class BlockELLPattern:
                                          self.t_ptr.ctypes.data, self.t_row.ctypes.data,
                                          self.t_vblk.ctypes.data, self.order.ctypes.data),
                    "Block-ELL transpose")
+        self.grp = self._group_schedule(L)
         self._dev = {}
+
+    def _group_schedule(self, L) -> np.ndarray:
+        """The forward's pair schedule, packed as one int32 array:
+        grp_ptr [n_groups + 1], grp_out [2 n_groups], steps [n_steps, 3]."""
+        import ctypes
+        ng = (self.n_bcol + 1) // 2
+        cap = self.n_brow * self.width
+        gp = np.empty(ng + 1, dtype=np.int32)
+        go = np.empty(2 * ng, dtype=np.int32)
+        st = np.empty(3 * cap, dtype=np.int32)
+        n_g, n_s = ctypes.c_int(0), ctypes.c_int(0)
+        _lib.check(L.tmac_bell_group_schedule(self.col_idx.ctypes.data, self.n_brow, self.n_bcol,
+                                              self.width, 0, 2, gp.ctypes.data, go.ctypes.data,
+                                              st.ctypes.data, cap, ctypes.byref(n_g), ctypes.byref(n_s)),
+                   "Block-ELL group schedule")
+        return np.concatenate([gp, go, st[:3 * n_s.value]])
 
     @classmethod
     def sample(cls, seed: int, n_brow: int, n_bcol: int, width: int) -> "BlockELLPattern":
@@ -95,6 +114,7 @@ class BlockELLPattern:
             self._dev[key] = {
                 "col_idx": mk(self.col_idx.reshape(-1)), "t_ptr": mk(self.t_ptr),
                 "t_row": mk(self.t_row), "t_vblk": mk(self.t_vblk), "order": mk(self.order),
+                "grp": mk(self.grp),
             }
         return self._dev[key]
 
@@ -129,10 +149,29 @@ def _check_values(values: torch.Tensor, what: str) -> None:
         raise TypeError(f"{what}: the kernels take bfloat16, float16 or float32, got {values.dtype}")
 
 
+_GROUPED_MIN_TILES = 256  # the grouped kernel runs one persistent workgroup per CU
+
+
+def _grouped_args(grp: Optional[torch.Tensor], M: int, ldx: int, n_bcol: int, dtype) -> Optional[tuple]:
+    """(grp_ptr, grp_out, steps, n_groups) device pointers for tmac_bell_fwd_grouped when
+    it applies (16-bit, more than 64 rows, enough 512-row x 2-column tiles to fill the
+    GPU, row pitch within its 32-bit offsets), else None (tmac_bell_fwd)."""
+    if grp is None or dtype not in (torch.bfloat16, torch.float16) or M <= 64 or ldx > (1 << 22):
+        return None
+    ng = (n_bcol + 1) // 2
+    if -(-M // 512) * ng < _GROUPED_MIN_TILES:
+        return None
+    base = grp.data_ptr()
+    return base, base + 4 * (ng + 1), base + 4 * (3 * ng + 1), ng
+
+
 def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
               t_row: torch.Tensor, t_vblk: torch.Tensor, order: torch.Tensor,
-              bias: Optional[torch.Tensor], gelu: bool) -> torch.Tensor:
-    """y = (gelu)(x · W + bias) with W in Block-ELL; x [..., 64*n_brow] -> y [..., 64*n_bcol]."""
+              bias: Optional[torch.Tensor], gelu: bool,
+              grp: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = (gelu)(x · W + bias) with W in Block-ELL; x [..., 64*n_brow] -> y [..., 64*n_bcol].
+    With the pattern's grouped schedule `grp`, large 16-bit calls run the grouped
+    kernel (bitwise-identical results)."""
     _check_values(values, "bell_fwd")
     n_brow, width = int(values.shape[0]), int(values.shape[1])
     n_bcol = int(t_ptr.numel()) - 1
@@ -150,12 +189,19 @@ def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_pt
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
+        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype)
+        epi = _lib.EPI_GELU if gelu else _lib.EPI_NONE
         with _lib.device_guard(dev):
-            rc = _lib.lib().tmac_bell_fwd(
-                _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
-                _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, M, n_brow,
-                n_bcol, width, _lib.dtype_code(x.dtype), _lib.EPI_GELU if gelu else _lib.EPI_NONE,
-                _lib.stream_ptr(dev))
+            if ga is not None:
+                rc = _lib.lib().tmac_bell_fwd_grouped(
+                    _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), ga[0], ga[1], ga[2], ga[3], 2,
+                    _lib.ptr(bias), _lib.ptr(y), N, M, n_brow, n_bcol, width,
+                    _lib.dtype_code(x.dtype), epi, _lib.stream_ptr(dev))
+            else:
+                rc = _lib.lib().tmac_bell_fwd(
+                    _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
+                    _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, M, n_brow,
+                    n_bcol, width, _lib.dtype_code(x.dtype), epi, _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_bell_fwd")
     return y.reshape(*x.shape[:-1], N)
 
@@ -164,14 +210,15 @@ bell_fwd = torch.library.custom_op("titanmac::bell_fwd", mutates_args=())(_bell_
 
 
 @bell_fwd.register_fake
-def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu):
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, grp=None):
     n_bcol = t_ptr.shape[0] - 1
     return x.new_empty((*x.shape[:-1], BLOCK * n_bcol))
 
 
 def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
                    t_ptr: torch.Tensor, t_row: torch.Tensor, t_vblk: torch.Tensor,
-                   order: torch.Tensor, bias: Optional[torch.Tensor]) -> Tuple[torch.Tensor, torch.Tensor]:
+                   order: torch.Tensor, bias: Optional[torch.Tensor],
+                   grp: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """(gelu(z), z) with z = x · W + bias, both from the forward kernel's epilogue
     (16-bit only): the training form of fc1 + GELU, z kept for the backward."""
     _check_values(values, "bell_fwd_gelu")
@@ -194,11 +241,18 @@ def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     z = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
+        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype)
         with _lib.device_guard(dev):
-            rc = _lib.lib().tmac_bell_fwd_gelu_aux(
-                _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
-                _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M,
-                n_brow, n_bcol, width, _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+            if ga is not None:
+                rc = _lib.lib().tmac_bell_fwd_grouped_gelu_aux(
+                    _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), ga[0], ga[1], ga[2], ga[3], 2,
+                    _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M, n_brow, n_bcol, width,
+                    _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
+            else:
+                rc = _lib.lib().tmac_bell_fwd_gelu_aux(
+                    _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), _lib.ptr(t_ptr), _lib.ptr(t_row),
+                    _lib.ptr(t_vblk), _lib.ptr(order), _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M,
+                    n_brow, n_bcol, width, _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
         _lib.check(rc, "tmac_bell_fwd_gelu_aux")
     shape = (*x.shape[:-1], N)
     return y.reshape(shape), z.reshape(shape)
@@ -208,7 +262,7 @@ bell_fwd_gelu = torch.library.custom_op("titanmac::bell_fwd_gelu", mutates_args=
 
 
 @bell_fwd_gelu.register_fake
-def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias):
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, grp=None):
     shape = (*x.shape[:-1], BLOCK * (t_ptr.shape[0] - 1))
     return x.new_empty(shape), x.new_empty(shape)
 
@@ -347,7 +401,7 @@ def _sddmm_workspace_bytes(L, M: int, n_brow: int, n_bcol: int, width: int) -> i
 
 
 def _fwd_setup_context(ctx, inputs, output):
-    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu = inputs
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, _grp = inputs
     if gelu:
         # The fused activation keeps no pre-activation for the backward; the
         # module only fuses GELU when no gradient is needed.
@@ -378,14 +432,14 @@ def _fwd_backward(ctx, gy):
             gb = _bell_bias_grad(g2).to(g2.dtype)  # fixed-order fp32 column sums
         else:
             gb = g2.sum(0)
-    return gx, gv, None, None, None, None, None, gb, None
+    return gx, gv, None, None, None, None, None, gb, None, None
 
 
 bell_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
 
 
 def _fwd_gelu_setup_context(ctx, inputs, output):
-    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias = inputs
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, _grp = inputs
     ctx.mark_non_differentiable(output[1])
     ctx.set_materialize_grads(False)  # no zero-filled gradient for the pre-activation output
     ctx.save_for_backward(x, values, col_idx, output[1])
@@ -410,7 +464,7 @@ def _fwd_gelu_backward(ctx, ga, _gz_unused):
         gv = bell_sddmm(x, gz, col_idx, n_brow, width, values.dtype)
     if want_b:
         gb = db.to(ctx.bias_dtype)
-    return gx, gv, None, None, None, None, None, gb
+    return gx, gv, None, None, None, None, None, gb, None
 
 
 bell_fwd_gelu.register_autograd(_fwd_gelu_backward, setup_context=_fwd_gelu_setup_context)
@@ -445,11 +499,11 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
         # training: the kernel writes gelu(z) and z; the backward runs GELU' and
         # the bias gradient in one pass (bell_fwd_gelu's autograd)
         y, _ = bell_fwd_gelu(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
-                             idx["order"], bias)
+                             idx["order"], bias, idx["grp"])
         return y
     op = _bell_fwd if _lib.direct_call(x, values, bias) else bell_fwd
     y = op(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"], idx["order"], bias,
-           fuse)
+           fuse, idx["grp"])
     if activation == "gelu" and not fuse:
         y = torch.nn.functional.gelu(y)
     return y
