@@ -627,8 +627,40 @@ def cpu_threads() -> tuple[int, dict]:
     except OSError:
         pass
     info = {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "omp_num_threads_env": omp,
-            "cpu_model": model}
+            "cpu_model": model, **cpu_topology()}
     return max(1, n), info
+
+
+def cpu_topology() -> dict:
+    """Physical cores and hardware threads behind this process's CPUs (sysfs topology),
+    and the clocks the host reports, so that a per-thread rate can be checked against a
+    core's peak: SMT siblings share one core's FMA units."""
+    cpus = sorted(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else list(range(os.cpu_count() or 1))
+    cores, pkgs = set(), set()
+    for c in cpus:
+        base = Path(f"/sys/devices/system/cpu/cpu{c}/topology")
+        try:
+            pkg = int((base / "physical_package_id").read_text())
+            core = int((base / "core_id").read_text())
+        except (OSError, ValueError):
+            return {"physical_cores": None, "threads_per_core": None, "cpu_mhz": None}
+        cores.add((pkg, core))
+        pkgs.add(pkg)
+    mhz = []
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.lower().startswith("cpu mhz"):
+                mhz.append(float(line.split(":", 1)[1]))
+    except (OSError, ValueError):
+        pass
+    max_mhz = None
+    try:
+        max_mhz = int(Path("/sys/devices/system/cpu/cpu0/cpufreq/cpuinfo_max_freq").read_text()) / 1000
+    except (OSError, ValueError):
+        pass
+    return {"physical_cores": len(cores), "sockets": len(pkgs),
+            "threads_per_core": round(len(cpus) / max(1, len(cores)), 2),
+            "cpu_mhz": round(float(np.median(mhz)), 1) if mhz else None, "cpu_max_mhz": max_mhz}
 
 
 def cpu_baseline(spmm) -> dict:
@@ -663,6 +695,8 @@ def cpu_baseline(spmm) -> dict:
                       f"{blas[0].get('internal_api') if blas else '?'} BLAS), {reps} reps in {el:.1f} s; "
                       f"effective (stored-block) FLOPs counted, as on the GPU",
             "dense_gflops_per_thread": round(dense * reps / el / 1e9 / max(1, blas_threads), 1),
+            "dense_gflops_per_physical_core": round(
+                dense * reps / el / 1e9 / max(1, min(blas_threads, info.get("physical_cores") or blas_threads)), 1),
             "torch_threads": torch.get_num_threads(), "blas_threads": blas_threads, **info}
 
 

@@ -388,7 +388,27 @@ typedef struct {
    * in forward and backward. 0 <= p < 1. */
   float dropout_p;
   uint64_t dropout_seed;
+  /* Gradient of an additive mask (tmac_wattn_bwd_ex only; NULL: none), as
+   * F.scaled_dot_product_attention differentiates a float attn_mask
+   * (attn/windowed_attention.py:311-323): the backward writes, as fp32 into
+   * d_mask_grad [B, H, S, S] (contiguous), dS[b, h, q, k] = dL/d(score) of
+   * every pair in a 64-key tile that holds an allowed pair of q's 32-row slice;
+   * the other entries (all-masked tiles, whose gradient is 0) are not written,
+   * so the caller zero-fills the buffer first. Summing over broadcast mask
+   * dimensions: tmac_wattn_mask_grad_reduce. TMAC_MASK_ADD_F32 masks only
+   * (a bool mask, or no mask, with d_mask_grad returns TMAC_ERR_VALUE). */
+  float* d_mask_grad;
 } tmac_attn_opts;
+
+/* The gradient of a broadcast additive mask from tmac_wattn_bwd_ex's per-head
+ * d_mask_grad: d_out[mb][mh][q][k] = sum over the (b, h) that mask row
+ * (mb, mh) serves of d_ds[b][h][q][k], in ascending b, then h (a fixed order:
+ * the same bits on every call). mask_batch is 1 or B, mask_heads 1 or H; d_out
+ * [mask_batch, mask_heads, S, S] fp32, contiguous; d_out may not overlap d_ds.
+ * No counterpart in the reference (autograd sums the broadcast dimensions of
+ * SDPA's mask gradient). */
+int tmac_wattn_mask_grad_reduce(const float* d_ds, int B, int H, int S, int mask_batch,
+                                int mask_heads, float* d_out, void* stream);
 
 /* Bytes of the work-list workspace of a mask of [mask_batch, mask_heads, S, S];
  * 0 for a non-positive argument. No counterpart in the reference (which masks
@@ -450,7 +470,8 @@ int tmac_wattn_bwd_ex(const void* d_Q, const int64_t q_strides[3],
  * shares that GPU's scratch: calls that overlap on one GPU (concurrent streams,
  * threads) race and must be serialised by the caller. The scratch's device
  * address is looked up once per device, on the first call with that device
- * current. */
+ * current; the stream must belong to the current device (a stream of another
+ * device returns TMAC_ERR_VALUE, nothing launched). */
 int tmac_wattn_bwd_noalloc(const void* d_Q, const int64_t q_strides[3],
                            const void* d_K, const int64_t k_strides[3],
                            const void* d_V, const int64_t v_strides[3],

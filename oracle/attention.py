@@ -94,15 +94,19 @@ def biased_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, bias: np.ndarr
 def biased_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.ndarray,
                            bias: np.ndarray, scale: float | None = None,
                            drop: np.ndarray | None = None, dtype=np.float64,
-                           out: np.ndarray | None = None):
-    """(dq, dk, dv) of biased_attention for the output gradient `do`.
+                           out: np.ndarray | None = None, bias_grad: bool = False):
+    """(dq, dk, dv) of biased_attention for the output gradient `do`; with
+    bias_grad also dS, the gradient of an additive bias (per score, before any
+    summation over the bias's broadcast dimensions).
 
     With P = softmax(S), S = q·kᵀ·scale + bias, Z the dropout factors (1 without
     dropout) and O = (P ⊙ Z)·v: dV = (P ⊙ Z)ᵀ·dO, dP' = dO·Vᵀ, Δ = rowsum(dO ⊙ O)
     (= rowsum(P ⊙ Z ⊙ dP')), dS = P ⊙ (Z ⊙ dP' − Δ), dq = scale·dS·k,
-    dk = scale·dSᵀ·q. Fully masked rows get no gradient. `out`, when given, is
-    the forward output as stored (e.g. rounded to 16 bits) and enters Δ in place
-    of the exact O, as the saved output does in SDPA's backward.
+    dk = scale·dSᵀ·q; the bias enters S with weight 1, so dS is its gradient
+    (F.scaled_dot_product_attention's float attn_mask, attn/windowed_attention.py:318-323).
+    Fully masked rows get no gradient. `out`, when given, is the forward output
+    as stored (e.g. rounded to 16 bits) and enters Δ in place of the exact O, as
+    the saved output does in SDPA's backward.
     """
     q, k, v, do = (np.asarray(t, dtype=dtype) for t in (q, k, v, do))
     if scale is None:
@@ -119,6 +123,8 @@ def biased_attention_grads(q: np.ndarray, k: np.ndarray, v: np.ndarray, do: np.n
     dp = do @ np.swapaxes(v, -1, -2)
     delta = (do * o).sum(axis=-1, keepdims=True)
     ds = p * (z * dp - delta)
+    if bias_grad:
+        return scale * (ds @ k), scale * (np.swapaxes(ds, -1, -2) @ q), dv, ds
     return scale * (ds @ k), scale * (np.swapaxes(ds, -1, -2) @ q), dv
 
 

@@ -134,39 +134,155 @@ def test_caller_mask_fwd_bwd(dev, dtype, B, H, S, dh, lead, kind):
         assert np.all(o[..., 5, :] == 0)      # the fully masked row
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dh", [32, 64, 128])
 @pytest.mark.parametrize("B,H,S,w,Np,pattern,bs,p", [
     (1, 2, 200, 64, 4, "band", 64, 0.1), (2, 2, 300, 100, 5, "band", 64, 0.5),
     (1, 1, 333, 128, 16, "blockwin", 64, 0.3), (1, 2, 129, 1000, 0, "band", 64, 0.9)])
-def test_dropout_with_pattern(dev, dtype, B, H, S, w, Np, pattern, bs, p):
-    q, k, v, do = tensors((B, H, S, 64), dtype, seed=7 * S)
-    seed = 0x1234_5678_9ABC + S
+def test_dropout_with_pattern(dev, dtype, dh, B, H, S, w, Np, pattern, bs, p):
+    """Dropout with the band / block-window pattern at every head dimension and dtype:
+    the 16-bit dK/dV kernels (copy-ring at 64, generic at 32 and 128), the fp32 dK/dV
+    kernel's keep-octet path and the dQ kernels' row draws."""
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=7 * S + dh)
+    seed = 0x1234_5678_9ABC + S + dh
     o, dq, dk, dv = run(dev, q, k, v, do, None, p, seed, w, Np, pattern, bs)
     mask = om.make_mask(S, w, Np, True, pattern, bs)
     z = od.drop_factors(B, H, S, seed, p)
-    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), as_bias(mask), 0.125, z,
-                            None if dtype == torch.float32 else o)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), as_bias(mask),
+                            1.0 / np.sqrt(dh), z, None if dtype == torch.float32 else o)
     chk = close_f32 if dtype == torch.float32 else close
     chk(o, wo, what="out")
     for got, want, name in zip((dq, dk, dv), wg, "qkv"):
         chk(got, want, what=f"d{name}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-def test_dropout_with_caller_mask(dev, dtype):
-    B, H, S, dh, p = 2, 2, 260, 64, 0.25
-    rng = np.random.default_rng(11)
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dh", [32, 64, 128])
+def test_dropout_with_caller_mask(dev, dtype, dh):
+    B, H, S, p = 2, 2, 260, 0.25
+    rng = np.random.default_rng(11 + dh)
     bias = random_bias(rng, (2, 1), S)
-    q, k, v, do = tensors((B, H, S, dh), dtype, seed=13)
-    seed = 987654321987
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=13 + dh)
+    seed = 987654321987 + dh
     o, dq, dk, dv = run(dev, q, k, v, do, torch.from_numpy(bias).float(), p, seed)
     z = od.drop_factors(B, H, S, seed, p)
-    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), bias, 0.125, z,
-                            None if dtype == torch.float32 else o)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), bias, 1.0 / np.sqrt(dh),
+                            z, None if dtype == torch.float32 else o)
     chk = close_f32 if dtype == torch.float32 else close
     chk(o, wo, what="out")
     for got, want, name in zip((dq, dk, dv), wg, "qkv"):
         chk(got, want, what=f"d{name}")
+
+
+def test_dropout_generic_dkdv_kernel_at_head_dim_64(dev):
+    """A query-row stride above 2^25 elements sends the head-dim-64 dK/dV work to the
+    generic kernel (the copy-ring kernel addresses 64 rows with 32-bit offsets), with
+    dropout on: same oracle and bar."""
+    B, H, S, dh, w, Np, p = 1, 1, 70, 64, 32, 3, 0.3
+    q, k, v, do = tensors((B, H, S, dh), torch.bfloat16, seed=29)
+    pitch = (1 << 25) + 64
+    buf = torch.zeros((S - 1) * pitch + dh, dtype=torch.bfloat16, device=dev)
+    qd = buf.as_strided((B, H, S, dh), (S * pitch, S * pitch, pitch, 1))
+    qd.copy_(q.to(dev))
+    assert qd.stride(2) > (1 << 25)
+    qd.requires_grad_()
+    kd, vd = (t.to(dev).requires_grad_() for t in (k, v))
+    seed = 31337
+    o = windowed_attention(qd, kd, vd, w, Np, True, "band", 64, None, dropout_p=p, seed=seed)
+    o.backward(do.to(dev))
+    got = [t.detach().float().cpu().numpy() for t in (o, qd.grad, kd.grad, vd.grad)]
+    mask = om.make_mask(S, w, Np, True, "band", 64)
+    z = od.drop_factors(B, H, S, seed, p)
+    wo, wg = oracle_fwd_bwd(*(t.float().numpy() for t in (q, k, v, do)), as_bias(mask), 0.125, z,
+                            got[0])
+    close(got[0], wo, what="out")
+    for g, want, name in zip(got[1:], wg, "qkv"):
+        close(g, want, what=f"d{name}")
+    del buf
+
+
+MASK_GRAD_CASES = [  # B, H, S, dh, mask form, dropout p, mask dtype
+    (2, 3, 200, 64, "SS", 0.0, torch.float32), (2, 3, 257, 64, "HSS", 0.0, torch.float32),
+    (2, 3, 130, 64, "B1SS", 0.2, torch.float32), (2, 3, 150, 32, "1HSS", 0.0, torch.float32),
+    (1, 2, 260, 128, "BHSS", 0.0, torch.float32), (2, 2, 100, 64, "expand", 0.0, torch.float32),
+    (1, 2, 190, 64, "SS", 0.0, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("B,H,S,dh,form,p,mdtype", MASK_GRAD_CASES)
+def test_additive_mask_gradient(dev, dtype, B, H, S, dh, form, p, mdtype):
+    """A float attn_mask that requires grad gets dL/dmask, as SDPA's autograd gives it:
+    dS = P ⊙ (Z ⊙ dP − Δ) of every (b, h, q, k), summed over the mask's broadcast
+    dimensions (fixed order). Oracle: biased_attention_grads(bias_grad=True), pinned
+    against fp64 torch autograd in test_oracle_dropout.py, with Δ from the stored
+    output for 16-bit inputs; the forms cover [S, S], [H, S, S], [B, 1, S, S],
+    [1, H, S, S], [B, H, S, S] and an expanded [S, S] -> [B, H, S, S] view."""
+    if mdtype == torch.bfloat16 and dtype == torch.float32:
+        pytest.skip("a bf16 mask's gradient is bf16: checked with 16-bit inputs")
+    lead = {"SS": (), "HSS": (H,), "B1SS": (B, 1), "1HSS": (1, H), "BHSS": (B, H), "expand": ()}[form]
+    rng = np.random.default_rng(S + dh + len(lead))
+    bias = random_bias(rng, lead, S)
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=S + 1)
+    m_leaf = torch.from_numpy(bias).to(mdtype).to(dev).requires_grad_()
+    m_in = m_leaf.expand(B, H, S, S) if form == "expand" else m_leaf
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    seed = 4242 + S
+    o = windowed_attention(qd, kd, vd, 0, 0, attn_mask=m_in, dropout_p=p, seed=seed)
+    o.backward(do.to(dev))
+    torch.cuda.synchronize()
+    got = m_leaf.grad.float().cpu().numpy()
+    assert m_leaf.grad.dtype == mdtype and got.shape == bias.shape
+    bias_used = m_leaf.detach().float().cpu().numpy()  # as rounded to the mask dtype
+    b4 = np.broadcast_to(bias_used.reshape((1,) * (4 - bias_used.ndim) + bias_used.shape), (B, H, S, S))
+    z = od.drop_factors(B, H, S, seed, p) if p else None
+    o_np = o.detach().float().cpu().numpy()
+    qn, kn, vn, gn = (t.float().numpy() for t in (q, k, v, do))
+    ds = np.empty((B, H, S, S))
+    for b in range(B):
+        for h in range(H):
+            ds[b, h] = oa.biased_attention_grads(
+                qn[b, h], kn[b, h], vn[b, h], gn[b, h], b4[b, h], 1.0 / np.sqrt(dh),
+                None if z is None else z[b, h], out=None if dtype == torch.float32 else o_np[b, h],
+                bias_grad=True)[3]
+    shape4 = (1,) * (4 - bias.ndim) + bias.shape
+    want = ds.sum(axis=tuple(i for i in range(2) if shape4[i] == 1), keepdims=True).reshape(bias.shape)
+    if form == "expand":
+        want = ds.sum(axis=(0, 1))
+    chk = close_f32 if dtype == torch.float32 else close
+    chk(got, want, what="dmask")
+    assert np.all(got[np.isinf(bias)] == 0)
+    # the q/k/v gradients are unchanged by the mask gradient
+    qd2, kd2, vd2 = (t.to(dev).requires_grad_() for t in (q, k, v))
+    windowed_attention(qd2, kd2, vd2, 0, 0, attn_mask=m_in.detach(), dropout_p=p, seed=seed).backward(
+        do.to(dev))
+    for a, b2 in ((qd, qd2), (kd, kd2), (vd, vd2)):
+        assert torch.equal(a.grad, b2.grad)
+
+
+def test_mask_grad_reduce_entry(dev):
+    """tmac_wattn_mask_grad_reduce: fixed-order sums over the broadcast (b, h) of each
+    mask row, bit for bit against the same sums taken in that order on the CPU."""
+    L = _lib.lib()
+    B, H, S = 3, 4, 37
+    g = torch.Generator().manual_seed(9)
+    ds = torch.randn(B, H, S, S, generator=g)
+    for mb, mh in ((1, 1), (B, 1), (1, H), (B, H)):
+        out = torch.full((mb, mh, S, S), float("nan"), device=dev)
+        _lib.check(L.tmac_wattn_mask_grad_reduce(_lib.ptr(ds.to(dev)), B, H, S, mb, mh, _lib.ptr(out),
+                                                 _lib.stream_ptr(dev)), "reduce")
+        want = torch.zeros(mb, mh, S, S)
+        for b in range(B):
+            for h in range(H):
+                want[0 if mb == 1 else b, 0 if mh == 1 else h] += ds[b, h]
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu(), want), (mb, mh)
+    dsd = ds.to(dev)
+    assert L.tmac_wattn_mask_grad_reduce(_lib.ptr(dsd), B, H, S, 2, 1, _lib.ptr(dsd), None) == -2
+    assert L.tmac_wattn_mask_grad_reduce(_lib.ptr(dsd), B, H, S, 1, 1, _lib.ptr(dsd), None) == -8
+    assert L.tmac_wattn_mask_grad_reduce(None, B, H, S, 1, 1, _lib.ptr(dsd), None) == -1
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])

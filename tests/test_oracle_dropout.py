@@ -95,9 +95,10 @@ def test_keep_mask_draw_layout():
 
 
 def _torch_ref(q, k, v, bias, scale, z, do=None):
-    """fp64 torch: safe softmax (rows with every key masked give 0), dropout factors z."""
+    """fp64 torch: safe softmax (rows with every key masked give 0), dropout factors z.
+    With `do`: (dq, dk, dv, dbias) by autograd, dbias in the bias's own (broadcast) shape."""
     qt, kt, vt = (torch.from_numpy(t).requires_grad_() for t in (q, k, v))
-    bt = torch.from_numpy(np.asarray(bias, np.float64))
+    bt = torch.from_numpy(np.asarray(bias, np.float64).copy()).requires_grad_()
     dead = torch.isinf(bt).all(-1, keepdim=True) & (bt < 0).all(-1, keepdim=True)
     s = qt @ kt.transpose(-1, -2) * scale + torch.where(dead, torch.zeros_like(bt), bt)
     p = torch.softmax(s, -1) * (~dead)
@@ -105,7 +106,7 @@ def _torch_ref(q, k, v, bias, scale, z, do=None):
     if do is None:
         return o.detach().numpy()
     o.backward(torch.from_numpy(do))
-    return qt.grad.numpy(), kt.grad.numpy(), vt.grad.numpy()
+    return qt.grad.numpy(), kt.grad.numpy(), vt.grad.numpy(), bt.grad.numpy()
 
 
 def _bias(rng, shape, S, frac_masked=0.3):
@@ -162,11 +163,15 @@ def test_biased_attention_grads_against_torch_autograd(p):
     q, k, v, do = (rng.standard_normal((2, 3, S, 32)) for _ in range(4))
     bias = _bias(rng, (2, 1), S)
     z = od.drop_factors(2, 3, S, seed=123, p=p) if p else None
-    got = oa.biased_attention_grads(q, k, v, do, bias, scale=0.3, drop=z)
+    got = oa.biased_attention_grads(q, k, v, do, bias, scale=0.3, drop=z, bias_grad=True)
     want = _torch_ref(q, k, v, bias, 0.3, z, do)
+    # the bias broadcasts over heads: autograd sums dS over them
+    got = (*got[:3], got[3].sum(axis=1, keepdims=True))
+    assert want[3].shape == bias.shape
     for g, w in zip(got, want):
         assert np.allclose(g, w, rtol=1e-9, atol=1e-11)
     assert np.all(got[0][:, :, 3] == 0)  # a fully masked row gets no dq
+    assert np.all(got[3][:, :, 3] == 0) and np.all(got[3][np.isinf(bias)] == 0)
 
 
 def test_drop_factors_scale():

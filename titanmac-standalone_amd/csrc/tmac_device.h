@@ -316,6 +316,8 @@ __host__ __device__ inline U32x4 philox4x32_10(U32x4 c, uint32_t k0, uint32_t k1
 // kFeatBool (with kFeatMask): the mask is boolean, so no slice takes a bias
 // (kind 3) and the kernels leave that path out; it holds about 20 VGPRs.
 constexpr int kFeatMask = 1, kFeatDrop = 2, kFeatBool = 4;
+// the dQ kernels also write dS, the gradient of an additive mask (AttnX::dbias)
+constexpr int kFeatDBias = 8;
 
 struct AttnX {
   const void* mask;      // TMAC_MASK_BOOL: uint8 (0 = masked); TMAC_MASK_ADD_F32: fp32 added to the scores
@@ -329,7 +331,22 @@ struct AttnX {
   uint32_t seed0, seed1; // dropout seed
   uint32_t thresh;       // dropped when the 16-bit draw is below thresh (= floor(p * 2^16))
   float keep_scale;      // 2^16 / (2^16 - thresh): the inverse of the keep probability
+  float* dbias;          // additive mask's gradient: dS as fp32 [B*H, S, S] (backward; may be null)
 };
+
+// dS of this lane's query row q and keys k0 + 8g + (0..3), g = 0..3 (the
+// lane's 16 accumulator elements of a 32-key half), into the fp32 [B*H, S, S]
+// gradient of an additive mask; rows and keys past S are skipped.
+__device__ __forceinline__ void store_dbias(float* __restrict__ dbias, int bh, int S, int q, int k0,
+                                            const float (&ds)[16]) {
+  if (q >= S) return;
+  float* row = dbias + (static_cast<int64_t>(bh) * S + q) * S;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int k = k0 + 8 * (j >> 2) + (j & 3);
+    if (k < S) row[k] = ds[j];
+  }
+}
 
 // Row of the custom work lists of (b, head): the mask's own (batch, head) row.
 __device__ __forceinline__ int mask_row(const AttnX& x, int b, int hd) {

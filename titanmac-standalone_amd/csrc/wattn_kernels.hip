@@ -1293,6 +1293,14 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
             dp[j] = DR ? pj * (z[t] * dp[j] - dl) : pj * (dp[j] - dl);
           }
         }
+        if constexpr ((FEAT & kFeatDBias) != 0) {
+          {
+            float ds[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ds[j] = dp[j];
+            store_dbias(ax.dbias, bh, S, q_row, kt * 64 + 32 * kh + 4 * h, ds);
+          }
+        }
         // dQᵀ[d][q] += Σ_key K[key][d] dS[q][key], 16 keys per MFMA.
 #pragma unroll
         for (int k2 = 0; k2 < 2; ++k2) {
@@ -1500,6 +1508,14 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 2) void wattn_bwd_q_f32m_kernel(
 #pragma unroll
           for (int j = 0; j < 16; ++j)
             st[j] = __builtin_amdgcn_exp2f(st[j] - l2) * (dpt[j] - dl);
+        }
+        if constexpr ((FEAT & kFeatDBias) != 0) {
+          {
+            float ds[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) ds[j] = st[j];
+            store_dbias(ax.dbias, bh, S, q_row, kt * 64 + 32 * kh + 4 * h, ds);
+          }
         }
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
@@ -1952,6 +1968,13 @@ int make_attn_x(const tmac_attn_opts* o, int B, int H, int S, AttnX* x, int* fea
     x->seed0 = static_cast<uint32_t>(o->dropout_seed);
     x->seed1 = static_cast<uint32_t>(o->dropout_seed >> 32);
   }
+  if (o->d_mask_grad) {
+    // a gradient exists for an additive mask only
+    if (!o->d_mask || o->mask_format != TMAC_MASK_ADD_F32) return TMAC_ERR_VALUE;
+    if (reinterpret_cast<uintptr_t>(o->d_mask_grad) & 3u) return TMAC_ERR_ALIGN;
+    x->dbias = o->d_mask_grad;
+    *feat |= kFeatDBias;
+  }
   if (o->d_mask) {
     if (o->mask_format != TMAC_MASK_BOOL && o->mask_format != TMAC_MASK_ADD_F32) return TMAC_ERR_DTYPE;
     if (!(o->mask_batch == 1 || o->mask_batch == B) || !(o->mask_heads == 1 || o->mask_heads == H))
@@ -2060,7 +2083,7 @@ void launch_bwd_mfma(const AttnLaunch& a) {
   // The copy-ring kernel addresses 64 rows of Q and dO with 32-bit byte offsets.
   if constexpr (D == 64) {
     if (qs[2] <= (1ll << 25) && gs[2] <= (1ll << 25)) {
-      hipLaunchKernelGGL((wattn_bwd_kv64_kernel<DT, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
+      hipLaunchKernelGGL((wattn_bwd_kv64_kernel<DT, (FEAT & ~kFeatDBias)>), dim3(a.grid_kv), dim3(256), 0, a.s, Q,
                          K, V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
                          static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
                          vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0],
@@ -2069,7 +2092,7 @@ void launch_bwd_mfma(const AttnLaunch& a) {
       return;
     }
   }
-  hipLaunchKernelGGL((wattn_bwd_kv_kernel<DT, D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
+  hipLaunchKernelGGL((wattn_bwd_kv_kernel<DT, D, (FEAT & ~kFeatDBias)>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
                      V, G, a.lse, a.delta, static_cast<uint16_t*>(a.dK),
                      static_cast<uint16_t*>(a.dV), qs[0], qs[1], qs[2], ks[0], ks[1], ks[2],
                      vs[0], vs[1], vs[2], gs[0], gs[1], gs[2], dks[0], dks[1], dks[2], dvs[0],
@@ -2091,7 +2114,7 @@ void launch_bwd_f32(const AttnLaunch& a) {
   const unsigned dgrid = static_cast<unsigned>((n_rows * D + 2047) / 2048);
   hipLaunchKernelGGL((wattn_bwd_delta_f32_kernel<D>), dim3(dgrid), dim3(256), 0, a.s, O, G,
                      a.delta, os[0], os[1], os[2], gs[0], gs[1], gs[2], a.H, a.S, n_rows);
-  hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D, FEAT>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
+  hipLaunchKernelGGL((wattn_bwd_kv_f32m_kernel<D, (FEAT & ~kFeatDBias)>), dim3(a.grid_kv), dim3(256), 0, a.s, Q, K,
                      V, G, a.lse, a.delta, static_cast<float*>(a.dK), static_cast<float*>(a.dV),
                      qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
                      gs[2], dks[0], dks[1], dks[2], dvs[0], dvs[1], dvs[2], a.H, a.mp, a.scale,
@@ -2107,9 +2130,10 @@ template <int FEAT>
 void dispatch(const AttnLaunch& a, bool bwd) {
   const int d = a.dh;
   if (!bwd) {
-    if (d == 32) launch_fwd<32, FEAT>(a);
-    else if (d == 64) launch_fwd<64, FEAT>(a);
-    else launch_fwd<128, FEAT>(a);
+    constexpr int F = FEAT & ~kFeatDBias;  // the forward writes no gradient
+    if (d == 32) launch_fwd<32, F>(a);
+    else if (d == 64) launch_fwd<64, F>(a);
+    else launch_fwd<128, F>(a);
   } else if (a.dtype == TMAC_F32) {
     if (d == 32) launch_bwd_f32<32, FEAT>(a);
     else if (d == 64) launch_bwd_f32<64, FEAT>(a);
@@ -2196,6 +2220,8 @@ int launch_status(const AttnLaunch& a, int feat, bool bwd) {
     case kFeatDrop: dispatch<kFeatDrop>(a, bwd); break;
     case kFeatMask | kFeatDrop: dispatch<kFeatMask | kFeatDrop>(a, bwd); break;
     case kFeatMask | kFeatBool: dispatch<kFeatMask | kFeatBool>(a, bwd); break;
+    case kFeatMask | kFeatDBias: dispatch<kFeatMask | kFeatDBias>(a, bwd); break;
+    case kFeatMask | kFeatDrop | kFeatDBias: dispatch<kFeatMask | kFeatDrop | kFeatDBias>(a, bwd); break;
     default: dispatch<kFeatMask | kFeatDrop | kFeatBool>(a, bwd); break;
   }
   const hipError_t err = hipGetLastError();
@@ -2238,7 +2264,7 @@ int wattn_fwd_impl(const void* d_Q, const int64_t q_strides[3], const void* d_K,
   st = setup_lists(a, opts, window, n_persistent, causal, pattern, block_size, d_row_ptr,
                    d_entries, d_order, n_lead, nullptr, nullptr, nullptr, 0, &feat);
   if (st != TMAC_OK) return st;
-  return launch_status(a, feat, false);
+  return launch_status(a, feat & ~kFeatDBias, false);  // the forward writes no gradient
 }
 
 }  // namespace
@@ -2271,6 +2297,57 @@ extern "C" int tmac_wattn_fwd_ex(const void* d_Q, const int64_t q_strides[3], co
 extern "C" size_t tmac_wattn_mask_workspace(int S, int mask_batch, int mask_heads) {
   if (S <= 0 || mask_batch <= 0 || mask_heads <= 0) return 0;
   return mask_ws_layout(S, mask_batch, mask_heads).total;
+}
+
+namespace {
+
+// out[r][e] = sum over the (b, h) served by mask row r = (mb, mh) of
+// ds[b][h][e], e < n (= S * S), in ascending b then h. Four elements per thread.
+__global__ __launch_bounds__(256) void wattn_mask_grad_reduce_kernel(
+    const float* __restrict__ ds, float* __restrict__ out, int64_t n, int B, int H, int mb1,
+    int mh1) {
+  const int r = blockIdx.y;  // mask row
+  const int MH = mh1 ? 1 : H;
+  const int rb = r / MH, rh = r - rb * MH;
+  const int b0 = mb1 ? 0 : rb, b1 = mb1 ? B : rb + 1;
+  const int h0 = mh1 ? 0 : rh, h1 = mh1 ? H : rh + 1;
+  const int64_t e = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (e >= n) return;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int b = b0; b < b1; ++b)
+    for (int hd = h0; hd < h1; ++hd) {
+      const float* src = ds + (static_cast<int64_t>(b) * H + hd) * n + e;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (e + i < n) acc[i] += src[i];
+    }
+  float* dst = out + static_cast<int64_t>(r) * n + e;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (e + i < n) dst[i] = acc[i];
+}
+
+}  // namespace
+
+extern "C" int tmac_wattn_mask_grad_reduce(const float* d_ds, int B, int H, int S, int mask_batch,
+                                           int mask_heads, float* d_out, void* stream) {
+  if (!d_ds || !d_out) return TMAC_ERR_NULL;
+  if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
+  if (!(mask_batch == 1 || mask_batch == B) || !(mask_heads == 1 || mask_heads == H))
+    return TMAC_ERR_SHAPE;
+  const int64_t n = static_cast<int64_t>(S) * S;
+  const int64_t rows = static_cast<int64_t>(mask_batch) * mask_heads;
+  const int64_t blocks = (n + 1023) / 1024;
+  if (rows > 65535 || blocks > (1ll << 31) - 1) return TMAC_ERR_SHAPE;
+  const float* out_end = d_out + rows * n;
+  const float* ds_end = d_ds + static_cast<int64_t>(B) * H * n;
+  if (d_out < ds_end && d_ds < out_end) return TMAC_ERR_VALUE;  // overlapping buffers
+  hipLaunchKernelGGL(wattn_mask_grad_reduce_kernel,
+                     dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(rows)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), d_ds, d_out, n, B, H,
+                     mask_batch == 1 && B > 1 ? 1 : 0, mask_heads == 1 && H > 1 ? 1 : 0);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? TMAC_OK : static_cast<int>(err);
 }
 
 extern "C" int tmac_wattn_mask_lists(const tmac_attn_opts* opts, int S, void* stream) {
@@ -2457,6 +2534,16 @@ extern "C" int tmac_wattn_bwd_noalloc(
     void* stream) {
   if (B <= 0 || H <= 0 || S <= 0) return TMAC_ERR_SHAPE;
   if (static_cast<int64_t>(B) * H * S > TMAC_WATTN_BWD_SCRATCH_ROWS) return TMAC_ERR_TOO_LARGE;
+  // The scratch array is looked up for the current device; a stream of another
+  // device would run the kernels there against this device's array.
+  if (stream) {
+    int cur = -1;
+    hipDevice_t sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess) e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (static_cast<int>(sdev) != cur) return TMAC_ERR_VALUE;
+  }
   int err = TMAC_OK;
   float* delta = scratch_on_current_device(&err);
   if (!delta) return err;

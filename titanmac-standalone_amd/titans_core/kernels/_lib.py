@@ -80,6 +80,7 @@ SIGNATURES = {
                           _i, _i, _i, _i, _i, _i, _i, _i, _i, ctypes.c_float, _vp, _vp, _vp, _i,
                           _vp, _vp, _vp, _i, _i, _vp, _vp],
     "tmac_wattn_mask_lists": [_vp, _i, _vp],
+    "tmac_wattn_mask_grad_reduce": [_vp, _i, _i, _i, _i, _i, _vp, _vp],
     "tmac_dwconv_causal": [_vp, _i64, _vp, _vp, _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_dwconv_causal_bwd_workspace": [_i, _i, _i, _i, ctypes.POINTER(_sz)],
     "tmac_dwconv_causal_bwd": [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _sz, _i, _i, _i, _i,

@@ -293,7 +293,7 @@ class AttnOpts(ctypes.Structure):
                 ("mask_batch", ctypes.c_int), ("mask_heads", ctypes.c_int),
                 ("mask_strides", ctypes.c_int64 * 3), ("d_mask_ws", ctypes.c_void_p),
                 ("mask_ws_bytes", ctypes.c_size_t), ("dropout_p", ctypes.c_float),
-                ("dropout_seed", ctypes.c_uint64)]
+                ("dropout_seed", ctypes.c_uint64), ("d_mask_grad", ctypes.c_void_p)]
 
 
 def mask_operand(mask: torch.Tensor, B: int, H: int, S: int):
@@ -423,13 +423,25 @@ def _(q, k, v, mask, window_size, n_persistent, causal, pattern, block_size, sca
     return q.new_empty((B, S, H, dh)), lse, q.new_empty((nbytes,), dtype=torch.uint8)
 
 
+def _mask_grad_dims(mask: torch.Tensor, B: int, H: int) -> tuple[int, int]:
+    """(batch, head) sizes of an additive mask's own gradient: 1 where the mask
+    broadcasts (a missing or size-1 leading dimension), else B or H."""
+    shape = (1,) * (4 - mask.dim()) + tuple(mask.shape)
+    return (B if shape[0] > 1 else 1), (H if shape[1] > 1 else 1)
+
+
 def _window_attn_bwd_ex(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor,
                         v: torch.Tensor, out: torch.Tensor, lse: torch.Tensor,
                         mask: Optional[torch.Tensor], ws: torch.Tensor, window_size: int,
                         n_persistent: int, causal: bool, pattern: int, block_size: int,
-                        scale: float, dropout_p: float,
-                        seed: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(dq, dk, dv) of _window_attn_fwd_ex: same mask, workspace, dropout_p and seed."""
+                        scale: float, dropout_p: float, seed: int,
+                        mask_grad: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor,
+                                                          torch.Tensor]:
+    """(dq, dk, dv, dmask) of _window_attn_fwd_ex: same mask, workspace, dropout_p and seed.
+    With mask_grad (an additive float mask), dmask is the gradient of the mask in its
+    own shape and dtype, as SDPA's autograd gives it: dS = P * (dP - Delta) of every
+    (b, h, q, k), summed over the mask's broadcast dimensions in a fixed order
+    (tmac_wattn_mask_grad_reduce); else an empty tensor."""
     _check_qkv(q, k, v)
     B, H, S, dh = (int(s) for s in q.shape)
     if out.shape != (B, S, H, dh) or grad_out.shape != (B, S, H, dh):
@@ -444,9 +456,16 @@ def _window_attn_bwd_ex(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor
     lse = lse.contiguous()
     grads = [torch.empty((B, S, H, dh), dtype=q.dtype, device=dev) for _ in range(3)]
     views = [g.permute(0, 2, 1, 3) for g in grads]
+    if mask_grad and (mask is None or mask.dtype == torch.bool):
+        raise ValueError("a mask gradient exists for an additive float attn_mask only")
     if B * H * S == 0:
-        return tuple(views)
+        dm = torch.zeros_like(mask) if mask_grad else torch.empty(0, device=dev)
+        return (*views, dm)
     delta = torch.empty((B, H, S), dtype=torch.float32, device=dev)
+    ds = None
+    if mask_grad:
+        # dS of every (b, h) pair; tiles without an allowed pair are not written (0)
+        ds = torch.zeros((B, H, S, S), dtype=torch.float32, device=dev)
     row_ptr = entries = order = col_ptr = entries_kv = order_kv = None
     n_lead = n_lead_kv = 0
     if mask is not None:
@@ -454,6 +473,8 @@ def _window_attn_bwd_ex(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor
         if ws.numel() < _lib.lib().tmac_wattn_mask_workspace(S, mb, mh):
             raise ValueError("ws must be the mask workspace window_attn_fwd_ex returned")
         o = _opts(m, fmt, mb, mh, strides, ws, dropout_p, seed)
+        if ds is not None:
+            o.d_mask_grad = ds.data_ptr()
     else:
         row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
                                                             pattern, block_size, dev)
@@ -473,7 +494,19 @@ def _window_attn_bwd_ex(grad_out: torch.Tensor, q: torch.Tensor, k: torch.Tensor
             _lib.ptr(col_ptr), _lib.ptr(entries_kv), _lib.ptr(order_kv), n_lead_kv,
             _lib.dtype_code(q.dtype), _lib.stream_ptr(dev), ctypes.byref(o))
     _lib.check(rc, "tmac_wattn_bwd_ex")
-    return tuple(views)
+    dm = torch.empty(0, device=dev)
+    if ds is not None:
+        gb, gh = _mask_grad_dims(mask, B, H)
+        if (gb, gh) == (B, H):
+            g = ds
+        else:
+            g = torch.empty((gb, gh, S, S), dtype=torch.float32, device=dev)
+            with _lib.device_guard(dev):
+                rc = _lib.lib().tmac_wattn_mask_grad_reduce(_lib.ptr(ds), B, H, S, gb, gh,
+                                                            _lib.ptr(g), _lib.stream_ptr(dev))
+            _lib.check(rc, "tmac_wattn_mask_grad_reduce")
+        dm = g.reshape(mask.shape).to(mask.dtype)
+    return (*views, dm)
 
 
 window_attn_bwd_ex = torch.library.custom_op("titanmac::window_attn_bwd_ex",
@@ -482,9 +515,10 @@ window_attn_bwd_ex = torch.library.custom_op("titanmac::window_attn_bwd_ex",
 
 @window_attn_bwd_ex.register_fake
 def _(grad_out, q, k, v, out, lse, mask, ws, window_size, n_persistent, causal, pattern,
-      block_size, scale, dropout_p, seed):
+      block_size, scale, dropout_p, seed, mask_grad=False):
     B, H, S, dh = q.shape
-    return tuple(q.new_empty((B, S, H, dh)).permute(0, 2, 1, 3) for _ in range(3))
+    dm = mask.new_empty(mask.shape) if mask_grad else q.new_empty((0,))
+    return (*(q.new_empty((B, S, H, dh)).permute(0, 2, 1, 3) for _ in range(3)), dm)
 
 
 def _setup_ex(ctx, inputs, output):
@@ -502,9 +536,11 @@ def _backward_ex(ctx, grad_out, grad_lse, grad_ws):
         raise RuntimeError("window_attn_fwd_ex was called with need_lse=False; its backward "
                            "needs the log-sum-exp (windowed_attention sets it under autograd)")
     q, k, v, out, lse, mask, ws = ctx.saved_tensors
+    mask_grad = mask is not None and mask.dtype != torch.bool and ctx.needs_input_grad[3]
     op = _window_attn_bwd_ex if _lib.direct_call(grad_out, q, k, v) else window_attn_bwd_ex
-    dq, dk, dv = op(grad_out, q, k, v, out, lse, mask, ws, *ctx.args)
-    return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
+    dq, dk, dv, dm = op(grad_out, q, k, v, out, lse, mask, ws, *ctx.args, mask_grad)
+    return (dq, dk, dv, dm if mask_grad else None, None, None, None, None, None, None, None, None,
+            None)
 
 
 window_attn_fwd_ex.register_autograd(_backward_ex, setup_context=_setup_ex)
@@ -531,7 +567,8 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
     attn_mask (optional): bool (True = attend) or additive float mask broadcastable
     to [B, H, S, S]; it replaces the pattern (window_size, n_persistent, causal,
     pattern, block_size are then unused), as in WindowedAttention.forward
-    (:307-315). Rows with no allowed key give 0. No gradient flows to the mask.
+    (:307-315). Rows with no allowed key give 0. A float mask that requires grad
+    gets its gradient (dS summed over its broadcast dimensions), as SDPA gives it.
     dropout_p: attention dropout after the softmax (kept probabilities scaled by
     the inverse of the keep probability, 1 / (1 - p) to within 2^-16); seed: its
     Philox seed (default: drawn from torch's CPU
@@ -544,12 +581,11 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
             raise ValueError(f"num_persistent_tokens ({n_persistent}) must be < seq_len ({S})")
         if window_size < 0:
             raise ValueError(f"window_size must be non-negative, got {window_size}")
-    elif attn_mask.requires_grad:
-        raise NotImplementedError("windowed_attention computes no gradient for attn_mask")
     if scale is None:
         scale = 1.0 / math.sqrt(q.shape[-1])
+    mask_rg = attn_mask is not None and attn_mask.requires_grad
     need_lse = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
-                                            or v.requires_grad)
+                                            or v.requires_grad or mask_rg)
     if attn_mask is None and dropout_p == 0.0:
         op = _window_attn_fwd if _lib.direct_call(q, k, v) else window_attn_fwd
         out, _ = op(q, k, v, int(window_size), int(n_persistent), bool(causal), code,
@@ -557,7 +593,7 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
         return out.transpose(1, 2)
     if seed is None:
         seed = new_dropout_seed() if dropout_p > 0.0 else 0
-    op = _window_attn_fwd_ex if _lib.direct_call(q, k, v) else window_attn_fwd_ex
+    op = _window_attn_fwd_ex if _lib.direct_call(q, k, v, attn_mask) else window_attn_fwd_ex
     out, _, _ = op(q, k, v, attn_mask, int(window_size), int(n_persistent), bool(causal), code,
                    int(block_size), float(scale), float(dropout_p), int(seed), need_lse)
     return out.transpose(1, 2)
