@@ -1,5 +1,7 @@
 """GPU parity of the attention kernels at head dimensions 32 and 128 (the kernels are
-instantiated for 32, 64 and 128; 64 is covered case by case in the other attention tests).
+instantiated for 32, 64 and 128; 64 is covered case by case in the other attention tests),
+and of other head dimensions (8, 16, 80, 100), which windowed_attention zero-pads to the
+next of those.
 
 Bars as there: bf16/fp16 |got - want| <= 2e-2 + 1e-2 |want| against the fp64 oracle on
 the same 16-bit inputs (gradients divided by max(1, max |want|) first); fp32 within 1e-4
@@ -135,3 +137,89 @@ def test_module_training_step_bf16(dev, d_model, n_heads):
     yr.backward(dy.double())
     close(y.float().detach().cpu().numpy(), yr.detach().numpy(), atol=2e-2, rtol=2e-2, what="y")
     close(xd.grad.float().cpu().numpy(), xr.grad.numpy(), atol=2e-2, rtol=2e-2, what="dx")
+
+
+# Head dimensions the kernels are not built for: zero-padded to the next of 32, 64, 128
+# inside windowed_attention (the reference accepts any d_model / n_heads).
+PAD_DH = [8, 16, 80, 100]
+
+
+@pytest.mark.parametrize("dh", PAD_DH)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("B,H,S,w,Np,causal,pattern,bs", [GRID[3], GRID[4], GRID[7]])
+def test_padded_head_dims_forward_backward(dev, dh, dtype, B, H, S, w, Np, causal, pattern, bs):
+    q, k, v, do = tensors((B, H, S, dh), dtype, seed=S + 3 * dh)
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    o = windowed_attention(qd, kd, vd, w, Np, causal, pattern, bs)
+    assert o.shape == (B, H, S, dh) and o.dtype == dtype
+    o.backward(do.to(dev))
+    mask = om.make_mask(S, w, Np, causal, pattern, bs)
+    qn, kn, vn, gn = (t.double().numpy() for t in (q, k, v, do))
+    ref = oa.masked_attention(qn, kn, vn, mask)
+    want = oa.masked_attention_grads(qn, kn, vn, gn, mask)
+    got = [o.detach()] + [t.grad for t in (qd, kd, vd)]
+    for g, r, name in zip(got, [ref, *want], ("out", "dq", "dk", "dv")):
+        assert g.shape == (B, H, S, dh)
+        if dtype == torch.float32:
+            err = np.abs(g.float().cpu().numpy() - r).max()
+            assert err <= 1e-4 * max(1.0, np.abs(r).max()), f"{name}: {err}"
+        else:
+            close(g.float().cpu(), r, what=name)
+
+
+def test_padded_head_dim_with_caller_mask_and_dropout(dev):
+    """dh 80 with an additive mask and dropout: the padded call keeps the Philox
+    decisions (they do not depend on the head dimension) and the mask gradient."""
+    from oracle import dropout as od
+    B, H, S, dh, p, seed = 2, 2, 200, 80, 0.2, 777
+    rng = np.random.default_rng(80)
+    bias = np.where(rng.random((S, S)) < 0.3, -np.inf, rng.standard_normal((S, S)))
+    np.fill_diagonal(bias, 0.0)
+    q, k, v, do = tensors((B, H, S, dh), torch.bfloat16, seed=80)
+    qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+    md = torch.from_numpy(bias).float().to(dev).requires_grad_()
+    o = windowed_attention(qd, kd, vd, 0, 0, attn_mask=md, dropout_p=p, seed=seed)
+    o.backward(do.to(dev))
+    z = od.drop_factors(B, H, S, seed, p)
+    o_np = o.detach().float().cpu().numpy()
+    qn, kn, vn, gn = (t.float().numpy() for t in (q, k, v, do))
+    dmask = np.zeros((S, S))
+    for b in range(B):
+        for h in range(H):
+            wo = oa.biased_attention(qn[b, h], kn[b, h], vn[b, h], bias, 1 / np.sqrt(dh), z[b, h])
+            close(o_np[b, h], wo, what="out")
+            gq, gk, gv, ds = oa.biased_attention_grads(qn[b, h], kn[b, h], vn[b, h], gn[b, h], bias,
+                                                       1 / np.sqrt(dh), z[b, h], out=o_np[b, h],
+                                                       bias_grad=True)
+            dmask += ds
+            for got, want, name in zip((qd, kd, vd), (gq, gk, gv), "qkv"):
+                close(got.grad[b, h].float().cpu(), want, what=f"d{name}")
+    close(md.grad.cpu().numpy(), dmask, what="dmask")
+
+
+@pytest.mark.parametrize("pattern", ["band", "blockwin"])
+def test_module_head_dim_80(dev, pattern):
+    """TitanMACConfig(d_model=640, n_heads=8) (head dim 80) builds and runs both attention
+    modules; the band module's output against fp64 SDPA of the module's function."""
+    torch.manual_seed(3)
+    cfg = tc.TitanMACConfig(d_model=640, n_heads=8, n_layers=1, window_size=64, n_persistent=8,
+                            use_block_sparse=pattern == "blockwin")
+    blk = tc.TitanBlock(cfg).to(dev, torch.bfloat16).train()
+    x = torch.randn(2, 200, 640, device=dev, dtype=torch.bfloat16, requires_grad=True)
+    y = blk(x)
+    y.float().square().mean().backward()
+    assert y.shape == x.shape and torch.isfinite(y).all() and torch.isfinite(x.grad).all()
+    if pattern == "band":
+        m = tc.WindowedAttention(cfg).to(dev).eval()
+        xx = torch.randn(1, 150, 640, device=dev)
+        with torch.no_grad():
+            got = m(xx).double().cpu()
+        w_qkv, w_out = m.qkv_proj.weight.double().cpu(), m.out_proj.weight.double().cpu()
+        xr = xx.double().cpu()
+        q, k, v = (xr @ w_qkv.T).reshape(1, 150, 3, 8, 80).permute(2, 0, 3, 1, 4)
+        add = torch.zeros(150, 150, dtype=torch.float64).masked_fill(
+            ~torch.from_numpy(om.band_mask(150, 64, 8)), float("-inf"))
+        o = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=add)
+        want = o.transpose(1, 2).reshape(1, 150, 640) @ w_out.T
+        err = (got - want).abs().max().item()
+        assert err <= 1e-4 * max(1.0, want.abs().max().item()), err

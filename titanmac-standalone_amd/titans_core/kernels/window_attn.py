@@ -560,6 +560,8 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
     """softmax(q·kᵀ·scale + mask)·v on allowed pairs only; q/k/v and result [B, H, S, dh].
 
     scale defaults to 1/sqrt(head_dim), SDPA's default (attn/windowed_attention.py:318-323).
+    head_dim 32, 64 or 128 runs the kernels directly; any other head_dim up to 128 is
+    zero-padded to the next of those (results unchanged up to rounding order).
     Raises ValueError where build_band_mask does (n_persistent >= S, window_size < 0);
     the block-window pattern also accepts n_persistent == S (only persistent
     tokens), as BlockSparseAttention does.
@@ -574,6 +576,22 @@ def windowed_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window
     Philox seed (default: drawn from torch's CPU
     generator), reused by the backward.
     """
+    dh = int(q.shape[-1])
+    if dh not in HEAD_DIMS:
+        # Other head dimensions (the reference takes any d_model / n_heads,
+        # attn/windowed_attention.py:229-230): zero-pad q, k, v to the next size
+        # the kernels are built for. The padded dimensions add 0 to every score and
+        # give output columns of 0, which are dropped; the scale stays 1/sqrt(dh).
+        if not (1 <= dh <= HEAD_DIMS[-1]) or q.shape != k.shape or q.shape != v.shape:
+            _check_qkv(q, k, v)  # raises for mismatched shapes
+            raise ValueError(f"head_dim must be at most {HEAD_DIMS[-1]}, got {dh}")
+        dp = next(d for d in HEAD_DIMS if d >= dh)
+        pad = (0, dp - dh)
+        out = windowed_attention(torch.nn.functional.pad(q, pad), torch.nn.functional.pad(k, pad),
+                                 torch.nn.functional.pad(v, pad), window_size, n_persistent, causal,
+                                 pattern, block_size, dh ** -0.5 if scale is None else scale,
+                                 attn_mask, dropout_p, seed)
+        return out[..., :dh]
     S = q.shape[2]
     code = _pattern_code(pattern)
     if attn_mask is None:
