@@ -308,7 +308,8 @@ int tmac_wattn_launch_order(const int32_t* h_ptr, int n_blocks, int32_t* h_order
  * row_ptr/entries: device copies of tmac_wattn_schedule's output built with
  * q_block = 128, sub_rows = 32; order/n_lead: device copy of
  * tmac_wattn_launch_order of that row_ptr, and its lead count.
- * dtype: TMAC_BF16 / TMAC_F16 (MFMA path) or TMAC_F32 (fp32 FMA path). */
+ * dtype: TMAC_BF16 / TMAC_F16 (16-bit MFMA kernels) or TMAC_F32 (fp32 MFMA kernels,
+ * v_mfma_f32_32x32x2_f32). */
 int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
                    const void* d_V, const int64_t v_strides[3],
@@ -335,8 +336,9 @@ int tmac_wattn_fwd(const void* d_Q, const int64_t q_strides[3],
  * row_ptr/entries/order/n_lead: as for tmac_wattn_fwd;
  * col_ptr/entries_kv: tmac_wattn_schedule_kv with k_block = 128,
  * sub_cols = 32, order_kv/n_lead_kv: tmac_wattn_launch_order of col_ptr
- * (device copies). dtype: TMAC_BF16 / TMAC_F16 (MFMA kernels) or TMAC_F32
- * (FMA kernels, for fp32 modules); dh: 32, 64 or 128. */
+ * (device copies). dtype: TMAC_BF16 / TMAC_F16 (16-bit MFMA kernels) or TMAC_F32
+ * (fp32 MFMA kernels, for fp32 modules); dh: 32, 64 or 128 (the Python wrapper
+ * zero-pads other head dimensions up to 128). */
 int tmac_wattn_bwd(const void* d_Q, const int64_t q_strides[3],
                    const void* d_K, const int64_t k_strides[3],
                    const void* d_V, const int64_t v_strides[3],

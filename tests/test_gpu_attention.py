@@ -88,9 +88,12 @@ def test_value_errors(dev):
         windowed_attention(q, q, q, 4, 16)
     with pytest.raises(ValueError):
         windowed_attention(q, q, q, -1, 0)
+    # head dims above 128 have no kernel (48 and other sizes up to 128 are zero-padded)
     with pytest.raises(ValueError):
-        windowed_attention(torch.zeros(1, 1, 16, 48, device=dev, dtype=torch.bfloat16),
-                           *[torch.zeros(1, 1, 16, 48, device=dev, dtype=torch.bfloat16)] * 2, 4, 0)
+        windowed_attention(torch.zeros(1, 1, 16, 160, device=dev, dtype=torch.bfloat16),
+                           *[torch.zeros(1, 1, 16, 160, device=dev, dtype=torch.bfloat16)] * 2, 4, 0)
+    z48 = torch.zeros(1, 1, 16, 48, device=dev, dtype=torch.bfloat16)
+    assert windowed_attention(z48, z48, z48, 4, 0).shape == (1, 1, 16, 48)
 
 
 def test_config1_module_fp32(dev):

@@ -278,9 +278,11 @@ __host__ __device__ inline Span mask_col_span(const MaskParams& p, int j) {
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
 // 1, 2, 3", SC 2011): ten rounds of a keyed bijection on a 128-bit counter; the
-// multipliers and Weyl increments are the paper's. Attention dropout draws one
-// call per (query, group of 4 keys, batch*head): counter {key / 4, query, bh, 0},
-// key {seed low, seed high}; output word key % 4 decides (query, key).
+// multipliers and Weyl increments are the paper's. Attention dropout makes one
+// call per (query, group of 8 keys, batch*head): counter {key / 8, query, bh, 0},
+// key {seed low, seed high}; the call's four words give eight 16-bit draws, key k
+// taking bits 16 (k % 2) .. 16 (k % 2) + 15 of word (k % 8) / 2, and (query, key)
+// is kept iff its draw >= floor(p * 2^16) (drop_row8, keep_octet2).
 struct U32x4 {
   uint32_t x, y, z, w;
 };

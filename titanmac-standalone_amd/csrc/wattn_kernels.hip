@@ -2100,7 +2100,7 @@ void launch_bwd_mfma(const AttnLaunch& a) {
                      a.order_kv, a.wm_kv, a.ax_kv);
 }
 
-// Backward, fp32 FMA kernels.
+// Backward, fp32 MFMA kernels (v_mfma_f32_32x32x2_f32): Δ, then dK/dV, then dQ.
 template <int D, int FEAT>
 void launch_bwd_f32(const AttnLaunch& a) {
   const int64_t *qs = a.qs, *ks = a.ks, *vs = a.vs, *os = a.os, *gs = a.gs, *dqs = a.dqs,

@@ -367,6 +367,28 @@ def mask_work_lists(mask: torch.Tensor, B: int, H: int, S: int):
     return (m, fmt, mb, mh, strides), ws
 
 
+_mask_cache: dict = {}  # (device, stream) -> (weakref to the mask, version, B, H, S, lists)
+
+
+def _cached_mask_work_lists(mask: torch.Tensor, B: int, H: int, S: int):
+    """mask_work_lists, reused while the same mask tensor (same object, unmodified:
+    same version counter) comes back for the same B, H, S on the same stream, as when
+    a model hands one attn_mask to every layer. One entry per (device, stream)."""
+    import weakref
+    key = (str(mask.device), _lib.stream_ptr(mask.device))
+    hit = _mask_cache.get(key)
+    if hit is not None:
+        ref, ver, b, h, s_, lists = hit
+        if ref() is mask and ver == mask._version and (b, h, s_) == (B, H, S):
+            return lists
+    lists = mask_work_lists(mask, B, H, S)
+    try:
+        _mask_cache[key] = (weakref.ref(mask), mask._version, B, H, S, lists)
+    except TypeError:  # a tensor type without weak references: no caching
+        pass
+    return lists
+
+
 def _window_attn_fwd_ex(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                         mask: Optional[torch.Tensor], window_size: int, n_persistent: int,
                         causal: bool, pattern: int, block_size: int, scale: float,
@@ -391,7 +413,7 @@ def _window_attn_fwd_ex(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     n_lead = 0
     if mask is not None:
         _lib.require_device(q, mask, what="windowed_attention attn_mask")
-        (m, fmt, mb, mh, strides), ws = mask_work_lists(mask, B, H, S)
+        (m, fmt, mb, mh, strides), ws = _cached_mask_work_lists(mask, B, H, S)
         o = _opts(m, fmt, mb, mh, strides, ws, dropout_p, seed)
     else:
         row_ptr, entries, order, n_lead = _device_work_list(S, window_size, n_persistent, causal,
