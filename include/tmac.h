@@ -149,7 +149,8 @@ int tmac_bell_fwd(const void* d_X, int64_t ldx, const void* d_vals,
  * Replaces `self.fc1(x)` followed by `self.activation(hidden)` of
  * MLPBlock.forward when gradients are recorded (blocks/mlp.py:58,61). As
  * tmac_bell_fwd with epi = TMAC_EPI_GELU, plus Z [M, N] with leading dimension
- * ldz; dtype TMAC_BF16 or TMAC_F16. */
+ * ldz; any dtype of tmac_bell_fwd (16-bit: Z and Y rounded from the same fp32
+ * value; TMAC_F32: Z and Y in fp32, the GELU with the device library's erff). */
 int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
                            const int32_t* d_t_ptr, const int32_t* d_t_row,
                            const int32_t* d_t_vblk, const int32_t* d_order,
@@ -183,24 +184,24 @@ int tmac_bell_fwd_grouped_gelu_aux(const void* d_X, int64_t ldx, const void* d_v
 int tmac_bell_gelu_bwd_workspace(int M, int N, size_t* ws_bytes);
 
 /* GELU backward and bias gradient of fc1, one pass over the gradient:
- * gZ = gA ⊙ GELU'(Z) (erf form) for [M, N] row-major 16-bit operands with
- * leading dimensions (N and the pitches multiples of 8), and with d_dbias
- * non-null dbias[n] = Σ_m gZ[m][n] in fp32 (of the stored 16-bit gZ, summed in
- * a fixed order: deterministic; 0 when M = 0). Replaces autograd's backward of
- * nn.GELU and the bias gradient of fc1 in MLPBlock's backward
- * (blocks/mlp.py:58,61). d_ws: tmac_bell_gelu_bwd_workspace bytes (needed with
- * d_dbias only; the row operands may be null when M = 0). dtype: TMAC_BF16 or
- * TMAC_F16. */
+ * gZ = gA ⊙ GELU'(Z) (erf form) for [M, N] row-major operands with leading
+ * dimensions (N and the pitches multiples of 16 bytes: 8 elements for 16-bit,
+ * 4 for fp32), and with d_dbias non-null dbias[n] = Σ_m gZ[m][n] in fp32 (of
+ * gZ as stored, summed in a fixed order: deterministic; 0 when M = 0).
+ * Replaces autograd's backward of nn.GELU and the bias gradient of fc1 in
+ * MLPBlock's backward (blocks/mlp.py:58,61). d_ws: tmac_bell_gelu_bwd_workspace
+ * bytes (needed with d_dbias only; the row operands may be null when M = 0).
+ * dtype: TMAC_BF16, TMAC_F16 or TMAC_F32. */
 int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_Z, int64_t ldz, void* d_gZ,
                        int64_t ldgz, float* d_dbias, void* d_ws, size_t ws_bytes, int M, int N,
                        int dtype, void* stream);
 
 /* Bias gradient of a Block-ELL linear without activation (fc2):
- * dbias[n] = Σ_m gY[m][n] in fp32 over a [M, N] row-major 16-bit gradient (N and
- * the pitch multiples of 8), summed in a fixed order (deterministic; 0 when
+ * dbias[n] = Σ_m gY[m][n] in fp32 over a [M, N] row-major gradient (N and the
+ * pitch multiples of 16 bytes), summed in a fixed order (deterministic; 0 when
  * M = 0). Replaces the bias gradient of F.linear in MLPBlock's backward
  * (blocks/mlp.py:64). d_ws: tmac_bell_gelu_bwd_workspace(M, N) bytes. dtype:
- * TMAC_BF16 or TMAC_F16. */
+ * TMAC_BF16, TMAC_F16 or TMAC_F32. */
 int tmac_bell_bias_grad(const void* d_gY, int64_t ldgy, float* d_dbias, void* d_ws,
                         size_t ws_bytes, int M, int N, int dtype, void* stream);
 

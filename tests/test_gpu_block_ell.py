@@ -118,11 +118,16 @@ def test_fp32_config4_shape_and_determinism(dev):
     close_rel(dv.cpu(), ob.sddmm(Xn, dYn, pat.col_idx), what="dW")
 
 
-def test_mlp_block_ell_fp32_training_matches_dense_fp64(dev):
+def test_mlp_block_ell_fp32_training_matches_dense_fp64(dev, monkeypatch):
     """An fp32 Block-ELL MLP (fc2(gelu(fc1(x)))) trains without autocast: output and the
     gradients of x, both layers' stored blocks and biases against fp64 autograd of the
-    same dense weights on the CPU, within 1e-4 of each tensor's largest entry."""
+    same dense weights on the CPU, within 1e-4 of each tensor's largest entry. fc1 + GELU
+    runs the fused training form (the fp32 kernel stores gelu(z) and z; GELU' and the
+    bias gradient in one pass)."""
     from titans_core.blocks.mlp import MLPBlock
+    calls = []
+    fused = kb.bell_fwd_gelu
+    monkeypatch.setattr(kb, "bell_fwd_gelu", lambda *a: calls.append(1) or fused(*a))
     torch.manual_seed(3)
     mlp = MLPBlock(192, 384, block_ell=True, density=0.5).to(dev)
     assert mlp.fc1.values.dtype == torch.float32
@@ -138,6 +143,7 @@ def test_mlp_block_ell_fp32_training_matches_dense_fp64(dev):
     F = torch.nn.functional
     yd = F.linear(F.gelu(F.linear(xd, W1, b1)), W2, b2)
     yd.backward(gy.double().cpu())
+    assert calls == [1]
     close_rel(y.detach().cpu(), yd.detach(), what="y")
     close_rel(x.grad.cpu(), xd.grad, what="dx")
     close_rel(mlp.fc1.bias.grad.cpu(), b1.grad, what="db1")
@@ -327,8 +333,8 @@ def test_row_pitch_inputs_and_padded_outputs(dev, M):
     assert (dXw[:, :16] == sentinel).all() and (dXw[:, 16 + K:] == sentinel).all()
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M", [50, 300])  # few-row kernel, gather GEMM
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("M", [50, 300])  # few-row kernel, gather GEMM (16-bit)
 def test_fwd_gelu_aux_outputs_bit_exact(dev, dtype, M):
     """tmac_bell_fwd_gelu_aux writes gelu(z) and z: bit-identical to the plain
     forward with and without its fused GELU (same kernel, same sums)."""
@@ -376,10 +382,33 @@ def test_gelu_bwd_and_bias_grad(dev, dtype, M, N):
     assert torch.equal(gz3, gz) and db3.numel() == 0
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N", [(0, 64), (1, 64), (257, 192), (5000, 2560)])
+def test_gelu_bwd_and_bias_grad_fp32(dev, M, N):
+    """fp32 rows: gz = ga ⊙ GELU'(z) against the fp64 oracle within 1e-5 relative
+    (erff/expf of the device library), the bias gradient the fixed-order column sum of
+    gz (rerun bit-identical), and a row-strided view giving the same bits."""
+    g = torch.Generator().manual_seed(M + 2 * N)
+    ga = torch.randn(M, N, generator=g)
+    z = torch.randn(M, N, generator=g) * 3
+    gz, db = kb._bell_gelu_bwd(ga.to(dev), z.to(dev), True)
+    assert gz.dtype == torch.float32 and db.dtype == torch.float32
+    want = ga.double().numpy() * ob.gelu_erf_grad(z.double().numpy())
+    err = np.abs(gz.double().cpu().numpy() - want)
+    assert (err <= 1e-5 * (1.0 + np.abs(want))).all(), f"max err {err.max():.3g}"
+    g64 = gz.double().cpu().numpy()
+    assert np.abs(db.cpu().numpy() - g64.sum(0)).max() <= 1e-5 * (1.0 + np.abs(g64).sum(0).max())
+    gz2, db2 = kb._bell_gelu_bwd(ga.to(dev), z.to(dev), True)
+    assert torch.equal(gz, gz2) and torch.equal(db, db2)
+    wide = torch.zeros(M, N + 8)
+    wide[:, :N] = ga
+    gz3, db3 = kb._bell_gelu_bwd(wide.to(dev)[:, :N], z.to(dev), False)
+    assert torch.equal(gz3, gz) and db3.numel() == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("M,N", [(0, 64), (1, 64), (257, 192), (32768, 640)])
 def test_bias_grad_column_sums(dev, dtype, M, N):
-    """tmac_bell_bias_grad: fp32 column sums of a 16-bit gradient against the fp64 sum,
+    """tmac_bell_bias_grad: fp32 column sums of a 16-bit or fp32 gradient against the fp64 sum,
     bit-identical on a rerun, and 0 for no rows; a row-strided view gives the same bits."""
     g = torch.Generator().manual_seed(M + 3 * N)
     gy = torch.randn(M, N, generator=g).to(dtype)

@@ -223,8 +223,10 @@ def test_bias_grad_argument_errors(lib):
     assert lib.tmac_bell_bias_grad(*bad) == -2           # pitch < N
     bad = list(g); bad[5] = -1
     assert lib.tmac_bell_bias_grad(*bad) == -2
-    bad = list(g); bad[7] = 0
-    assert lib.tmac_bell_bias_grad(*bad) == -4           # 16-bit only
+    bad = list(g); bad[7] = 7
+    assert lib.tmac_bell_bias_grad(*bad) == -4           # not a dtype
+    bad = list(g); bad[7] = 0; bad[6] = 642
+    assert lib.tmac_bell_bias_grad(*bad) == -2           # fp32: N % 4
     bad = list(g); bad[4] = ws.value - 1
     assert lib.tmac_bell_bias_grad(*bad) == -6
     bad = list(g); bad[0] = MISALIGNED
@@ -238,8 +240,8 @@ def test_fused_gelu_argument_errors(lib):
           1, None]
     bad = list(ok); bad[10] = None
     assert lib.tmac_bell_fwd_gelu_aux(*bad) == -1        # Z required
-    bad = list(ok); bad[16] = 0
-    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -4        # 16-bit only
+    bad = list(ok); bad[16] = 7
+    assert lib.tmac_bell_fwd_gelu_aux(*bad) == -4        # not a dtype
     bad = list(ok); bad[11] = 10200
     assert lib.tmac_bell_fwd_gelu_aux(*bad) == -2        # ldz < N
     bad = list(ok); bad[10] = MISALIGNED
@@ -255,8 +257,10 @@ def test_fused_gelu_argument_errors(lib):
     assert lib.tmac_bell_gelu_bwd(*bad) == -1            # bias gradient needs the workspace
     bad = list(g); bad[10] = 2564
     assert lib.tmac_bell_gelu_bwd(*bad) == -2            # N % 8
-    bad = list(g); bad[11] = 0
-    assert lib.tmac_bell_gelu_bwd(*bad) == -4
+    bad = list(g); bad[11] = 7
+    assert lib.tmac_bell_gelu_bwd(*bad) == -4            # not a dtype
+    bad = list(g); bad[11] = 0; bad[10] = 2562
+    assert lib.tmac_bell_gelu_bwd(*bad) == -2            # fp32: N % 4
     bad = list(g); bad[8] = ws.value - 1
     assert lib.tmac_bell_gelu_bwd(*bad) == -6
     bad = list(g); bad[1] = 2568

@@ -939,8 +939,8 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_f32_kernel(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ vals,
     const int32_t* __restrict__ t_ptr, const int32_t* __restrict__ in_blk,
     const int32_t* __restrict__ t_vblk, const int32_t* __restrict__ order,
-    const float* __restrict__ bias, int epi, float* __restrict__ Y, int64_t ldy, int M, int n_out,
-    int width, int n_mtiles, int per_xcd) {
+    const float* __restrict__ bias, int epi, float* __restrict__ Y, int64_t ldy,
+    float* __restrict__ Z, int64_t ldz, int M, int n_out, int width, int n_mtiles, int per_xcd) {
   __shared__ __attribute__((aligned(16))) float xs[kBMf * kPf];  // activation tile [m][k]
   __shared__ __attribute__((aligned(16))) float ws[64 * kPf];    // weight block as Bᵀ [n][k]
 
@@ -1035,6 +1035,7 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_f32_kernel(
       const int row = m0 + 32 * wave + 8 * (j >> 2) + 4 * h + (j & 3);
       if (row >= M) continue;
       float v = acc[ct][j] + bv;
+      if (Z) Z[static_cast<int64_t>(row) * ldz + col] = v;  // pre-activation (training)
       if (epi == TMAC_EPI_GELU) v = 0.5f * v * (1.f + erff(v * 0.70710678118654752f));
       Y[static_cast<int64_t>(row) * ldy + col] = v;
     }
@@ -1230,6 +1231,61 @@ __global__ __launch_bounds__(256) void bell_gelu_bwd_kernel(
   }
 }
 
+// d/dx of the exact erf GELU, 0.5 (1 + erf(x/√2)) + x exp(-x²/2) / √(2π), with the
+// device library's erff and expf: the fp32 form (the forward's fp32 epilogue uses
+// erff as well).
+__device__ __forceinline__ float gelu_grad_f32(float x) {
+  return fmaf(x * 0.39894228040143268f, expf(-0.5f * x * x),
+              0.5f * (1.0f + erff(x * 0.70710678118654752f)));
+}
+
+// fp32 form of bell_gelu_bwd_kernel: lane = 4 columns (16 bytes), workgroup =
+// 256 columns x 4 waves, the same row walk and fixed-order sums (of gZ as
+// stored, here unrounded fp32). Grid (ceil(N / 256), parts).
+template <bool GELU = true>
+__global__ __launch_bounds__(256) void bell_gelu_bwd_f32_kernel(
+    const float* __restrict__ gA, int64_t lda, const float* __restrict__ Z, int64_t ldz,
+    float* __restrict__ gZ, int64_t ldg, float* __restrict__ part, int M, int N,
+    int rows_per_part) {
+  __shared__ float red[4][256];
+  const int cg = threadIdx.x & 63, rl = threadIdx.x >> 6;
+  const int col = blockIdx.x * 256 + cg * 4;
+  const int r0 = blockIdx.y * rows_per_part;
+  const int r1 = min(M, r0 + rows_per_part);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (col < N) {
+    for (int r = r0 + rl; r < r1; r += 16) {
+      f32x4 a[4], z[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int rr = min(r + 4 * u, r1 - 1);
+        a[u] = *reinterpret_cast<const f32x4*>(gA + static_cast<int64_t>(rr) * lda + col);
+        if constexpr (GELU) z[u] = *reinterpret_cast<const f32x4*>(Z + static_cast<int64_t>(rr) * ldz + col);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const bool valid = r + 4 * u < r1;
+        f32x4 g = a[u];
+        if constexpr (GELU) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) g[i] = a[u][i] * gelu_grad_f32(z[u][i]);
+          if (valid) *reinterpret_cast<f32x4*>(gZ + static_cast<int64_t>(r + 4 * u) * ldg + col) = g;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += valid ? g[i] : 0.f;
+      }
+    }
+  }
+  if (!part) return;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) red[rl][cg * 4 + k] = acc[k];
+  __syncthreads();
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c < N)
+    part[static_cast<int64_t>(blockIdx.y) * N + c] =
+        ((red[0][threadIdx.x] + red[1][threadIdx.x]) + red[2][threadIdx.x]) + red[3][threadIdx.x];
+}
+
 // Row parts of bell_gelu_bwd_kernel: about 128 rows each, at most kGeluParts.
 void gelu_parts(int M, int* n_parts, int* rows_per_part) {
   int p = (M + 127) / 128;
@@ -1305,8 +1361,8 @@ int bell_fwd_impl(const void* d_X, int64_t ldx, const void* d_vals, const int32_
     hipLaunchKernelGGL((bell_gemm_f32_kernel<true>), dim3(8 * pxcd), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const float*>(d_X), ldx,
                        static_cast<const float*>(d_vals), d_t_ptr, d_t_row, d_t_vblk, d_order,
-                       static_cast<const float*>(d_bias), epi, static_cast<float*>(d_Y), ldy, M,
-                       n_bcol, width, n_mt, pxcd);
+                       static_cast<const float*>(d_bias), epi, static_cast<float*>(d_Y), ldy,
+                       static_cast<float*>(d_Z), ldz, M, n_bcol, width, n_mt, pxcd);
     return launch_status();
   }
   const int n_mtiles = (M + kBM - 1) / kBM;
@@ -1357,7 +1413,6 @@ extern "C" int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* 
                                       int64_t ldz, int M, int n_brow, int n_bcol, int width,
                                       int dtype, void* stream) {
   if (!d_Z) return TMAC_ERR_NULL;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
   return bell_fwd_impl(d_X, ldx, d_vals, d_t_ptr, d_t_row, d_t_vblk, d_order, d_bias, d_Y, ldy,
                        d_Z, ldz, M, n_brow, n_bcol, width, dtype, TMAC_EPI_GELU, stream);
 }
@@ -1462,7 +1517,8 @@ extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,
     hipLaunchKernelGGL((bell_gemm_f32_kernel<false>), dim3(8 * pxcd), dim3(256), 0,
                        static_cast<hipStream_t>(stream), static_cast<const float*>(d_dY), lddy,
                        static_cast<const float*>(d_vals), nullptr, d_col_idx, nullptr, nullptr,
-                       nullptr, 0, static_cast<float*>(d_dX), lddx, M, n_brow, width, n_mt, pxcd);
+                       nullptr, 0, static_cast<float*>(d_dX), lddx, nullptr, 0, M, n_brow, width,
+                       n_mt, pxcd);
     return launch_status();
   }
   const int n_mtiles = (M + kBM - 1) / kBM;
@@ -1563,10 +1619,11 @@ extern "C" int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_
                                   size_t ws_bytes, int M, int N, int dtype, void* stream) {
   // with M = 0 the row operands are not read (empty tensors may pass null)
   if ((M > 0 && (!d_gA || !d_Z || !d_gZ)) || (d_dbias && !d_ws)) return TMAC_ERR_NULL;
-  if (M < 0 || N <= 0 || (N % 8) || ldga < N || ldz < N || ldgz < N) return TMAC_ERR_SHAPE;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
-  if (!aligned16(d_gA) || !aligned16(d_Z) || !aligned16(d_gZ) || (ldga % 8) || (ldz % 8) ||
-      (ldgz % 8))
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
+  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16 bytes
+  if (M < 0 || N <= 0 || (N % vec) || ldga < N || ldz < N || ldgz < N) return TMAC_ERR_SHAPE;
+  if (!aligned16(d_gA) || !aligned16(d_Z) || !aligned16(d_gZ) || (ldga % vec) || (ldz % vec) ||
+      (ldgz % vec))
     return TMAC_ERR_ALIGN;
   int n_parts, rows;
   gelu_parts(M, &n_parts, &rows);
@@ -1577,7 +1634,14 @@ extern "C" int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_
     part = static_cast<float*>(d_ws);
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (M > 0) {
+  if (M > 0 && dtype == TMAC_F32) {
+    const dim3 grid(static_cast<unsigned>((N + 255) / 256), static_cast<unsigned>(n_parts));
+    hipLaunchKernelGGL(bell_gelu_bwd_f32_kernel<true>, grid, dim3(256), 0, s,
+                       static_cast<const float*>(d_gA), ldga, static_cast<const float*>(d_Z), ldz,
+                       static_cast<float*>(d_gZ), ldgz, part, M, N, rows);
+    const int st = launch_status();
+    if (st != TMAC_OK) return st;
+  } else if (M > 0) {
     const dim3 grid(static_cast<unsigned>((N + 511) / 512), static_cast<unsigned>(n_parts));
     const auto* gA = static_cast<const uint16_t*>(d_gA);
     const auto* Z = static_cast<const uint16_t*>(d_Z);
@@ -1603,15 +1667,23 @@ extern "C" int tmac_bell_gelu_bwd(const void* d_gA, int64_t ldga, const void* d_
 extern "C" int tmac_bell_bias_grad(const void* d_gY, int64_t ldgy, float* d_dbias, void* d_ws,
                                    size_t ws_bytes, int M, int N, int dtype, void* stream) {
   if ((M > 0 && !d_gY) || !d_dbias || !d_ws) return TMAC_ERR_NULL;
-  if (M < 0 || N <= 0 || (N % 8) || ldgy < N) return TMAC_ERR_SHAPE;
-  if (dtype != TMAC_BF16 && dtype != TMAC_F16) return TMAC_ERR_DTYPE;
-  if (!aligned16(d_gY) || (ldgy % 8) || !aligned16(d_ws)) return TMAC_ERR_ALIGN;
+  if (dtype != TMAC_BF16 && dtype != TMAC_F16 && dtype != TMAC_F32) return TMAC_ERR_DTYPE;
+  const int vec = dtype == TMAC_F32 ? 4 : 8;  // elements per 16 bytes
+  if (M < 0 || N <= 0 || (N % vec) || ldgy < N) return TMAC_ERR_SHAPE;
+  if (!aligned16(d_gY) || (ldgy % vec) || !aligned16(d_ws)) return TMAC_ERR_ALIGN;
   int n_parts, rows;
   gelu_parts(M, &n_parts, &rows);
   if (ws_bytes < static_cast<size_t>(n_parts) * N * sizeof(float)) return TMAC_ERR_WORKSPACE;
   auto* part = static_cast<float*>(d_ws);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (M > 0) {
+  if (M > 0 && dtype == TMAC_F32) {
+    const dim3 grid(static_cast<unsigned>((N + 255) / 256), static_cast<unsigned>(n_parts));
+    hipLaunchKernelGGL(bell_gelu_bwd_f32_kernel<false>, grid, dim3(256), 0, s,
+                       static_cast<const float*>(d_gY), ldgy, nullptr, int64_t{0}, nullptr, int64_t{0},
+                       part, M, N, rows);
+    const int st = launch_status();
+    if (st != TMAC_OK) return st;
+  } else if (M > 0) {
     const dim3 grid(static_cast<unsigned>((N + 511) / 512), static_cast<unsigned>(n_parts));
     const auto* gY = static_cast<const uint16_t*>(d_gY);
     if (dtype == TMAC_BF16)

@@ -219,11 +219,9 @@ def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
                    t_ptr: torch.Tensor, t_row: torch.Tensor, t_vblk: torch.Tensor,
                    order: torch.Tensor, bias: Optional[torch.Tensor],
                    grp: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
-    """(gelu(z), z) with z = x · W + bias, both from the forward kernel's epilogue
-    (16-bit only): the training form of fc1 + GELU, z kept for the backward."""
+    """(gelu(z), z) with z = x · W + bias, both from the forward kernel's epilogue:
+    the training form of fc1 + GELU, z kept for the backward."""
     _check_values(values, "bell_fwd_gelu")
-    if values.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError(f"bell_fwd_gelu: bfloat16 or float16 only, got {values.dtype}")
     n_brow, width = int(values.shape[0]), int(values.shape[1])
     n_bcol = int(t_ptr.numel()) - 1
     K, N = BLOCK * n_brow, BLOCK * n_bcol
@@ -299,8 +297,9 @@ bell_gelu_bwd = torch.library.custom_op("titanmac::bell_gelu_bwd", mutates_args=
 
 
 def _bell_bias_grad(gy: torch.Tensor) -> torch.Tensor:
-    """fp32 column sums of a 16-bit [M, N] gradient (rows at a pitch that is a
-    multiple of 8): the bias gradient of a linear layer, summed in a fixed order."""
+    """fp32 column sums of a 16-bit or fp32 [M, N] gradient (rows at a pitch of a
+    multiple of 16 bytes): the bias gradient of a linear layer, summed in a fixed
+    order."""
     import ctypes
     M, N = gy.shape
     dev = _lib.require_device(gy, what="bell_bias_grad")
@@ -428,7 +427,7 @@ def _fwd_backward(ctx, gy):
                                                      values.dtype)
     if ctx.has_bias and ctx.needs_input_grad[7]:
         g2 = gy.reshape(-1, gy.shape[-1])
-        if g2.dtype in (torch.bfloat16, torch.float16) and g2.shape[-1] % 8 == 0:
+        if g2.dtype in (torch.bfloat16, torch.float16, torch.float32):
             gb = _bell_bias_grad(g2).to(g2.dtype)  # fixed-order fp32 column sums
         else:
             gb = g2.sum(0)
@@ -475,10 +474,9 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
     """y = activation(x · W + bias) with W = (pattern, values) in Block-ELL.
 
     activation: None or "gelu" (erf form, as nn.GELU()). The GELU is fused into
-    the kernel's store. When gradients are recorded (16-bit), the kernel also
-    stores the pre-activation, and the backward computes GELU' and the bias
-    gradient in one pass over the gradient (titanmac::bell_fwd_gelu); fp32 runs
-    the GELU as a separate op. The kernels compute in
+    the kernel's store. When gradients are recorded, the kernel also stores the
+    pre-activation, and the backward computes GELU' and the bias gradient in one
+    pass over the gradient (titanmac::bell_fwd_gelu). The kernels compute in
     bfloat16 / float16 (fp32 accumulation) or float32 (fp32 MFMA); under
     torch.autocast the inputs are cast to the autocast dtype first, as for
     nn.Linear.
@@ -495,7 +493,7 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
     idx = pattern.device_index(values.device)
     fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
         x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
-    if activation == "gelu" and not fuse and values.dtype in (torch.bfloat16, torch.float16):
+    if activation == "gelu" and not fuse and x.dtype == values.dtype:
         # training: the kernel writes gelu(z) and z; the backward runs GELU' and
         # the bias gradient in one pass (bell_fwd_gelu's autograd)
         y, _ = bell_fwd_gelu(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
