@@ -130,13 +130,23 @@ def setup_spmm(dev):
             c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
     # the headline path: the grouped forward (block-column pairs sharing block-rows, one
     # activation-tile copy per union step), what block_ell_mm runs at this shape
-    ga = kbe._grouped_args(idx["grp"], c["M"], K, c["n_bcol"], torch.bfloat16)
+    # (tiles spread over the persistent workgroups in the pattern's balanced order)
+    tord = pat.tile_order(c["M"], dev)
+    ga = kbe._grouped_args(idx["grp"], c["M"], K, c["n_bcol"], torch.bfloat16, tord)
     assert ga is not None, "config 2 is expected to take the grouped forward"
-    gargs = (_lib.ptr(X), K, _lib.ptr(V), ga[0], ga[1], ga[2], ga[3], 2, _lib.ptr(None), _lib.ptr(Y),
-             N, c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
+    gargs = (_lib.ptr(X), K, _lib.ptr(V), ga[0], ga[1], ga[2], ga[3], 2, ga[4], ga[5], _lib.ptr(None),
+             _lib.ptr(Y), N, c["M"], c["n_brow"], c["n_bcol"], c["width"], _lib.BF16, _lib.EPI_NONE, stream)
 
     def launch():
         rc = L.tmac_bell_fwd_grouped(*gargs)
+        if rc:
+            _lib.check(rc, "tmac_bell_fwd_grouped")
+
+    # the same grouped kernel with its tiles dealt round-robin (secondary figure)
+    gargs_rr = gargs[:8] + (None, 0) + gargs[10:]
+
+    def launch_rr():
+        rc = L.tmac_bell_fwd_grouped(*gargs_rr)
         if rc:
             _lib.check(rc, "tmac_bell_fwd_grouped")
 
@@ -157,7 +167,7 @@ def setup_spmm(dev):
     nnz = c["n_brow"] * c["width"]
     flops = 2 * c["M"] * nnz * BS * BS
     bytes_ = c["M"] * K * 2 + nnz * BS * BS * 2 + (c["n_bcol"] + 1 + 2 * nnz + c["n_bcol"]) * 4 + c["M"] * N * 2
-    return dict(launch=launch, launch_gather=launch_gather, launch_m64=launch_m64,
+    return dict(launch=launch, launch_rr=launch_rr, launch_gather=launch_gather, launch_m64=launch_m64,
                 weight_bytes=nnz * BS * BS * 2, flops=flops,
                 bytes=bytes_, pat=pat, X_cpu=X_cpu, V_cpu=V_cpu, keep=(X, V, Y, idx))
 
@@ -871,6 +881,7 @@ def main() -> int:
         if args.mode == "all":
             out["spmm"]["dense_ms"] = dense_gemm_baseline(spmm, dev, K, stream)
         out["spmm"]["gather_ms"] = timed(spmm["launch_gather"], K, W, stream)
+        out["spmm"]["rr_ms"] = timed(spmm["launch_rr"], K, W, stream)
         out["spmm"]["m64_ms"] = timed(spmm["launch_m64"], K, W, stream)
         out["spmm"]["m64_weight_tbs"] = spmm["weight_bytes"] / out["spmm"]["m64_ms"] / 1e9
     if args.mode in ("all", "attn", "attn_bwd"):
@@ -1026,6 +1037,7 @@ def main() -> int:
             "windowed_attn_fwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["fwd_ms"], 5),
             "windowed_attn_bwd_mask_dropout0.1_ms": round(out["attn_ex"]["mask_dropout"]["bwd_ms"], 5),
             "bell_fwd_cfg2_gather_kernel_ms": round(out["spmm"]["gather_ms"], 5),
+            "bell_fwd_cfg2_grouped_round_robin_ms": round(out["spmm"]["rr_ms"], 5),
             "bell_fwd_cfg2_m64_us": round(out["spmm"]["m64_ms"] * 1e3, 2),
             "bell_fwd_cfg2_m64_weight_tbs": round(out["spmm"]["m64_weight_tbs"], 3),
             "bell_dx_cfg4_ms": round(out["dx"]["ms"], 5),

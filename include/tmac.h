@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define TMAC_ABI_VERSION 7
+#define TMAC_ABI_VERSION 8
 #define TMAC_BLOCK 64
 
 typedef enum {
@@ -122,6 +122,26 @@ int tmac_bell_group_schedule(const int32_t* h_col_idx, int n_brow, int n_bcol, i
                              int group, int32_t* h_grp_ptr, int32_t* h_grp_out, int32_t* h_steps,
                              int capacity, int* n_groups, int* n_steps);
 
+/* Geometry of the grouped forward's launch: output rows per tile, and
+ * persistent workgroups per XCD (8 XCDs). */
+#define TMAC_BELL_GROUP_ROWS 512
+#define TMAC_BELL_GROUP_SLOTS 32
+
+/* Balanced tile order for tmac_bell_fwd_grouped (host, deterministic). The
+ * launch splits the tiles (tile = m_tile * n_groups + group, m_tile of
+ * TMAC_BELL_GROUP_ROWS rows) into 8 XCD ranges of per_xcd = ceil(n_tiles / 8)
+ * consecutive tiles, each served by n_slots = min(per_xcd, TMAC_BELL_GROUP_SLOTS)
+ * persistent workgroups in n_rounds = ceil(per_xcd / n_slots) rounds. Per XCD,
+ * each round keeps the round-robin deal's tiles (the next n_slots of the range,
+ * so the tiles that run together, and share the L2, stay the same), but hands
+ * them out longest first (union steps + 2) to the slots with the least work so
+ * far; an XCD whose deal that does not improve keeps the round-robin one.
+ * h_order[(xcd * n_rounds + round) * n_slots + slot] = tile, or -1. With h_order == NULL only *n_entries (= 8 * n_rounds * n_slots)
+ * is computed. h_grp_ptr: tmac_bell_group_schedule's output for the pattern.
+ * No counterpart in the reference. */
+int tmac_bell_group_tile_order(const int32_t* h_grp_ptr, int n_groups, int M, int32_t* h_order,
+                               int capacity, int* n_entries);
+
 /* ------------------------------------------------------------------------- */
 /* Block-ELL kernels (device).                                                */
 /* ------------------------------------------------------------------------- */
@@ -165,10 +185,15 @@ int tmac_bell_fwd_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
  * summed over its own list in the same order). 16-bit only; group must be 2;
  * d_grp_ptr/d_grp_out/d_steps: device copies of tmac_bell_group_schedule(dir 0,
  * group 2); ldx <= 2^22. Faster than tmac_bell_fwd once ceil(M/512) *
- * n_groups fills the GPU (>= 256 tiles); the Python wrapper chooses. */
+ * n_groups fills the GPU (>= 256 tiles); the Python wrapper chooses.
+ * d_tile_order (nullable): a device copy of tmac_bell_group_tile_order(same
+ * grp_ptr, same M), tile_order_len its n_entries (TMAC_ERR_SHAPE if another
+ * length); which workgroup computes which tile changes, the results do not.
+ * NULL: tiles in round-robin order within each XCD range. */
 int tmac_bell_fwd_grouped(const void* d_X, int64_t ldx, const void* d_vals,
                           const int32_t* d_grp_ptr, const int32_t* d_grp_out,
-                          const int32_t* d_steps, int n_groups, int group, const void* d_bias,
+                          const int32_t* d_steps, int n_groups, int group,
+                          const int32_t* d_tile_order, int tile_order_len, const void* d_bias,
                           void* d_Y, int64_t ldy, int M, int n_brow, int n_bcol, int width,
                           int dtype, int epi, void* stream);
 
@@ -176,6 +201,7 @@ int tmac_bell_fwd_grouped(const void* d_X, int64_t ldx, const void* d_vals,
 int tmac_bell_fwd_grouped_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
                                    const int32_t* d_grp_ptr, const int32_t* d_grp_out,
                                    const int32_t* d_steps, int n_groups, int group,
+                                   const int32_t* d_tile_order, int tile_order_len,
                                    const void* d_bias, void* d_Y, int64_t ldy, void* d_Z,
                                    int64_t ldz, int M, int n_brow, int n_bcol, int width,
                                    int dtype, void* stream);

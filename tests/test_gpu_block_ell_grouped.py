@@ -40,9 +40,10 @@ def grouped_ptrs(pat, dev):
     return base, base + 4 * (ng + 1), base + 4 * (3 * ng + 1), ng
 
 
-def run_both(pat, X, V, bias, mode, dev):
+def run_both(pat, X, V, bias, mode, dev, ordered=True):
     """(gather, grouped) outputs; mode: 'plain', 'gelu' (bias + GELU) or 'aux'
-    (bias + GELU with the pre-activation Z)."""
+    (bias + GELU with the pre-activation Z); ordered: the grouped call takes the
+    pattern's balanced tile order (else round-robin)."""
     L = _lib.lib()
     idx = pat.device_index(dev)
     M, K = X.shape
@@ -57,12 +58,14 @@ def run_both(pat, X, V, bias, mode, dev):
         epi = _lib.EPI_NONE if mode == "plain" else _lib.EPI_GELU
         if grouped:
             gp, go, st, ng = grouped_ptrs(pat, dev)
+            to = pat.tile_order(M, dev) if ordered else None
+            tp, tn = (_lib.ptr(to), to.numel()) if ordered else (None, 0)
             if mode == "aux":
-                rc = L.tmac_bell_fwd_grouped_gelu_aux(_lib.ptr(X), K, _lib.ptr(V), gp, go, st, ng, 2, b,
-                                                      _lib.ptr(Y), N, _lib.ptr(Z), N, M, pat.n_brow,
+                rc = L.tmac_bell_fwd_grouped_gelu_aux(_lib.ptr(X), K, _lib.ptr(V), gp, go, st, ng, 2, tp, tn,
+                                                      b, _lib.ptr(Y), N, _lib.ptr(Z), N, M, pat.n_brow,
                                                       pat.n_bcol, pat.width, dt, s)
             else:
-                rc = L.tmac_bell_fwd_grouped(_lib.ptr(X), K, _lib.ptr(V), gp, go, st, ng, 2, b,
+                rc = L.tmac_bell_fwd_grouped(_lib.ptr(X), K, _lib.ptr(V), gp, go, st, ng, 2, tp, tn, b,
                                              _lib.ptr(Y), N, M, pat.n_brow, pat.n_bcol, pat.width, dt,
                                              epi, s)
         else:
@@ -104,6 +107,9 @@ def test_grouped_matches_gather_and_oracle(dev, dtype, M, n_brow, n_bcol, width)
     for mode in ("plain", "gelu", "aux"):
         (y0, z0), (y1, z1) = run_both(pat, Xd, Vd, bd, mode, dev)
         assert torch.equal(y0, y1), f"{mode}: grouped Y differs from the gather kernel"
+        if mode == "plain":
+            _, (y2, _) = run_both(pat, Xd, Vd, bd, mode, dev, ordered=False)
+            assert torch.equal(y2, y1), "round-robin tile order gives other bits"
         if mode == "aux":
             assert torch.equal(z0, z1), "aux: grouped Z differs from the gather kernel"
             close(z1.float().cpu(), ref + bn)
@@ -120,6 +126,7 @@ def test_wrapper_routes_large_calls_to_grouped_kernel(dev):
     X = torch.randn(M, 64 * n_brow, generator=g).to(torch.bfloat16).to(dev)
     V = (torch.randn(n_brow, width, 64, 64, generator=g) * 0.02).to(torch.bfloat16).to(dev)
     assert kb._grouped_args(pat.device_index(dev)["grp"], M, 64 * n_brow, n_bcol, X.dtype) is not None
+    assert pat.tile_order(M, dev) is pat.tile_order(M, dev)  # cached per (device, M)
     idx = pat.device_index(dev)
     y = kb.block_ell_mm(X, V, pat)
     y_gather = kb._bell_fwd(X, V, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
@@ -136,12 +143,14 @@ def test_grouped_entry_argument_errors(dev):
     Y = torch.empty(100, 320, dtype=torch.bfloat16, device=dev)
     gp, go, st, ng = grouped_ptrs(pat, dev)
     s = _lib.stream_ptr(dev)
+    to = pat.tile_order(100, dev)
 
     def call(**kw):
-        a = dict(x=_lib.ptr(X), ldx=192, ng=ng, group=2, dt=_lib.BF16, epi=_lib.EPI_NONE, y=_lib.ptr(Y))
+        a = dict(x=_lib.ptr(X), ldx=192, ng=ng, group=2, dt=_lib.BF16, epi=_lib.EPI_NONE, y=_lib.ptr(Y),
+                 to=_lib.ptr(to), tn=to.numel())
         a.update(kw)
         return L.tmac_bell_fwd_grouped(a["x"], a["ldx"], _lib.ptr(V), gp, go, st, a["ng"], a["group"],
-                                       None, a["y"], 320, 100, 3, 5, 2, a["dt"], a["epi"], s)
+                                       a["to"], a["tn"], None, a["y"], 320, 100, 3, 5, 2, a["dt"], a["epi"], s)
 
     assert call() == 0
     assert call(group=4) == -8       # TMAC_ERR_VALUE: the kernel pairs block-columns
@@ -151,4 +160,6 @@ def test_grouped_entry_argument_errors(dev):
     assert call(ldx=(1 << 22) + 8) == -2  # beyond the 32-bit copy offsets
     assert call(y=None) == -1        # TMAC_ERR_NULL
     assert call(epi=7) == -8
+    assert call(tn=to.numel() + 1) == -2  # TMAC_ERR_SHAPE: an order of another launch
+    assert call(to=None, tn=0) == 0       # round-robin
     torch.cuda.synchronize()

@@ -114,3 +114,59 @@ def test_schedule_errors():
     assert call(cap=1) == -7
     assert call(col=np.array([[2, 0], [1, 2]], np.int32)) == -3  # unsorted row
     assert call(n_bcol=2) == -3                                   # index out of range
+
+
+def tile_order(gp, M):
+    n = ctypes.c_int()
+    L = _lib.lib()
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, len(gp) - 1, M, None, 0, ctypes.byref(n)) == 0
+    out = np.full(n.value, 7, np.int32)
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, len(gp) - 1, M, out.ctypes.data, n.value,
+                                        ctypes.byref(n)) == 0
+    return out
+
+
+@pytest.mark.parametrize("M", [1, 511, 512, 8192, 17920, 32768])
+@pytest.mark.parametrize("pat_case", ["cfg2", (10, 40, 20), (40, 10, 5), (3, 5, 2)])
+def test_tile_order_properties(M, pat_case):
+    """The balanced order is a per-XCD permutation of the launch's tiles laid out in
+    rounds of n_slots (holes -1): every tile exactly once, in its own XCD's range, at
+    most one per slot and round; its makespan (steps + 2 per tile) never exceeds the
+    round-robin deal's."""
+    if pat_case == "cfg2":
+        ci, n_bcol = np.load(GOLDEN / "bell_col_idx_cfg2.npy"), 160
+    else:
+        n_brow, n_bcol, width = pat_case
+        ci = BlockELLPattern.sample(1, n_brow, n_bcol, width).col_idx
+    gp, _, _ = schedule(ci, n_bcol, 0, 2)
+    ng = len(gp) - 1
+    n_tiles = -(-M // 512) * ng
+    per_xcd = -(-n_tiles // 8)
+    n_slots = min(per_xcd, 32)
+    n_rounds = -(-per_xcd // n_slots)
+    order = tile_order(gp, M)
+    assert order.shape == (8 * n_rounds * n_slots,)
+    lay = order.reshape(8, n_rounds, n_slots)
+    cost = lambda t: int(gp[t % ng + 1] - gp[t % ng]) + 2  # noqa: E731
+    for x in range(8):
+        got = lay[x][lay[x] >= 0]
+        want = np.arange(x * per_xcd, min(n_tiles, (x + 1) * per_xcd))
+        assert sorted(got.tolist()) == want.tolist()
+        assert (lay[x] >= -1).all()
+        load = [sum(cost(t) for t in lay[x][:, s] if t >= 0) for s in range(n_slots)]
+        rr = [sum(cost(t) for t in want[s::n_slots]) for s in range(n_slots)]
+        assert max(load) <= max(rr)
+
+
+def test_tile_order_errors():
+    L = _lib.lib()
+    gp = np.array([0, 5, 3], np.int32)  # decreasing offsets
+    n = ctypes.c_int()
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, 2, 100, None, 0, ctypes.byref(n)) == -8
+    gp = np.array([0, 5, 9], np.int32)
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, 2, 0, None, 0, ctypes.byref(n)) == -2
+    assert L.tmac_bell_group_tile_order(None, 2, 100, None, 0, ctypes.byref(n)) == -1
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, 2, 100, None, 0, ctypes.byref(n)) == 0
+    out = np.zeros(n.value, np.int32)
+    assert L.tmac_bell_group_tile_order(gp.ctypes.data, 2, 100, out.ctypes.data, n.value - 1,
+                                        ctypes.byref(n)) == -7

@@ -325,11 +325,13 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 // before the next barrier.
 //
 // Persistent: workgroup b runs on XCD b % 8 and walks that XCD's share of the
-// logical tiles (slab-major, longest group first) round-robin. After a tile's
+// logical tiles (slab-major, longest group first), in the host's balanced
+// order (tmac_bell_group_tile_order) when given, else round-robin. After a tile's
 // last step it issues the next tile's first copies and only then converts and
 // stores the finished tile, staged through the activation stage the next tile
 // does not use yet, so the stores drain while the next tile computes.
-constexpr int kGM = 512;  // output rows per grouped tile (4 waves x 128 per member)
+constexpr int kGM = TMAC_BELL_GROUP_ROWS;  // output rows per grouped tile (4 waves x 128 per member)
+static_assert(kGM == 512, "the grouped kernel's waves cover 512 rows");
 
 // s_waitcnt vmcnt(n) for a run-time n in 0..31 (exact); larger n waits for 31.
 __device__ __forceinline__ void wait_vm_upto31(int n) {
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
     const int32_t* __restrict__ grp_ptr, const int32_t* __restrict__ grp_out,
     const int32_t* __restrict__ steps, const uint16_t* __restrict__ bias, int epi,
     uint16_t* __restrict__ Y, int64_t ldy, uint16_t* __restrict__ Z, int64_t ldz, int M,
-    int n_groups, int n_tiles, int per_xcd) {
+    int n_groups, int n_tiles, int per_xcd, const int32_t* __restrict__ order, int n_rounds) {
   constexpr int G = 2;                   // members per group
   constexpr int kX = kGM * 64;           // activation tile, 16-bit elements (64 KB)
   constexpr int kW = G * 4096;           // weight slots of a stage (16 KB)
@@ -385,8 +387,27 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
 
   const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3, n_slots = gridDim.x >> 3;
   const int t_end = min(n_tiles, (xcd + 1) * per_xcd);
-  int t = xcd * per_xcd + slot;
-  if (t >= t_end) return;
+  // This slot's tiles, round by round: the host's balanced order (entry (xcd *
+  // n_rounds + round) * n_slots + slot; -1 or out of range: none that round), or
+  // tiles xcd * per_xcd + slot + round * n_slots of the XCD's range.
+  auto tile_of = [&](int r) {
+    if (order) {
+      const int t = order[(xcd * n_rounds + r) * n_slots + slot];
+      return t >= 0 && t < n_tiles ? t : -1;
+    }
+    const int t = xcd * per_xcd + slot + r * n_slots;
+    return t < t_end ? t : -1;
+  };
+  auto next_tile = [&](int& r) {  // first tile at round >= r (r advanced to it), or -1
+    for (; r < n_rounds; ++r) {
+      const int t = tile_of(r);
+      if (t >= 0) return t;
+    }
+    return -1;
+  };
+  int rnd = 0;
+  int t = next_tile(rnd);
+  if (t < 0) return;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -531,8 +552,9 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
     // every wave is done with the ring before the next tile's copies go in
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     asm volatile("s_barrier" ::: "memory");
-    const int t_next = t + n_slots;
-    const bool more = t_next < t_end;
+    ++rnd;
+    const int t_next = next_tile(rnd);
+    const bool more = t_next >= 0;
     if (more) {
       t = t_next;
       mtile = t / n_groups;
@@ -1423,8 +1445,9 @@ namespace {
 // per XCD), fewer when there are fewer tiles.
 int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, const int32_t* d_grp_ptr,
                           const int32_t* d_grp_out, const int32_t* d_steps, int n_groups, int group,
-                          const void* d_bias, int epi, void* d_Y, int64_t ldy, void* d_Z, int64_t ldz,
-                          int M, int n_brow, int n_bcol, int width, int dtype, void* stream) {
+                          const int32_t* d_order, int order_len, const void* d_bias, int epi,
+                          void* d_Y, int64_t ldy, void* d_Z, int64_t ldz, int M, int n_brow,
+                          int n_bcol, int width, int dtype, void* stream) {
   if (!d_A || !d_vals || !d_grp_ptr || !d_grp_out || !d_steps || !d_Y) return TMAC_ERR_NULL;
   int st = check_bell_shape(M, n_brow, n_bcol, width);
   if (st != TMAC_OK) return st;
@@ -1445,7 +1468,11 @@ int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, cons
   const int64_t total = static_cast<int64_t>(n_mtiles) * n_groups;
   if (total > (1ll << 30)) return TMAC_ERR_SHAPE;
   const int per_xcd = static_cast<int>((total + 7) / 8);
-  const int grid = 8 * (per_xcd < 32 ? per_xcd : 32);
+  const int n_slots = per_xcd < TMAC_BELL_GROUP_SLOTS ? per_xcd : TMAC_BELL_GROUP_SLOTS;
+  const int n_rounds = (per_xcd + n_slots - 1) / n_slots;
+  // the balanced order must be tmac_bell_group_tile_order's for this launch
+  if (d_order && static_cast<int64_t>(order_len) != 8ll * n_rounds * n_slots) return TMAC_ERR_SHAPE;
+  const int grid = 8 * n_slots;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* A = static_cast<const uint16_t*>(d_A);
   const auto* V = static_cast<const uint16_t*>(d_vals);
@@ -1457,7 +1484,7 @@ int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, cons
 #define TMAC_GG_LAUNCH(DT, E)                                                                       \
   hipLaunchKernelGGL((bell_ggemm_kernel<DT, E>), dim3(grid), dim3(512), 0, s, A, lda, V, d_grp_ptr, \
                      d_grp_out, d_steps, b, epi, Y, ldy, Z, ldz, M, n_groups,                      \
-                     static_cast<int>(total), per_xcd)
+                     static_cast<int>(total), per_xcd, d_order, n_rounds)
   if (dtype == TMAC_BF16) {
     if (epi_any)
       TMAC_GG_LAUNCH(TMAC_BF16, true);
@@ -1478,23 +1505,25 @@ int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, cons
 extern "C" int tmac_bell_fwd_grouped(const void* d_X, int64_t ldx, const void* d_vals,
                                      const int32_t* d_grp_ptr, const int32_t* d_grp_out,
                                      const int32_t* d_steps, int n_groups, int group,
+                                     const int32_t* d_tile_order, int tile_order_len,
                                      const void* d_bias, void* d_Y, int64_t ldy, int M, int n_brow,
                                      int n_bcol, int width, int dtype, int epi, void* stream) {
   return bell_fwd_grouped_impl(d_X, ldx, d_vals, d_grp_ptr, d_grp_out, d_steps, n_groups, group,
-                               d_bias, epi, d_Y, ldy, nullptr, 0, M, n_brow, n_bcol, width, dtype,
-                               stream);
+                               d_tile_order, tile_order_len, d_bias, epi, d_Y, ldy, nullptr, 0, M,
+                               n_brow, n_bcol, width, dtype, stream);
 }
 
 extern "C" int tmac_bell_fwd_grouped_gelu_aux(const void* d_X, int64_t ldx, const void* d_vals,
                                               const int32_t* d_grp_ptr, const int32_t* d_grp_out,
                                               const int32_t* d_steps, int n_groups, int group,
+                                              const int32_t* d_tile_order, int tile_order_len,
                                               const void* d_bias, void* d_Y, int64_t ldy, void* d_Z,
                                               int64_t ldz, int M, int n_brow, int n_bcol, int width,
                                               int dtype, void* stream) {
   if (!d_Z) return TMAC_ERR_NULL;
   return bell_fwd_grouped_impl(d_X, ldx, d_vals, d_grp_ptr, d_grp_out, d_steps, n_groups, group,
-                               d_bias, TMAC_EPI_GELU, d_Y, ldy, d_Z, ldz, M, n_brow, n_bcol, width,
-                               dtype, stream);
+                               d_tile_order, tile_order_len, d_bias, TMAC_EPI_GELU, d_Y, ldy, d_Z,
+                               ldz, M, n_brow, n_bcol, width, dtype, stream);
 }
 
 extern "C" int tmac_bell_dx(const void* d_dY, int64_t lddy, const void* d_vals,

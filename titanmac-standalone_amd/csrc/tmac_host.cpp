@@ -238,6 +238,68 @@ extern "C" int tmac_bell_group_schedule(const int32_t* h_col_idx, int n_brow, in
   return TMAC_OK;
 }
 
+extern "C" int tmac_bell_group_tile_order(const int32_t* h_grp_ptr, int n_groups, int M,
+                                          int32_t* h_order, int capacity, int* n_entries) {
+  if (!h_grp_ptr || !n_entries) return TMAC_ERR_NULL;
+  if (n_groups <= 0 || M <= 0) return TMAC_ERR_SHAPE;
+  for (int g = 0; g < n_groups; ++g)
+    if (h_grp_ptr[g + 1] < h_grp_ptr[g]) return TMAC_ERR_VALUE;
+  // the grouped launcher's split: 8 XCD ranges of per_xcd consecutive tiles
+  // (tile = m_tile * n_groups + group), min(per_xcd, 32) persistent slots each
+  const int64_t n_mtiles = (static_cast<int64_t>(M) + TMAC_BELL_GROUP_ROWS - 1) / TMAC_BELL_GROUP_ROWS;
+  const int64_t n_tiles = n_mtiles * n_groups;
+  if (n_tiles > (1ll << 30)) return TMAC_ERR_SHAPE;
+  const int per_xcd = static_cast<int>((n_tiles + 7) / 8);
+  const int n_slots = per_xcd < TMAC_BELL_GROUP_SLOTS ? per_xcd : TMAC_BELL_GROUP_SLOTS;
+  const int n_rounds = (per_xcd + n_slots - 1) / n_slots;
+  const int64_t total = 8ll * n_rounds * n_slots;
+  *n_entries = static_cast<int>(total);
+  if (!h_order) return TMAC_OK;
+  if (capacity < total) return TMAC_ERR_CAPACITY;
+  std::fill(h_order, h_order + total, -1);
+  // Per XCD, round by round, the round's tiles are those of the round-robin
+  // deal (the next n_slots of the XCD's range, so the tiles that run together,
+  // and share the L2, stay the same); longest first (steps plus a fixed cost for
+  // the prologue and epilogue; ties by tile index), they go to the slots in
+  // ascending order of their load so far (ties by slot).
+  constexpr int64_t kTileCost = 2;
+  std::vector<int> tiles, slots(n_slots);
+  std::vector<int64_t> load(n_slots);
+  auto cost = [&](int t) {
+    const int g = t % n_groups;
+    return static_cast<int64_t>(h_grp_ptr[g + 1] - h_grp_ptr[g]) + kTileCost;
+  };
+  for (int x = 0; x < 8; ++x) {
+    const int64_t t0 = static_cast<int64_t>(x) * per_xcd;
+    const int64_t t1 = std::min<int64_t>(n_tiles, t0 + per_xcd);
+    std::fill(load.begin(), load.end(), 0);
+    for (int r = 0; r < n_rounds; ++r) {
+      tiles.clear();
+      for (int64_t t = t0 + static_cast<int64_t>(r) * n_slots; t < t1 && tiles.size() < static_cast<size_t>(n_slots); ++t)
+        tiles.push_back(static_cast<int>(t));
+      std::stable_sort(tiles.begin(), tiles.end(), [&](int a, int b) { return cost(a) > cost(b); });
+      for (int j = 0; j < n_slots; ++j) slots[j] = j;
+      std::stable_sort(slots.begin(), slots.end(), [&](int a, int b) { return load[a] < load[b]; });
+      for (size_t j = 0; j < tiles.size(); ++j) {
+        const int sl = slots[j];
+        h_order[(static_cast<int64_t>(x) * n_rounds + r) * n_slots + sl] = tiles[j];
+        load[sl] += cost(tiles[j]);
+      }
+    }
+    // keep the round-robin deal where the greedy one is not better
+    std::vector<int64_t> rr(n_slots, 0);
+    for (int64_t t = t0; t < t1; ++t) rr[(t - t0) % n_slots] += cost(static_cast<int>(t));
+    if (*std::max_element(load.begin(), load.end()) > *std::max_element(rr.begin(), rr.end())) {
+      for (int r = 0; r < n_rounds; ++r)
+        for (int sl = 0; sl < n_slots; ++sl) {
+          const int64_t t = t0 + static_cast<int64_t>(r) * n_slots + sl;
+          h_order[(static_cast<int64_t>(x) * n_rounds + r) * n_slots + sl] = t < t1 ? static_cast<int>(t) : -1;
+        }
+    }
+  }
+  return TMAC_OK;
+}
+
 // ---------------------------------------------------------------------------
 // Attention tile maps
 // ---------------------------------------------------------------------------

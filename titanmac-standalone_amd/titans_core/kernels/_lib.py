@@ -15,7 +15,7 @@ from pathlib import Path
 
 import torch  # the HIP runtime torch loads (libamdhip64.so.7) also serves libtmac.so
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, BF16, F16 = 0, 1, 2
 EPI_NONE, EPI_GELU = 0, 1
@@ -43,10 +43,11 @@ SIGNATURES = {
     "tmac_bell_transpose": [_vp, _i, _i, _i, _vp, _vp, _vp, _vp],
     "tmac_bell_group_schedule": [_vp, _i, _i, _i, _i, _i, _vp, _vp, _vp, _i, ctypes.POINTER(_i),
                                  ctypes.POINTER(_i)],
-    "tmac_bell_fwd_grouped": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _i, _i, _i, _i,
-                              _i, _i, _vp],
-    "tmac_bell_fwd_grouped_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _vp, _i64, _vp,
-                                       _i64, _i, _i, _i, _i, _i, _vp],
+    "tmac_bell_group_tile_order": [_vp, _i, _i, _vp, _i, ctypes.POINTER(_i)],
+    "tmac_bell_fwd_grouped": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _i64, _i, _i,
+                              _i, _i, _i, _i, _vp],
+    "tmac_bell_fwd_grouped_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _i, _i, _vp, _i, _vp, _vp, _i64,
+                                       _vp, _i64, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_fwd": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i, _i, _i, _i, _i, _i, _vp],
     "tmac_bell_fwd_gelu_aux": [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp, _i64, _i, _i, _i,
                                _i, _i, _vp],

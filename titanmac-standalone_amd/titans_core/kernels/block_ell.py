@@ -39,8 +39,9 @@ class BlockELLPattern:
     Derived (host, via libtmac): the transposed index (t_ptr, t_row, t_vblk),
     the longest-first column order used by the forward kernel, and the grouped
     forward schedule (`grp`: block-columns paired by shared block-rows, see
-    tmac_bell_group_schedule), packed as [grp_ptr, grp_out, steps].
-    Device copies are cached per device.
+    tmac_bell_group_schedule), packed as [grp_ptr, grp_out, steps], and per row
+    count the balanced order of its tiles over the persistent workgroups
+    (tmac_bell_group_tile_order). Device copies are cached per device.
     """
 
     def __init__(self, col_idx, n_bcol: int):
@@ -63,6 +64,7 @@ class BlockELLPattern:
                    "Block-ELL transpose")
         self.grp = self._group_schedule(L)
         self._dev = {}
+        self._tord = {}
 
     def _group_schedule(self, L) -> np.ndarray:
         """The forward's pair schedule, packed as one int32 array:
@@ -105,6 +107,26 @@ class BlockELLPattern:
         m = np.zeros((self.n_brow, self.n_bcol), dtype=bool)
         m[np.arange(self.n_brow)[:, None], self.col_idx] = True
         return m
+
+    def tile_order(self, M: int, device: torch.device) -> torch.Tensor:
+        """Device copy of the grouped forward's balanced tile order for M rows
+        (tmac_bell_group_tile_order), cached per (device, M)."""
+        import ctypes
+        device = torch.device(device)
+        key = (str(device), int(M))
+        t = self._tord.get(key)
+        if t is None:
+            L = _lib.lib()
+            ng = (self.n_bcol + 1) // 2
+            gp = np.ascontiguousarray(self.grp[:ng + 1])
+            n = ctypes.c_int(0)
+            _lib.check(L.tmac_bell_group_tile_order(gp.ctypes.data, ng, int(M), None, 0, ctypes.byref(n)),
+                       "Block-ELL tile order")
+            out = np.empty(n.value, dtype=np.int32)
+            _lib.check(L.tmac_bell_group_tile_order(gp.ctypes.data, ng, int(M), out.ctypes.data, n.value,
+                                                    ctypes.byref(n)), "Block-ELL tile order")
+            t = self._tord[key] = torch.from_numpy(out).to(device)
+        return t
 
     def device_index(self, device: torch.device) -> dict:
         device = torch.device(device)
@@ -152,23 +174,26 @@ def _check_values(values: torch.Tensor, what: str) -> None:
 _GROUPED_MIN_TILES = 256  # the grouped kernel runs one persistent workgroup per CU
 
 
-def _grouped_args(grp: Optional[torch.Tensor], M: int, ldx: int, n_bcol: int, dtype) -> Optional[tuple]:
-    """(grp_ptr, grp_out, steps, n_groups) device pointers for tmac_bell_fwd_grouped when
-    it applies (16-bit, more than 64 rows, enough 512-row x 2-column tiles to fill the
-    GPU, row pitch within its 32-bit offsets), else None (tmac_bell_fwd)."""
+def _grouped_args(grp: Optional[torch.Tensor], M: int, ldx: int, n_bcol: int, dtype,
+                  tord: Optional[torch.Tensor] = None) -> Optional[tuple]:
+    """(grp_ptr, grp_out, steps, n_groups, tile_order, tile_order_len) for
+    tmac_bell_fwd_grouped when it applies (16-bit, more than 64 rows, enough 512-row x
+    2-column tiles to fill the GPU, row pitch within its 32-bit offsets), else None
+    (tmac_bell_fwd). `tord`: the pattern's tile_order(M) (None: round-robin)."""
     if grp is None or dtype not in (torch.bfloat16, torch.float16) or M <= 64 or ldx > (1 << 22):
         return None
     ng = (n_bcol + 1) // 2
     if -(-M // 512) * ng < _GROUPED_MIN_TILES:
         return None
     base = grp.data_ptr()
-    return base, base + 4 * (ng + 1), base + 4 * (3 * ng + 1), ng
+    to = (tord.data_ptr(), int(tord.numel())) if tord is not None else (None, 0)
+    return (base, base + 4 * (ng + 1), base + 4 * (3 * ng + 1), ng) + to
 
 
 def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_ptr: torch.Tensor,
               t_row: torch.Tensor, t_vblk: torch.Tensor, order: torch.Tensor,
               bias: Optional[torch.Tensor], gelu: bool,
-              grp: Optional[torch.Tensor] = None) -> torch.Tensor:
+              grp: Optional[torch.Tensor] = None, tord: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = (gelu)(x · W + bias) with W in Block-ELL; x [..., 64*n_brow] -> y [..., 64*n_bcol].
     With the pattern's grouped schedule `grp`, large 16-bit calls run the grouped
     kernel (bitwise-identical results)."""
@@ -189,13 +214,13 @@ def _bell_fwd(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor, t_pt
     M = x2.shape[0]
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
-        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype)
+        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype, tord)
         epi = _lib.EPI_GELU if gelu else _lib.EPI_NONE
         with _lib.device_guard(dev):
             if ga is not None:
                 rc = _lib.lib().tmac_bell_fwd_grouped(
                     _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), ga[0], ga[1], ga[2], ga[3], 2,
-                    _lib.ptr(bias), _lib.ptr(y), N, M, n_brow, n_bcol, width,
+                    ga[4], ga[5], _lib.ptr(bias), _lib.ptr(y), N, M, n_brow, n_bcol, width,
                     _lib.dtype_code(x.dtype), epi, _lib.stream_ptr(dev))
             else:
                 rc = _lib.lib().tmac_bell_fwd(
@@ -210,7 +235,7 @@ bell_fwd = torch.library.custom_op("titanmac::bell_fwd", mutates_args=())(_bell_
 
 
 @bell_fwd.register_fake
-def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, grp=None):
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, grp=None, tord=None):
     n_bcol = t_ptr.shape[0] - 1
     return x.new_empty((*x.shape[:-1], BLOCK * n_bcol))
 
@@ -218,7 +243,8 @@ def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, grp=None):
 def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
                    t_ptr: torch.Tensor, t_row: torch.Tensor, t_vblk: torch.Tensor,
                    order: torch.Tensor, bias: Optional[torch.Tensor],
-                   grp: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+                   grp: Optional[torch.Tensor] = None,
+                   tord: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """(gelu(z), z) with z = x · W + bias, both from the forward kernel's epilogue:
     the training form of fc1 + GELU, z kept for the backward."""
     _check_values(values, "bell_fwd_gelu")
@@ -239,12 +265,12 @@ def _bell_fwd_gelu(x: torch.Tensor, values: torch.Tensor, col_idx: torch.Tensor,
     y = torch.empty((M, N), dtype=x.dtype, device=dev)
     z = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M > 0:
-        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype)
+        ga = _grouped_args(grp, M, ldx, n_bcol, x.dtype, tord)
         with _lib.device_guard(dev):
             if ga is not None:
                 rc = _lib.lib().tmac_bell_fwd_grouped_gelu_aux(
                     _lib.ptr(x2), ldx, _lib.ptr(values.contiguous()), ga[0], ga[1], ga[2], ga[3], 2,
-                    _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M, n_brow, n_bcol, width,
+                    ga[4], ga[5], _lib.ptr(bias), _lib.ptr(y), N, _lib.ptr(z), N, M, n_brow, n_bcol, width,
                     _lib.dtype_code(x.dtype), _lib.stream_ptr(dev))
             else:
                 rc = _lib.lib().tmac_bell_fwd_gelu_aux(
@@ -260,7 +286,7 @@ bell_fwd_gelu = torch.library.custom_op("titanmac::bell_fwd_gelu", mutates_args=
 
 
 @bell_fwd_gelu.register_fake
-def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, grp=None):
+def _(x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, grp=None, tord=None):
     shape = (*x.shape[:-1], BLOCK * (t_ptr.shape[0] - 1))
     return x.new_empty(shape), x.new_empty(shape)
 
@@ -400,7 +426,7 @@ def _sddmm_workspace_bytes(L, M: int, n_brow: int, n_bcol: int, width: int) -> i
 
 
 def _fwd_setup_context(ctx, inputs, output):
-    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, _grp = inputs
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, gelu, _grp, _tord = inputs
     if gelu:
         # The fused activation keeps no pre-activation for the backward; the
         # module only fuses GELU when no gradient is needed.
@@ -431,14 +457,14 @@ def _fwd_backward(ctx, gy):
             gb = _bell_bias_grad(g2).to(g2.dtype)  # fixed-order fp32 column sums
         else:
             gb = g2.sum(0)
-    return gx, gv, None, None, None, None, None, gb, None, None
+    return gx, gv, None, None, None, None, None, gb, None, None, None
 
 
 bell_fwd.register_autograd(_fwd_backward, setup_context=_fwd_setup_context)
 
 
 def _fwd_gelu_setup_context(ctx, inputs, output):
-    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, _grp = inputs
+    x, values, col_idx, t_ptr, t_row, t_vblk, order, bias, _grp, _tord = inputs
     ctx.mark_non_differentiable(output[1])
     ctx.set_materialize_grads(False)  # no zero-filled gradient for the pre-activation output
     ctx.save_for_backward(x, values, col_idx, output[1])
@@ -463,7 +489,7 @@ def _fwd_gelu_backward(ctx, ga, _gz_unused):
         gv = bell_sddmm(x, gz, col_idx, n_brow, width, values.dtype)
     if want_b:
         gb = db.to(ctx.bias_dtype)
-    return gx, gv, None, None, None, None, None, gb, None
+    return gx, gv, None, None, None, None, None, gb, None, None
 
 
 bell_fwd_gelu.register_autograd(_fwd_gelu_backward, setup_context=_fwd_gelu_setup_context)
@@ -491,17 +517,21 @@ def block_ell_mm(x: torch.Tensor, values: torch.Tensor, pattern: BlockELLPattern
             x, values = x.to(dt), values.to(dt)
             bias = bias.to(dt) if bias is not None else None
     idx = pattern.device_index(values.device)
+    # the balanced tile order for this row count, where the grouped kernel would run
+    M = x.numel() // x.shape[-1] if x.shape[-1] else 0
+    tord = (pattern.tile_order(M, values.device)
+            if values.is_cuda and values.dtype in (torch.bfloat16, torch.float16) and M > 64 else None)
     fuse = activation == "gelu" and not (torch.is_grad_enabled() and (
         x.requires_grad or values.requires_grad or (bias is not None and bias.requires_grad)))
     if activation == "gelu" and not fuse and x.dtype == values.dtype:
         # training: the kernel writes gelu(z) and z; the backward runs GELU' and
         # the bias gradient in one pass (bell_fwd_gelu's autograd)
         y, _ = bell_fwd_gelu(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"],
-                             idx["order"], bias, idx["grp"])
+                             idx["order"], bias, idx["grp"], tord)
         return y
     op = _bell_fwd if _lib.direct_call(x, values, bias) else bell_fwd
     y = op(x, values, idx["col_idx"], idx["t_ptr"], idx["t_row"], idx["t_vblk"], idx["order"], bias,
-           fuse, idx["grp"])
+           fuse, idx["grp"], tord)
     if activation == "gelu" and not fuse:
         y = torch.nn.functional.gelu(y)
     return y
