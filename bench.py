@@ -86,6 +86,22 @@ def band_pairs(S: int, w: int, Np: int) -> int:
     return Np * Np + T * Np + a * (a - 1) // 2 + (T - a) * w + T
 
 
+CLOCK_SETTLE_S = 0.1  # untimed load before the headline's warmup (see settle)
+
+
+def settle(launch, seconds: float) -> None:
+    """Back-to-back launches of the workload for `seconds` of wall time, untimed. An
+    MI355X coming out of idle runs its first ≈ 10–20 ms of load below its sustained
+    clock (the SpMM's first block of launches after even a 2 s pause takes ≈ 160 µs
+    per launch, the following ones 133–144 µs), so without this the timed steps would
+    measure the ramp from idle rather than the throughput of a running job."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            launch()
+        torch.cuda.synchronize()
+
+
 def timed(launch, steps: int, warmup: int, stream) -> float:
     """Mean ms per launch over exactly `steps` back-to-back launches after `warmup`
     untimed ones: the device is synchronised, one HIP event is recorded on the launch
@@ -875,6 +891,7 @@ def main() -> int:
     out = {}
     if args.mode in ("all", "spmm"):
         spmm = setup_spmm(dev)
+        settle(spmm["launch"], CLOCK_SETTLE_S)
         ms = timed(spmm["launch"], K, W, stream)
         out["spmm"] = dict(ms=ms, tflops=spmm["flops"] / ms / 1e9, flops=spmm["flops"],
                            bytes=spmm["bytes"])
@@ -989,6 +1006,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
+        "clock_settle_s": CLOCK_SETTLE_S,
         "ms_per_step": round(s["ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
