@@ -310,16 +310,20 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 // there. A member's active steps are its own list in its own order, so each
 // output is summed exactly as in bell_gemm_kernel (bitwise-identical results).
 //
-// Tiles are 512 rows by 2 block-columns; 8 waves, wave w owns rows
-// 128 (w % 4) .. +127 of member w / 4 (4 x 2 MFMA tiles, 32 MFMAs per step),
-// so the two waves on each SIMD cover both members and every SIMD gets the
-// same MFMA work per step.
+// Tiles are 512 rows by 2 block-columns, 4R waves per member (R = 1 or 2):
+// wave w owns rows (128 / R)(w % 4R) .. +128/R - 1 of member w / 4R (4/R x 2
+// MFMA tiles, 32/R MFMAs per step), so every SIMD holds waves of both members
+// and gets the same MFMA work per step. R = 2 (16 waves, 128 VGPRs, four per
+// SIMD) runs the plain forward: the waves cover each other's LDS and copy
+// latency, so operands are read just before their MFMAs; R = 1 (8 waves, two per
+// SIMD, operands for k-step kk + 1 read before the MFMAs of kk) runs the bias /
+// GELU / Z epilogue, whose registers do not fit 128.
 //
 // Copies: global_load_lds (1 KB per wave instruction, eight lanes per 128-byte
 // row) written as assembly with an SGPR base and per-lane 32-bit offsets fixed
 // for the tile, into a two-stage ring (activation tile 64 KB + two weight
-// slots 16 KB per stage, all of LDS). Each wave copies 64 rows of the
-// activation tile and, when its member is active, 16 rows of that member's
+// slots 16 KB per stage, all of LDS). Each wave copies 64/R rows of the
+// activation tile and, when its member is active, 16/R rows of that member's
 // weight block; the next step's copies go out right after the barrier that
 // opens a step, and each wave waits for its own copies with an exact vmcnt
 // before the next barrier.
@@ -330,7 +334,7 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
 // last step it issues the next tile's first copies and only then converts and
 // stores the finished tile, staged through the activation stage the next tile
 // does not use yet, so the stores drain while the next tile computes.
-constexpr int kGM = TMAC_BELL_GROUP_ROWS;  // output rows per grouped tile (4 waves x 128 per member)
+constexpr int kGM = TMAC_BELL_GROUP_ROWS;  // output rows per grouped tile
 static_assert(kGM == 512, "the grouped kernel's waves cover 512 rows");
 
 // s_waitcnt vmcnt(n) for a run-time n in 0..31 (exact); larger n waits for 31.
@@ -372,14 +376,19 @@ __device__ __forceinline__ void wait_vm_upto31(int n) {
   }
 }
 
-template <int DT, bool EPI>
-__global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
+template <int DT, bool EPI, int R>
+__global__ __launch_bounds__(512 * R, 1) void bell_ggemm_kernel(
     const uint16_t* __restrict__ A, int64_t lda, const uint16_t* __restrict__ vals,
     const int32_t* __restrict__ grp_ptr, const int32_t* __restrict__ grp_out,
     const int32_t* __restrict__ steps, const uint16_t* __restrict__ bias, int epi,
     uint16_t* __restrict__ Y, int64_t ldy, uint16_t* __restrict__ Z, int64_t ldz, int M,
     int n_groups, int n_tiles, int per_xcd, const int32_t* __restrict__ order, int n_rounds) {
   constexpr int G = 2;                   // members per group
+  constexpr int NQ = 4 * R;              // waves per member, each on kGM / NQ rows
+  constexpr int RW = kGM / NQ;           // output rows per wave (128 or 64)
+  constexpr int MI = RW / 32;            // 32-row MFMA tiles per wave
+  constexpr int XI = 8 / R;              // 8-row activation copies per wave and step
+  constexpr int WI = 2 / R;              // 8-row weight copies per wave and step
   constexpr int kX = kGM * 64;           // activation tile, 16-bit elements (64 KB)
   constexpr int kW = G * 4096;           // weight slots of a stage (16 KB)
   constexpr int kRec = 1 + G;            // step record: block-row, G value blocks (-1: none)
@@ -411,17 +420,17 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int q = wave & 3, mem = wave >> 2;
+  const int q = wave % NQ, mem = wave / NQ;
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;  // which 16-column half of a 32-wide MFMA tile
   const int drow = lane >> 3, dpos = lane & 7;
   // Per-lane copy offsets (bytes). Lane L of an instruction covering rows
   // R..R+7 fills LDS chunk position L & 7 of row R + L / 8 and fetches the
   // global chunk that the swizzle stores there.
-  uint32_t woff[2];
+  uint32_t woff[WI];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = 16 * q + 8 * j + drow;
+  for (int j = 0; j < WI; ++j) {
+    const int row = 8 * WI * q + 8 * j + drow;
     const int a = (row >> 1) & 7;
     woff[j] = static_cast<uint32_t>(row * 128 + 16 * (dpos ^ (((a & 1) << 2) | (a >> 1))));
   }
@@ -433,12 +442,12 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
   const int32_t* rec0 = steps + static_cast<int64_t>(grp_ptr[gi]) * kRec;
   int m_tile0 = mtile * kGM;
   // activation rows past M read row M-1 (valid memory, results never stored)
-  uint32_t xoff[8];
+  uint32_t xoff[XI];
   auto set_xoff = [&]() {
     const int last = M - 1 - m_tile0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int row = 64 * wave + 8 * j + drow;
+    for (int j = 0; j < XI; ++j) {
+      const int row = 8 * XI * wave + 8 * j + drow;
       const int chunk = dpos ^ ((row >> 1) & 7);
       xoff[j] = static_cast<uint32_t>(min(row, last)) * static_cast<uint32_t>(2 * lda) +
                 16u * static_cast<uint32_t>(chunk);
@@ -473,42 +482,56 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
     const uint32_t sx = lds0 + static_cast<uint32_t>((gs & 1) * kX * 2);
     const uint16_t* xb = A + static_cast<int64_t>(m_tile0) * lda + static_cast<int64_t>(step_in(i)) * 64;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) dma_lds16(xb, xoff[j], sx + (64 * wave + 8 * j) * 128);
+    for (int j = 0; j < XI; ++j) dma_lds16(xb, xoff[j], sx + (8 * XI * wave + 8 * j) * 128);
     const int vb = own_vb(i);
     if (vb >= 0) {
       const uint32_t sw = lds0 + static_cast<uint32_t>((2 * kX + (gs & 1) * kW + mem * 4096) * 2);
       const uint16_t* wb = vals + static_cast<int64_t>(vb) * 4096;
 #pragma unroll
-      for (int j = 0; j < 2; ++j) dma_lds16(wb, woff[j], sw + (16 * q + 8 * j) * 128);
+      for (int j = 0; j < WI; ++j) dma_lds16(wb, woff[j], sw + (8 * WI * q + 8 * j) * 128);
     }
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[MI][2];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
   // MFMA operands of k-step kk: the wave's activation rows (B operand, 16-byte
   // reads of the swizzled tile) and its member's weight block (A operand,
   // transpose reads: W is N-contiguous but the reduction runs over K).
-  auto read_ops = [&](u32x4(&xa)[4], u32x4(&wf)[2], const uint16_t* xt, const uint16_t* wt, int kk) {
+  auto read_ops = [&](u32x4(&xa)[MI], u32x4(&wf)[2], const uint16_t* xt, const uint16_t* wt, int kk) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) xa[mi] = lds16(xt + xswz(128 * q + 32 * mi + l32, 2 * kk + h));
+    for (int mi = 0; mi < MI; ++mi) xa[mi] = lds16(xt + xswz(RW * q + 32 * mi + l32, 2 * kk + h));
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) wf[ni] = lds_read_tr8_swz64(wt, 16 * kk + 8 * h, 32 * ni + 16 * grp, lane);
   };
   // operand reads of k-step kk + 1 are issued before the MFMAs of k-step kk
   auto compute = [&](const uint16_t* xt, const uint16_t* wt) {
-    u32x4 xa[2][4], wf[2][2];
-    read_ops(xa[0], wf[0], xt, wt, 0);
+    if constexpr (R == 1) {
+      u32x4 xa[2][MI], wf[2][2];
+      read_ops(xa[0], wf[0], xt, wt, 0);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], xt, wt, kk + 1);
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk + 1 < 4) read_ops(xa[(kk + 1) & 1], wf[(kk + 1) & 1], xt, wt, kk + 1);
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni)
-          acc[mi][ni] = Mfma<DT>::run(wf[kk & 1][ni], xa[kk & 1][mi], acc[mi][ni]);
+          for (int ni = 0; ni < 2; ++ni)
+            acc[mi][ni] = Mfma<DT>::run(wf[kk & 1][ni], xa[kk & 1][mi], acc[mi][ni]);
+      }
+    } else {
+      // four waves per SIMD cover each other's LDS latency: no operand double buffer
+      u32x4 xa[MI], wf[2];
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        read_ops(xa, wf, xt, wt, kk);
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+          for (int ni = 0; ni < 2; ++ni)
+            acc[mi][ni] = Mfma<DT>::run(wf[ni], xa[mi], acc[mi][ni]);
+      }
     }
   };
 
@@ -535,7 +558,7 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
     }
     gs += n_steps;
     const int ob = grp_out[gi * G + mem];
-    const int m_out = m_tile0 + 128 * q;
+    const int m_out = m_tile0 + RW * q;
     const int64_t col0 = static_cast<int64_t>(ob) * 64;
     // The bias of this lane's 32 columns, loaded and waited for before the
     // next tile's copies are issued, so that no wait on it covers them.
@@ -602,7 +625,7 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
         }
       };
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
+      for (int mi = 0; mi < MI; ++mi) {
         if (EPI && bias) {
 #pragma unroll
           for (int ni = 0; ni < 2; ++ni)
@@ -628,7 +651,7 @@ __global__ __launch_bounds__(512, 1) void bell_ggemm_kernel(
     if (!more) break;
     pending = n_st;
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = f32x16{};
   }
@@ -1481,20 +1504,23 @@ int bell_fwd_grouped_impl(const void* d_A, int64_t lda, const void* d_vals, cons
   auto* Z = static_cast<uint16_t*>(d_Z);
   // the epilogue's bias / activation / Z code is compiled only where used
   const bool epi_any = b || Z || epi != TMAC_EPI_NONE;
-#define TMAC_GG_LAUNCH(DT, E)                                                                       \
-  hipLaunchKernelGGL((bell_ggemm_kernel<DT, E>), dim3(grid), dim3(512), 0, s, A, lda, V, d_grp_ptr, \
+#define TMAC_GG_LAUNCH(DT, E, R)                                                                    \
+  hipLaunchKernelGGL((bell_ggemm_kernel<DT, E, R>), dim3(grid), dim3(512 * R), 0, s, A, lda, V, d_grp_ptr, \
                      d_grp_out, d_steps, b, epi, Y, ldy, Z, ldz, M, n_groups,                      \
                      static_cast<int>(total), per_xcd, d_order, n_rounds)
+  // Without an epilogue: 16 waves (64 rows each, 128 VGPRs, four waves per SIMD to
+  // cover each other's LDS and copy latency). The bias / GELU / Z epilogue needs more
+  // registers than that allows without spilling: 8 waves of 128 rows.
   if (dtype == TMAC_BF16) {
     if (epi_any)
-      TMAC_GG_LAUNCH(TMAC_BF16, true);
+      TMAC_GG_LAUNCH(TMAC_BF16, true, 1);
     else
-      TMAC_GG_LAUNCH(TMAC_BF16, false);
+      TMAC_GG_LAUNCH(TMAC_BF16, false, 2);
   } else {
     if (epi_any)
-      TMAC_GG_LAUNCH(TMAC_F16, true);
+      TMAC_GG_LAUNCH(TMAC_F16, true, 1);
     else
-      TMAC_GG_LAUNCH(TMAC_F16, false);
+      TMAC_GG_LAUNCH(TMAC_F16, false, 2);
   }
 #undef TMAC_GG_LAUNCH
   return launch_status();
