@@ -69,6 +69,12 @@ __device__ __forceinline__ u32x4 lds_read_tr8_swz64(const uint16_t* tile, int r0
 
 typedef __attribute__((address_space(3))) void lds_void;
 
+// 16-byte store marked non-temporal (streamed past the caches' normal
+// replacement), for outputs no kernel of the same launch reads again.
+__device__ __forceinline__ void stg16_nt(uint16_t* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
 // Direct HBM/L2 -> LDS copy of 1 KB: lane L of the wave moves the 16 bytes at
 // src (its own address) to lds_base + 16 L. lds_base must be wave-uniform.
 __device__ __forceinline__ void dma16(const uint16_t* src, uint16_t* lds_base) {
@@ -294,8 +300,8 @@ __global__ __launch_bounds__(256, 2) void bell_gemm_kernel(
     const int row = it * 8 + (lane >> 3), ch = lane & 7;
     const int grow = m_base + row;
     if (grow < M) {
-      stg16(Y + static_cast<int64_t>(grow) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
-      if (Z) stg16(Z + static_cast<int64_t>(grow) * ldz + col0 + ch * 8, lds16(stage_z + row * kPitch + ch * 8));
+      stg16_nt(Y + static_cast<int64_t>(grow) * ldy + col0 + ch * 8, lds16(stage + row * kPitch + ch * 8));
+      if (Z) stg16_nt(Z + static_cast<int64_t>(grow) * ldz + col0 + ch * 8, lds16(stage_z + row * kPitch + ch * 8));
     }
   }
 }
@@ -619,7 +625,7 @@ __global__ __launch_bounds__(512 * R, 1) void bell_ggemm_kernel(
             const int row = 8 * it + (lane >> 3), ch = lane & 7;
             const u32x4 v4 = lds16(stage + row * 64 + ((ch ^ (row & 7)) << 3));
             if (base + (lane >> 3) < M)
-              stg16(out + static_cast<int64_t>(base + (lane >> 3)) * ld + col0 + ch * 8, v4);
+              stg16_nt(out + static_cast<int64_t>(base + (lane >> 3)) * ld + col0 + ch * 8, v4);
             n_st += 1;
           }
         }
