@@ -1,0 +1,74 @@
+"""GPU parity of the block-window forward where the persistent rows (n_persistent <= 32,
+all in the first 32-row slice) see every key and two waves share their key tiles (one
+32-key half each, the two softmax states merged at the end): against the fp64 oracle,
+n_persistent on both sides of 32, causal and not, head dimensions 32/64/128, and
+BASELINE config 3's shape.
+
+Bars: bf16/fp16 outputs |got - want| <= 2e-2 + 1e-2 |want| against the fp64 oracle on
+the same 16-bit inputs; the log-sum-exp within 1e-3 + 1e-4 |want| (fp32 output of fp32
+sums); reruns bitwise-identical.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oa
+from oracle import masks as om
+from titans_core.kernels import _lib
+from titans_core.kernels.window_attn import _window_attn_fwd
+
+pytestmark = pytest.mark.gpu
+
+BW = _lib.PATTERN_BLOCKWIN
+
+
+def close(got, want, atol=2e-2, rtol=1e-2, what=""):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    err = np.abs(got - want)
+    ok = err <= atol + rtol * np.abs(want)
+    assert ok.all(), f"{what} max err {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+# B, H, S, w, Np, causal, block_size, dh
+CASES = [(1, 2, 333, 128, 16, True, 64, 64), (1, 1, 700, 100, 32, True, 64, 64),
+         (1, 1, 700, 100, 33, True, 64, 64), (2, 1, 520, 64, 1, False, 32, 32),
+         (1, 2, 1000, 512, 16, True, 64, 128), (1, 1, 40, 8, 16, True, 64, 64),
+         (1, 1, 129, 0, 8, True, 64, 64), (1, 1, 300, 200, 20, False, 64, 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,S,w,Np,causal,bs,dh", CASES)
+def test_blockwin_forward_parity(dev, dtype, B, H, S, w, Np, causal, bs, dh):
+    g = torch.Generator().manual_seed(S + Np + dh)
+    q, k, v = (torch.randn(B, H, S, dh, generator=g).to(dtype) for _ in range(3))
+    scale = 1.0 / np.sqrt(dh)
+    o, lse = _window_attn_fwd(q.to(dev), k.to(dev), v.to(dev), w, Np, causal, BW, bs, scale,
+                              need_lse=True)
+    mask = om.blockwin_mask(S, w, bs, Np, causal)
+    qn, kn, vn = q.float().numpy(), k.float().numpy(), v.float().numpy()
+    ref, ref_lse = oa.masked_attention(qn, kn, vn, mask, scale=scale, return_lse=True)
+    close(o.permute(0, 2, 1, 3).float().cpu(), ref, what="O")
+    close(lse.cpu(), ref_lse, atol=1e-3, rtol=1e-4, what="lse")
+    o2, lse2 = _window_attn_fwd(q.to(dev), k.to(dev), v.to(dev), w, Np, causal, BW, bs, scale,
+                                need_lse=True)
+    assert torch.equal(o, o2) and torch.equal(lse, lse2)
+
+
+def test_blockwin_forward_config3_shape(dev):
+    """BASELINE config 3's shape with the block-window mask (B=8, H=10, S=4096, w=512,
+    Np=16): the persistent rows (all 64 key tiles) in full, sampled other rows."""
+    B, H, S, w, Np, dh = 8, 10, 4096, 512, 16, 64
+    g = torch.Generator().manual_seed(3)
+    q, k, v = (torch.randn(B, H, S, dh, generator=g).to(torch.bfloat16) for _ in range(3))
+    scale = 1.0 / np.sqrt(dh)
+    o, lse = _window_attn_fwd(q.to(dev), k.to(dev), v.to(dev), w, Np, True, BW, 64, scale,
+                              need_lse=True)
+    mask = om.blockwin_mask(S, w, 64, Np, True)
+    rows = np.r_[0:Np, 16:40, 100:130, 600:620, 4070:4096]
+    for b, h in [(0, 0), (3, 7), (7, 9)]:
+        qn = q[b:b + 1, h:h + 1, rows].float().numpy()
+        kn, vn = k[b:b + 1, h:h + 1].float().numpy(), v[b:b + 1, h:h + 1].float().numpy()
+        ref, ref_lse = oa.masked_attention(qn, kn, vn, mask[rows], scale=scale, return_lse=True)
+        close(o.permute(0, 2, 1, 3)[b:b + 1, h:h + 1, rows].float().cpu(), ref, what=f"O {b},{h}")
+        close(lse[b:b + 1, h:h + 1, rows].cpu(), ref_lse, atol=1e-3, rtol=1e-4, what=f"lse {b},{h}")
