@@ -1,12 +1,13 @@
-"""GPU parity of the block-window forward where the persistent rows (n_persistent <= 32,
+"""GPU parity of block-window attention where the persistent rows (n_persistent <= 32,
 all in the first 32-row slice) see every key and two waves share their key tiles (one
-32-key half each, the two softmax states merged at the end): against the fp64 oracle,
-n_persistent on both sides of 32, causal and not, head dimensions 32/64/128, and
-BASELINE config 3's shape.
+32-key half each; the forward merges the two softmax states, the dQ kernel adds the two
+partial sums): against the fp64 oracle, n_persistent on both sides of 32, causal and not,
+head dimensions 32/64/128, and BASELINE config 3's shape.
 
 Bars: bf16/fp16 outputs |got - want| <= 2e-2 + 1e-2 |want| against the fp64 oracle on
 the same 16-bit inputs; the log-sum-exp within 1e-3 + 1e-4 |want| (fp32 output of fp32
-sums); reruns bitwise-identical.
+sums); gradients at the same bar after division by max(1, max |want|) of each tensor
+(as in test_gpu_attention_bwd.py); reruns bitwise-identical.
 """
 import numpy as np
 import pytest
@@ -15,7 +16,7 @@ import torch
 from oracle import attention as oa
 from oracle import masks as om
 from titans_core.kernels import _lib
-from titans_core.kernels.window_attn import _window_attn_fwd
+from titans_core.kernels.window_attn import _window_attn_fwd, windowed_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -72,3 +73,22 @@ def test_blockwin_forward_config3_shape(dev):
         ref, ref_lse = oa.masked_attention(qn, kn, vn, mask[rows], scale=scale, return_lse=True)
         close(o.permute(0, 2, 1, 3)[b:b + 1, h:h + 1, rows].float().cpu(), ref, what=f"O {b},{h}")
         close(lse[b:b + 1, h:h + 1, rows].cpu(), ref_lse, atol=1e-3, rtol=1e-4, what=f"lse {b},{h}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,S,w,Np,causal,bs,dh", CASES)
+def test_blockwin_backward_parity(dev, dtype, B, H, S, w, Np, causal, bs, dh):
+    g = torch.Generator().manual_seed(2 * S + Np + dh)
+    q, k, v, do = (torch.randn(B, H, S, dh, generator=g).to(dtype) for _ in range(4))
+    grads = []
+    for _ in range(2):
+        qd, kd, vd = (t.to(dev).requires_grad_() for t in (q, k, v))
+        windowed_attention(qd, kd, vd, w, Np, causal, "blockwin", bs).backward(do.to(dev))
+        grads.append((qd.grad, kd.grad, vd.grad))
+    mask = om.blockwin_mask(S, w, bs, Np, causal)
+    want = oa.masked_attention_grads(*(t.float().numpy() for t in (q, k, v, do)), mask)
+    for got, ref, name in zip(grads[0], want, "qkv"):
+        sc = max(1.0, float(np.abs(ref).max()))
+        close(got.float().cpu().numpy() / sc, ref / sc, what=f"d{name}")
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
