@@ -135,22 +135,21 @@ void wattn_fwd_mfma_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int l32 = lane & 31, h = lane >> 5;
   const int grp = (lane >> 4) & 1;
-  int q_row = qb * 128 + wave * 32 + l32;  // this lane's query row
-  Span span = mask_row_span(mp, q_row);    // its allowed keys (partial tiles only)
+  const int q_row = qb * 128 + wave * 32 + l32;  // this lane's query row
+  const Span span = mask_row_span(mp, q_row);    // its allowed keys (partial tiles only)
 
   const uint16_t* Kbh = K + b * ksb + hd * ksh;
   const uint16_t* Vbh = V + b * vsb + hd * vsh;
 
   // Q rows as the B operand of Sᵀ = K·Qᵀ: lane holds Q[row][16kk + 8h .. +8].
   u32x4 qf[T::kKk];
-  auto load_q = [&]() __attribute__((always_inline)) {
+  {
     const uint16_t* qp = Q + b * qsb + hd * qsh + static_cast<int64_t>(min(q_row, S - 1)) * qss + 8 * h;
 #pragma unroll
     for (int kk = 0; kk < T::kKk; ++kk) qf[kk] = ldg16(qp + 16 * kk);
 #pragma unroll
     for (int kk = 0; kk < T::kKk; ++kk) settle(qf[kk]);
-  };
-  load_q();
+  }
 
   int e0, e1, mrow = 0;
   if constexpr (CM) {
@@ -218,31 +217,6 @@ void wattn_fwd_mfma_kernel(
   constexpr float kTau = 8.f;
   float m_ref = -INFINITY, l_run = 0.f;
 
-  // Block window with n_persistent <= 32: the persistent rows, all in wave 0's
-  // slice of query block 0, see every key, so that block's list runs over every
-  // key tile while waves 1-3 have work on its first tiles only. After the last
-  // entry where waves 1-3 have work (e_sw: the main loop ends there), waves 0
-  // and 1 share wave 0's slice: wave 0 takes the first 32 keys of each tile,
-  // wave 1 (after writing its own rows and loading wave 0's) the last 32, each
-  // with its own softmax state, and the two states are merged through LDS at the
-  // end (wave 0's first). The block's critical path is then about half as long.
-  // Plain forward only.
-  bool lead = false;
-  int e_sw = e1;
-  if constexpr (FEAT == 0) {
-    if (mp.pattern == TMAC_PATTERN_BLOCKWIN && qb == 0 && mp.Np > 0 && mp.Np <= 32) {
-      int last = e0 - 1;
-      for (int c0 = e0; c0 < e1; c0 += 64) {
-        const int e = c0 + lane;
-        const bool others = e < e1 && ((entries[min(e, e1 - 1)] >> 18) & 0x3f) != 0;
-        const uint64_t bal = __builtin_amdgcn_ballot_w64(others);
-        if (bal) last = c0 + 63 - __builtin_clzll(bal);
-      }
-      e_sw = last + 1;
-      lead = e_sw < e1;
-    }
-  }
-
   if (e0 < e1) {
     gload(entries[e0] & 0xffff);
     if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
@@ -250,7 +224,7 @@ void wattn_fwd_mfma_kernel(
   }
   __syncthreads();
   int buf = 0;
-  for (int e = e0; e < e_sw; ++e) {
+  for (int e = e0; e < e1; ++e) {
     const int ent = entries[e];
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
@@ -359,131 +333,21 @@ void wattn_fwd_mfma_kernel(
     buf ^= 1;
   }
 
-  // O and the log-sum-exp of this lane's row.
-  auto write_rows = [&]() __attribute__((always_inline)) {
-    if (q_row >= S) return;
-    const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
-    uint16_t* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
-    // ot[dt][j] = O[q_row][32dt + 8(j/4) + 4h + j%4]: four consecutive dh per j/4.
+  if (q_row >= S) return;
+  const float inv_l = l_run > 0.f ? 1.f / l_run : 0.f;
+  uint16_t* op = O + b * osb + hd * osh + static_cast<int64_t>(q_row) * oss;
+  // ot[dt][j] = O[q_row][32dt + 8(j/4) + 4h + j%4]: four consecutive dh per j/4.
 #pragma unroll
-    for (int dt = 0; dt < T::kDt; ++dt)
+  for (int dt = 0; dt < T::kDt; ++dt)
 #pragma unroll
-      for (int jg = 0; jg < 4; ++jg) {
-        u32x2 packed;
-        packed.x = Mfma<DT>::pack2(ot[dt][4 * jg] * inv_l, ot[dt][4 * jg + 1] * inv_l);
-        packed.y = Mfma<DT>::pack2(ot[dt][4 * jg + 2] * inv_l, ot[dt][4 * jg + 3] * inv_l);
-        *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * jg + 4 * h) = packed;
-      }
-    if (lse && h == 0)
-      lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
-  };
-
-  if constexpr (FEAT == 0) {
-    if (lead) {
-      if (wave == 1) {
-        // wave 1's own rows are done: write them, then take wave 0's rows
-        write_rows();
-        q_row = qb * 128 + l32;
-        span = mask_row_span(mp, q_row);
-        load_q();
-#pragma unroll
-        for (int dt = 0; dt < T::kDt; ++dt) ot[dt] = f32x16{};
-        m_ref = -INFINITY;
-        l_run = 0.f;
-      }
-      // Half kh (keys 32kh..32kh+31, kh = this wave) of a listed tile against
-      // wave 0's rows: the steps of the loop above for one 32-key half.
-      auto half_step = [&](int kh, int kt, int kind, int bf) __attribute__((always_inline)) {
-        const uint16_t* kt_lds = smem + (2 * bf) * T::kElems;
-        const uint16_t* vt_lds = smem + (2 * bf + 1) * T::kElems;
-        f32x16 st = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < T::kKk; ++kk) {
-          const u32x4 a = lds16(kt_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
-          st = Mfma<DT>::run(a, qf[kk], st);
-        }
-        if (kind == 2) apply_bits(st, span_bits32(span, kt * 64 + 32 * kh + 4 * h));
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, st[j]);
-        mx = xor32_max(mx) * sc;
-        const bool move = mx > m_ref + kTau;
-        if (__builtin_amdgcn_ballot_w64(move)) {
-          const float alpha = move ? __builtin_amdgcn_exp2f(m_ref - mx) : 1.f;
-          const float m_new = move ? mx : m_ref;
-          l_run *= alpha;
-#pragma unroll
-          for (int dt = 0; dt < T::kDt; ++dt) ot[dt] *= alpha;
-          m_ref = m_new;
-        }
-        const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-        u32x4 pb[2];
-        float r4[4];
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-          uint32_t w[4];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(st[8 * kp + 2 * t], sc, -m_use));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(st[8 * kp + 2 * t + 1], sc, -m_use));
-            w[t] = Mfma<DT>::pack2(p0, p1);
-            r4[t] = kp == 0 ? p0 + p1 : r4[t] + (p0 + p1);
-          }
-          pb[kp] = u32x4{w[0], w[1], w[2], w[3]};
-        }
-        l_run += xor32_add((r4[0] + r4[1]) + (r4[2] + r4[3]));
-#pragma unroll
-        for (int kp = 0; kp < 2; ++kp) {
-          const int ks = 2 * kh + kp;
-#pragma unroll
-          for (int dt = 0; dt < T::kDt; ++dt) {
-            const u32x4 va = lds_read_tr4x2<T::kP>(vt_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
-                                                   32 * dt + 16 * grp, lane);
-            ot[dt] = Mfma<DT>::run(va, pb[kp], ot[dt]);
-          }
-        }
-      };
-      // the staging pipeline continues: tile e_sw is in LDS buffer buf
-      for (int e = e_sw; e < e1; ++e) {
-        const int ent = entries[e];
-        const int kt = ent & 0xffff;
-        const int kind = (ent >> 16) & 3;  // wave 0's slice
-        const bool more = e + 1 < e1;
-        if (more) gload(entries[e + 1] & 0xffff);
-        if (kind != 0 && wave < 2) half_step(wave, kt, kind, buf);
-        if (more) sstore(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-      }
-      // wave 1's state for wave 0's rows, merged into wave 0's (the loop's last
-      // barrier freed the LDS): lane-major, element i at cf[i * 64 + lane]
-      float* cf = reinterpret_cast<float*>(smem);
-      constexpr int kN = 16 * T::kDt;
-      if (wave == 1) {
-#pragma unroll
-        for (int dt = 0; dt < T::kDt; ++dt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) cf[(16 * dt + j) * 64 + lane] = ot[dt][j];
-        cf[kN * 64 + lane] = m_ref;
-        cf[(kN + 1) * 64 + lane] = l_run;
-      }
-      __syncthreads();
-      if (wave == 1) return;
-      if (wave == 0) {
-        const float m1 = cf[kN * 64 + lane], l1 = cf[(kN + 1) * 64 + lane];
-        const float M = fmaxf(m_ref, m1);
-        const float a0 = m_ref == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_ref - M);
-        const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - M);
-        l_run = l_run * a0 + l1 * a1;
-#pragma unroll
-        for (int dt = 0; dt < T::kDt; ++dt)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) ot[dt][j] = ot[dt][j] * a0 + cf[(16 * dt + j) * 64 + lane] * a1;
-        m_ref = M;
-      }
+    for (int jg = 0; jg < 4; ++jg) {
+      u32x2 packed;
+      packed.x = Mfma<DT>::pack2(ot[dt][4 * jg] * inv_l, ot[dt][4 * jg + 1] * inv_l);
+      packed.y = Mfma<DT>::pack2(ot[dt][4 * jg + 2] * inv_l, ot[dt][4 * jg + 3] * inv_l);
+      *reinterpret_cast<u32x2*>(op + 32 * dt + 8 * jg + 4 * h) = packed;
     }
-  }
-  write_rows();
+  if (lse && h == 0)
+    lse[(static_cast<int64_t>(b) * H + hd) * S + q_row] = (m_ref + __log2f(l_run)) * kLn2;
 }
 
 // fp32 path on the matrix cores (head dimension 32, 64 or 128): the structure of
