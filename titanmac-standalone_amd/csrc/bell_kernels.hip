@@ -607,6 +607,13 @@ __global__ __launch_bounds__(512 * R, 1) void bell_ggemm_kernel(
     uint16_t* stage = smem + ((gs + 1) & 1) * kX + wave * 2048;
     int n_st = 0;
     if (ob >= 0) {
+      // The staging offsets below depend on the lane only; formed from these
+      // copies (the empty asm hides that they are loop-invariant), they are
+      // computed here per tile instead of being held in registers, or spilled,
+      // across the step loop.
+      int el = lane;
+      asm volatile("" : "+v"(el));
+      const int el32 = el & 31, eh = el >> 5;
       auto stage_store = [&](const f32x16(&v)[2], int mi, uint16_t* out, int64_t ld) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni)
@@ -616,13 +623,13 @@ __global__ __launch_bounds__(512 * R, 1) void bell_ggemm_kernel(
             packed.x = Mfma<DT>::pack2(v[ni][4 * jg], v[ni][4 * jg + 1]);
             packed.y = Mfma<DT>::pack2(v[ni][4 * jg + 2], v[ni][4 * jg + 3]);
             const int chunk = 4 * ni + jg;
-            *reinterpret_cast<u32x2*>(stage + l32 * 64 + ((chunk ^ (l32 & 7)) << 3) + 4 * h) = packed;
+            *reinterpret_cast<u32x2*>(stage + el32 * 64 + ((chunk ^ (el32 & 7)) << 3) + 4 * eh) = packed;
           }
 #pragma unroll
         for (int it = 0; it < 4; ++it) {
           const int base = m_out + 32 * mi + 8 * it;
           if (base < M) {
-            const int row = 8 * it + (lane >> 3), ch = lane & 7;
+            const int row = 8 * it + (el >> 3), ch = el & 7;
             const u32x4 v4 = lds16(stage + row * 64 + ((ch ^ (row & 7)) << 3));
             if (base + (lane >> 3) < M)
               stg16_nt(out + static_cast<int64_t>(base + (lane >> 3)) * ld + col0 + ch * 8, v4);
