@@ -1114,8 +1114,8 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
 // Three workgroups per CU at D ≤ 64 (≤ 168 VGPRs): the caller-mask variants
 // would otherwise take 169–174 and drop to two; with mask and dropout the cap
 // costs four spilled VGPRs and still runs faster.
-template <int DT, int D, int FEAT = 0>
-__global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
+template <int DT, int D, int FEAT = 0, bool RING = false>
+__global__ __launch_bounds__(256, RING ? 4 : (D > 64 ? 1 : 3)) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
     const uint16_t* __restrict__ dO, const uint16_t* __restrict__ O, int64_t osb, int64_t osh,
     int64_t oss, const float* __restrict__ lse, float* __restrict__ delta,
@@ -1126,7 +1126,10 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
     const int32_t* __restrict__ order, WorkMap wm, AttnX ax) {
   constexpr bool CM = (FEAT & kFeatMask) != 0, DR = (FEAT & kFeatDrop) != 0;
   using T = Tile<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * T::kElems];
+  static_assert(!RING || D == 64, "the copy ring stages 64-wide tiles");
+  // [buffer][K, V] 64 x D tiles: padded rows, or with RING unpadded swz64 tiles
+  constexpr int kTileE = RING ? 64 * 64 : T::kElems;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * kTileE];
 
   int bh, qb;
   if (!work_item(wm, order, bh, qb)) return;
@@ -1194,14 +1197,42 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
   }
   const float sc = CM ? 1.f : scale_log2;
 
-  u32x4 pre[2 * T::kPasses];
+  u32x4 pre[RING ? 1 : 2 * T::kPasses];
   const int r0 = tid / T::kCpr, c8 = (tid % T::kCpr) * 8;
   int64_t koff[T::kPasses], voff[T::kPasses];
+  if constexpr (!RING) {
 #pragma unroll
-  for (int p = 0; p < T::kPasses; ++p) {
-    koff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * kss + c8;
-    voff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * vss + c8;
+    for (int p = 0; p < T::kPasses; ++p) {
+      koff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * kss + c8;
+      voff[p] = static_cast<int64_t>(r0 + p * T::kRpp) * vss + c8;
+    }
   }
+  // RING: this wave's 16 rows of the K and V tiles go HBM/L2 -> LDS with
+  // global_load_lds (two 8-row instructions each, chunk positions as for swz64),
+  // rows past S reading row S - 1; four copies per wave and tile.
+  const int drow = lane >> 3, dpos = lane & 7;
+  int crow[2];
+  uint32_t cchunk[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    crow[j] = 16 * wave + 8 * j + drow;
+    const int a = (crow[j] >> 1) & 7;
+    cchunk[j] = 16u * static_cast<uint32_t>(dpos ^ (((a & 1) << 2) | (a >> 1)));
+  }
+  const uint32_t smem0 = lds_offset(smem);
+  auto issue = [&](int kt, int bf) __attribute__((always_inline)) {
+    const int lim = S - 1 - kt * 64;
+    const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
+    const uint16_t* vb = Vbh + static_cast<int64_t>(kt) * 64 * vss;
+    const uint32_t st = smem0 + static_cast<uint32_t>(2 * bf * kTileE * 2);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t r = static_cast<uint32_t>(min(crow[j], lim));
+      dma_lds16(kb, r * static_cast<uint32_t>(2 * kss) + cchunk[j], st + (16 * wave + 8 * j) * 128);
+      dma_lds16(vb, r * static_cast<uint32_t>(2 * vss) + cchunk[j],
+                st + kTileE * 2 + (16 * wave + 8 * j) * 128);
+    }
+  };
   auto gload = [&](int kt) __attribute__((always_inline)) {
     if (kt * 64 + 64 <= S) {
       const uint16_t* kb = Kbh + static_cast<int64_t>(kt) * 64 * kss;
@@ -1224,8 +1255,8 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
 #pragma unroll
     for (int p = 0; p < T::kPasses; ++p) {
       const int off = (r0 + p * T::kRpp) * T::kP + c8;
-      sts16(smem + (2 * buf) * T::kElems + off, pre[p]);
-      sts16(smem + (2 * buf + 1) * T::kElems + off, pre[T::kPasses + p]);
+      sts16(smem + (2 * buf) * kTileE + off, pre[p]);
+      sts16(smem + (2 * buf + 1) * kTileE + off, pre[T::kPasses + p]);
     }
   };
 
@@ -1234,34 +1265,49 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
   for (int dt = 0; dt < T::kDt; ++dt) dqt[dt] = f32x16{};
 
   uint64_t wb = 0, wb_next = 0;  // caller's mask: allowed-key bits of this row, two tiles
-  if (e0 < e1) {
-    gload(entries[e0] & 0xffff);
-    if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
-    sstore(0);
+  if constexpr (RING) {
+    if (e0 < e1) issue(entries[e0] & 0xffff, 0);
+  } else {
+    if (e0 < e1) {
+      gload(entries[e0] & 0xffff);
+      if constexpr (CM) wb = mask_word(ax, mrow, q_row, entries[e0] & 0xffff, S);
+      sstore(0);
+    }
+    __syncthreads();
   }
-  __syncthreads();
+  // K (or V) row r, 16-byte chunk c of a staged tile
+  auto tile_off = [&](int r, int c) __attribute__((always_inline)) {
+    if constexpr (RING) return swz64(r, c);
+    else return r * T::kP + 8 * c;
+  };
   int buf = 0;
   for (int e = e0; e < e1; ++e) {
     const int ent = entries[e];
     const int kt = ent & 0xffff;
     const int kind = (ent >> (16 + 2 * wave)) & 3;
     const bool more = e + 1 < e1;
-    if (more) {
+    if constexpr (RING) {
+      // this wave's copies of tile e have landed; after the barrier every wave's
+      // have, and every wave is done with tile e - 1, whose buffer the next copies fill
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      asm volatile("s_barrier" ::: "memory");
+      if (more) issue(entries[e + 1] & 0xffff, buf ^ 1);
+    } else if (more) {
       gload(entries[e + 1] & 0xffff);
       if constexpr (CM) wb_next = mask_word(ax, mrow, q_row, entries[e + 1] & 0xffff, S);
     }
 
     if (kind != 0) {
-      const uint16_t* k_lds = smem + (2 * buf) * T::kElems;
-      const uint16_t* v_lds = smem + (2 * buf + 1) * T::kElems;
+      const uint16_t* k_lds = smem + (2 * buf) * kTileE;
+      const uint16_t* v_lds = smem + (2 * buf + 1) * kTileE;
       // One 32-key half at a time (s, dp: 32 VGPRs instead of 64).
 #pragma unroll
       for (int kh = 0; kh < 2; ++kh) {
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int kk = 0; kk < T::kKk; ++kk) {
-          const u32x4 ka = lds16(k_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
-          const u32x4 va = lds16(v_lds + (32 * kh + l32) * T::kP + 16 * kk + 8 * h);
+          const u32x4 ka = lds16(k_lds + tile_off(32 * kh + l32, 2 * kk + h));
+          const u32x4 va = lds16(v_lds + tile_off(32 * kh + l32, 2 * kk + h));
           s = Mfma<DT>::run(ka, qf[kk], s);
           dp = Mfma<DT>::run(va, gf[kk], dp);
         }
@@ -1308,16 +1354,23 @@ __global__ __launch_bounds__(256, D > 64 ? 1 : 3) void wattn_bwd_q_kernel(
           const u32x4 db = pack8<DT>(dp, 8 * k2);
 #pragma unroll
           for (int dt = 0; dt < T::kDt; ++dt) {
-            const u32x4 ka = lds_read_tr4x2<T::kP>(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
-                                                   32 * dt + 16 * grp, lane);
+            u32x4 ka;
+            if constexpr (RING)
+              ka = lds_read_tr4x2_swz64(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h, 32 * dt + 16 * grp,
+                                        lane);
+            else
+              ka = lds_read_tr4x2<T::kP>(k_lds, 16 * ks + 4 * h, 16 * ks + 8 + 4 * h,
+                                         32 * dt + 16 * grp, lane);
             dqt[dt] = Mfma<DT>::run(ka, db, dqt[dt]);
           }
         }
       }
     }
-    if (more) sstore(buf ^ 1);
-    if constexpr (CM) wb = wb_next;
-    __syncthreads();
+    if constexpr (!RING) {
+      if (more) sstore(buf ^ 1);
+      if constexpr (CM) wb = wb_next;
+      __syncthreads();
+    }
     buf ^= 1;
   }
 
@@ -2075,11 +2128,22 @@ void launch_bwd_mfma(const AttnLaunch& a) {
   const auto* V = static_cast<const uint16_t*>(a.V);
   const auto* O = static_cast<const uint16_t*>(a.O);
   const auto* G = static_cast<const uint16_t*>(a.dO);
-  hipLaunchKernelGGL((wattn_bwd_q_kernel<DT, D, FEAT>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, V,
-                     G, O, os[0], os[1], os[2], a.lse, a.delta, static_cast<uint16_t*>(a.dQ),
-                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],
-                     gs[2], dqs[0], dqs[1], dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr,
-                     a.entries, a.order, a.wm_q, a.ax_q);
+  // The dQ copy ring addresses 64 rows of K and V with 32-bit byte offsets.
+  bool ring = false;
+  if constexpr (D == 64 && FEAT == 0) ring = ks[2] <= (1ll << 25) && vs[2] <= (1ll << 25);
+#define TMAC_BWD_Q(RG)                                                                              \
+  hipLaunchKernelGGL((wattn_bwd_q_kernel<DT, D, FEAT, RG>), dim3(a.grid_q), dim3(256), 0, a.s, Q, K, \
+                     V, G, O, os[0], os[1], os[2], a.lse, a.delta, static_cast<uint16_t*>(a.dQ),    \
+                     qs[0], qs[1], qs[2], ks[0], ks[1], ks[2], vs[0], vs[1], vs[2], gs[0], gs[1],  \
+                     gs[2], dqs[0], dqs[1], dqs[2], a.H, a.mp, a.scale, a.scale_log2, a.row_ptr,   \
+                     a.entries, a.order, a.wm_q, a.ax_q)
+  if constexpr (D == 64 && FEAT == 0) {
+    if (ring) TMAC_BWD_Q(true);
+    else TMAC_BWD_Q(false);
+  } else {
+    TMAC_BWD_Q(false);
+  }
+#undef TMAC_BWD_Q
   // The copy-ring kernel addresses 64 rows of Q and dO with 32-bit byte offsets.
   if constexpr (D == 64) {
     if (qs[2] <= (1ll << 25) && gs[2] <= (1ll << 25)) {
