@@ -1114,6 +1114,9 @@ __global__ __launch_bounds__(256, 2) void wattn_bwd_kv64_kernel(
 // Three workgroups per CU at D ≤ 64 (≤ 168 VGPRs): the caller-mask variants
 // would otherwise take 169–174 and drop to two; with mask and dropout the cap
 // costs four spilled VGPRs and still runs faster.
+// RING (D = 64, plain): K and V go HBM/L2 -> LDS with global_load_lds into two
+// unpadded swz64 stages, one tile ahead, so no staging registers are needed and
+// four workgroups fit per CU (≤ 128 VGPRs, 32 KB of LDS).
 template <int DT, int D, int FEAT = 0, bool RING = false>
 __global__ __launch_bounds__(256, RING ? 4 : (D > 64 ? 1 : 3)) void wattn_bwd_q_kernel(
     const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K, const uint16_t* __restrict__ V,
