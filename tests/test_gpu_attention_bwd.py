@@ -99,6 +99,29 @@ def test_backward_custom_scale(dev):
         close(got.float().cpu(), ref)
 
 
+def test_backward_register_staged_dq_at_head_dim_64(dev):
+    """A key-row stride above 2^25 elements sends the head-dim-64 dQ work to the
+    register-staged kernel (the copy-ring one addresses 64 key rows with 32-bit
+    offsets); the copy-ring case is every other head-dim-64 test here. Same oracle and
+    bar."""
+    B, H, S, w, Np = 1, 1, 70, 32, 3
+    q, k, v, do = tensors((B, H, S, 64), torch.bfloat16, seed=41)
+    pitch = (1 << 25) + 64
+    buf = torch.zeros((S - 1) * pitch + 64, dtype=torch.bfloat16, device=dev)
+    kd = buf.as_strided((B, H, S, 64), (S * pitch, S * pitch, pitch, 1))
+    kd.copy_(k.to(dev))
+    assert kd.stride(2) > (1 << 25)
+    kd.requires_grad_()
+    qd, vd = (t.to(dev).requires_grad_() for t in (q, v))
+    o = windowed_attention(qd, kd, vd, w, Np, True, "band", 64)
+    o.backward(do.to(dev))
+    want = oa.masked_attention_grads(*(t.float().numpy() for t in (q, k, v, do)),
+                                     om.band_mask(S, w, Np))
+    for got, ref, name in zip((qd.grad, kd.grad, vd.grad), want, "qkv"):
+        close(got.float().cpu(), ref, what=f"d{name}")
+    del buf
+
+
 def test_backward_deterministic(dev):
     q, k, v, do = tensors((2, 2, 700, 64), torch.bfloat16, seed=13)
     first = run_bwd(dev, q, k, v, do, 256, 16, True, "band", 64)[1:]
