@@ -1,8 +1,8 @@
-"""GPU parity of block-window attention where the persistent rows (n_persistent <= 32,
-all in the first 32-row slice) see every key and two waves share their key tiles (one
-32-key half each; the forward merges the two softmax states, the dQ kernel adds the two
-partial sums): against the fp64 oracle, n_persistent on both sides of 32, causal and not,
-head dimensions 32/64/128, and BASELINE config 3's shape.
+"""GPU parity of block-window attention (BlockSparseAttention's mask,
+attn/block_sparse_attention.py:277-334), whose persistent rows see every key so that the
+first query block of a head walks every key tile: forward and backward against the fp64
+oracle, n_persistent from 1 to 200 (persistent rows filling whole query blocks), causal and
+not, head dimensions 32/64/128, and BASELINE config 3's shape.
 
 Bars: bf16/fp16 outputs |got - want| <= 2e-2 + 1e-2 |want| against the fp64 oracle on
 the same 16-bit inputs; the log-sum-exp within 1e-3 + 1e-4 |want| (fp32 output of fp32
@@ -35,7 +35,8 @@ def close(got, want, atol=2e-2, rtol=1e-2, what=""):
 CASES = [(1, 2, 333, 128, 16, True, 64, 64), (1, 1, 700, 100, 32, True, 64, 64),
          (1, 1, 700, 100, 33, True, 64, 64), (2, 1, 520, 64, 1, False, 32, 32),
          (1, 2, 1000, 512, 16, True, 64, 128), (1, 1, 40, 8, 16, True, 64, 64),
-         (1, 1, 129, 0, 8, True, 64, 64), (1, 1, 300, 200, 20, False, 64, 64)]
+         (1, 1, 129, 0, 8, True, 64, 64), (1, 1, 300, 200, 20, False, 64, 64),
+         (1, 1, 700, 100, 200, True, 64, 64), (2, 1, 520, 64, 129, False, 32, 32)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
